@@ -1,0 +1,157 @@
+/*
+ * muon_sr_amd.h -- C ABI of libmuon_sr_amd.so, the MI355X (gfx950) kernels of
+ * the muon_sr optimizer-step hot path.
+ *
+ * Conventions (every entry point):
+ *  - All pointers are device pointers unless documented as host arrays; the
+ *    library never allocates or frees device memory (workspace comes from the
+ *    caller, sized by the matching *_workspace_bytes query).
+ *  - bf16 tensors are passed as uint16_t bit patterns, contiguous.
+ *  - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the
+ *    default stream).  Nothing synchronises.
+ *  - Return 0 on success, else a hipError_t or one of the MSR_ERR_* codes
+ *    below; msr_last_error() returns a message for the calling thread.
+ *  - fp32 scalars are the reference's Python floats rounded to fp32, as a
+ *    compiled Triton launch passes them.  Seeds are the reference's 32-bit
+ *    seeds; the library derives each stream's Philox key (SEED + k typing).
+ *  - noise_mode selects the stochastic-rounding noise source:
+ *      MSR_NOISE_TRITON  word 0 of Philox4x32-10 at counter (offset, 0, 0, 0):
+ *                        the same bits the reference's tl.randint produces;
+ *      MSR_NOISE_PHILOX8 one Philox4x32-10 call per 8 consecutive offsets
+ *                        (16 bits each): this library's fast stream;
+ *      MSR_NOISE_INJECT  noise read from `inject` (uint16 [streams][n]); tests.
+ *  - Entry points keep no global mutable state and are safe to call from
+ *    several host threads (autograd hooks run on the engine thread).
+ */
+#ifndef MUON_SR_AMD_H
+#define MUON_SR_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *msr_stream_t; /* == hipStream_t */
+
+#define MSR_NOISE_TRITON 0
+#define MSR_NOISE_PHILOX8 1
+#define MSR_NOISE_INJECT 2
+
+#define MSR_ERR_ARG 1001
+#define MSR_ERR_ALIGN 1002
+#define MSR_ERR_LAUNCH 1003
+#define MSR_ERR_WORKSPACE 1004
+
+/* Library version (major*10000 + minor*100 + patch) and error text. */
+int msr_version(void);
+const char *msr_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * (c) SR gradient accumulation.
+ * Replaces the _grad_accum_kernel launches of TritonSRAccumulator._accum_hook
+ * (muon_sr/triton_adamw.py:206-229, launched at :260 and :264).
+ *   acc[i] <- SR_bf16(f32(acc[i]) + f32(grad[i])),  noise offset i.
+ * grad_is_f32: 0 = bf16 grad, 1 = fp32 grad.
+ * zero_init != 0 treats acc as zero on input (fuses the zeros_like at :263);
+ * acc is then write-only.  inject: uint16 [n].
+ * ------------------------------------------------------------------------- */
+int msr_sr_accum(uint16_t *acc, const void *grad, int32_t grad_is_f32, int64_t n, uint32_t seed,
+                 int32_t zero_init, int32_t noise_mode, const uint16_t *inject, msr_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * BF16-moment AdamW step (PyTorch order: decay before the update).
+ * Replaces _adamw_kernel / _adamw_step (muon_sr/triton_adamw.py:9-114).
+ * Streams: ema uses SEED, ema_sq SEED+1, p SEED+2 (inject: uint16 [3][n]).
+ * ------------------------------------------------------------------------- */
+int msr_adamw_bf16_step(uint16_t *p, const uint16_t *g, uint16_t *ema, uint16_t *ema_sq, int64_t n,
+                        float lr, float beta1, float beta2, float eps, float weight_decay,
+                        float bias_correction, float bias_correction_sqrt, uint32_t seed,
+                        int32_t noise_mode, const uint16_t *inject, msr_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (a) 8-bit blockwise AdamW step (bitsandbytes order: decay after the update).
+ * Replaces the _adamw_8bit_kernel launch of TritonAdamW8bit.step
+ * (muon_sr/triton_adamw_8bit.py:56-99, launched at :198-204).
+ * quantized != 0: state1/state2 are uint8 codes [n], absmax1/absmax2 fp32
+ *   [ceil(n/block)], qmap1 (signed) / qmap2 (unsigned) fp32 [256].
+ * quantized == 0: state1/state2 are bf16 moments [n]; absmax/qmap unused.
+ * block: power of two in [32, 4096].  bc1 = 1-b1^step, bc2 = 1-b2^step.
+ * Streams: p uses SEED, bf16 m SEED+1, bf16 v SEED+2 (inject: uint16 [3][n]).
+ * ------------------------------------------------------------------------- */
+int msr_adamw8bit_step(uint16_t *p, const uint16_t *g, void *state1, void *state2,
+                       float *absmax1, float *absmax2, const float *qmap1, const float *qmap2,
+                       int64_t n, int32_t block, int32_t quantized,
+                       float lr, float beta1, float beta2, float eps, float weight_decay,
+                       float bc1, float bc2, uint32_t seed,
+                       int32_t noise_mode, const uint16_t *inject, msr_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (b) Muon momentum prologue over one shape group.
+ * Replaces the grad->stack copy and the _muon_prepare_kernel launch of
+ * _triton_muon_batch_step (muon_sr/triton_muon_sr.py:150-159) and, with
+ * count == 1, _run_prepare (:88-98).
+ *   grads: HOST array of `count` device pointers, each to numel_each bf16.
+ *   buf:   bf16 momentum stack [count][numel_each], updated in place (SR).
+ *   out:   bf16 pre-NS update [count][numel_each] (RNE).
+ * Noise offset of element j of matrix i: i*numel_each + j (stack offset).
+ * inject: uint16 [count*numel_each].
+ * ------------------------------------------------------------------------- */
+int msr_muon_prepare(const uint16_t *const *grads, uint16_t *buf, uint16_t *out,
+                     int64_t numel_each, int32_t count, float beta, int32_t nesterov,
+                     uint32_t seed, int32_t noise_mode, const uint16_t *inject, msr_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (b) Muon parameter update over several matrices of one shape.
+ * Replaces the per-parameter _muon_apply_kernel launches of
+ * _triton_muon_batch_step and _run_apply (muon_sr/triton_muon_sr.py:53-80,
+ * 105-113, 167-169).
+ *   params: HOST array of `count` device pointers, each to numel_each bf16.
+ *   upd:    bf16 Newton-Schulz output [count][numel_each] (parameter layout).
+ *   seeds:  HOST array of `count` seeds (salt-1 deterministic seeds).
+ *   p <- SR(p*(1-lr*wd) - lr*(f32(upd)*scale)), noise offset j within p.
+ * inject: uint16 [count][numel_each].
+ * ------------------------------------------------------------------------- */
+int msr_muon_apply(uint16_t *const *params, const uint16_t *upd, int64_t numel_each, int32_t count,
+                   float lr, float weight_decay, float scale, const uint32_t *seeds,
+                   int32_t noise_mode, const uint16_t *inject, msr_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (b) Batched Newton-Schulz orthogonalisation on bf16 MFMA.
+ * Replaces _newton_schulz(G, steps, out_dtype=None) (muon_sr/muon_sr.py:82-98)
+ * for a contiguous bf16 stack G [batch][rows][cols]; out has the same shape.
+ * The iteration runs on the wide orientation (transposed when rows > cols):
+ *   X = G/(||G||_F + 1e-7);  repeat: A = X X^T; B = b A + c A A; X = a X + B X.
+ * Products accumulate in fp32; A, B and X are stored in bf16 between GEMMs.
+ * Results do not depend on `batch` (each matrix is computed independently).
+ * ------------------------------------------------------------------------- */
+int msr_ns_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, size_t *bytes);
+int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows, int64_t cols,
+                      int32_t steps, float a, float b, float c, void *workspace, size_t workspace_bytes,
+                      msr_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Diagnostics (no counterpart in the reference; used by the parity tests).
+ * ------------------------------------------------------------------------- */
+
+/* out[i] = 16-bit noise of stream (seed, k) at offset offset0 + i. */
+int msr_noise_fill(uint16_t *out, int64_t n, int64_t offset0, uint32_t seed, uint32_t k,
+                   int32_t noise_mode, msr_stream_t stream);
+
+/* out[i] = quantizer code of x[i] against qmap (reference search rule). */
+int msr_quantize(const float *x, uint8_t *out, int64_t n, const float *qmap, int32_t is_signed,
+                 msr_stream_t stream);
+
+/* Batched bf16 GEMM  D[b] = alpha * P[b] Q[b]^T + beta * C[b]  (fp32 accumulate, RNE bf16 out).
+ * P: [M][K] (row stride ldp), Q: [N][K] (ldq), C/D: [M][N] (ldc/ldd); C may be NULL when beta == 0.
+ * M, N multiples of 256 and K a multiple of 64 (the NS workspace is padded to these). */
+int msr_gemm_nt(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q, int64_t ldq,
+                int64_t strideQ, const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D, int64_t ldd,
+                int64_t strideD, int64_t M, int64_t N, int64_t K, int64_t batch, float alpha, float beta,
+                msr_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MUON_SR_AMD_H */

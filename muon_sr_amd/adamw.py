@@ -1,0 +1,158 @@
+"""BF16-moment AdamW with stochastic rounding, and SR gradient accumulation.
+
+Drop-in for ``muon_sr.triton_adamw`` (bab2min/muon_sr 0.1.2): same class names,
+constructor signatures, param-group keys, state keys and seeds; the Triton
+kernels are replaced by the gfx950 kernels of libmuon_sr_amd.so.
+"""
+from __future__ import annotations
+
+import random
+
+import torch
+from torch.optim import Optimizer
+
+from . import _lib
+
+
+def _seed(step: int, param_idx: int) -> int:
+    """Per-(step, tensor) seed, muon_sr/triton_adamw.py:95-97."""
+    return (step * 2654435761 ^ param_idx * 1234567891) & 0xFFFFFFFF
+
+
+def _adamw_step(p: torch.Tensor, g: torch.Tensor, ema: torch.Tensor, ema_sq: torch.Tensor,
+                lr: float, beta1: float, beta2: float, eps: float, weight_decay: float,
+                step: int, param_idx: int) -> None:
+    """One fused AdamW step on one tensor (muon_sr/triton_adamw.py:75-114).
+
+    Bias corrections are Python doubles, passed to the kernel as fp32 (as a
+    compiled Triton launch passes Python floats).
+    """
+    bias_correction = 1.0 - beta1 ** step
+    bias_correction_sqrt = (1.0 - beta2 ** step) ** 0.5
+    _lib.require_gpu(p, "TritonAdamW", RuntimeError)
+    if not p.is_contiguous():
+        raise RuntimeError("TritonAdamW requires contiguous parameters")
+    g = g.contiguous()
+    L = _lib.lib()
+    rc = L.msr_adamw_bf16_step(p.data_ptr(), g.data_ptr(), ema.data_ptr(), ema_sq.data_ptr(), p.numel(),
+                               lr, beta1, beta2, eps, weight_decay, bias_correction, bias_correction_sqrt,
+                               _seed(step, param_idx), _lib.noise_mode(), None, _lib.stream_of(p))
+    _lib.check(rc, "msr_adamw_bf16_step")
+
+
+class TritonAdamW(Optimizer):
+    r"""
+    AdamW with stochastic rounding, one fused gfx950 kernel per tensor.
+
+    Arguments:
+        params: parameters to optimize
+        lr (float): learning rate (default: 1e-3)
+        betas (Tuple[float, float]): EMA coefficients (default: (0.9, 0.999))
+        eps (float): denominator epsilon (default: 1e-8)
+        weight_decay (float): decoupled weight decay (default: 0)
+        centralization (float): gradient centralization strength (default: 0)
+
+    Mirrors muon_sr/triton_adamw.py:117-203.
+    """
+
+    def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0, centralization=0):
+        defaults = dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, centralization=centralization)
+        super().__init__(params, defaults)
+
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            loss = closure()
+
+        param_offset = 0
+        for group in self.param_groups:
+            group_offset = param_offset
+            param_offset += len(group["params"])
+            beta1, beta2 = group["betas"]
+            lr = group["lr"]
+            eps = group["eps"]
+            weight_decay = group["weight_decay"]
+            centralization = group["centralization"]
+
+            for i, p in enumerate(group["params"]):
+                assert p.dtype == torch.bfloat16, "only bfloat16 is supported."
+                if p.grad is None:
+                    continue
+                grad = p.grad
+                if grad.is_sparse:
+                    raise RuntimeError("TritonAdamW does not support sparse gradients")
+
+                state = self.state[p]
+                if len(state) == 0:
+                    state["step"] = 0
+                    state["ema"] = torch.zeros_like(p.data, dtype=torch.bfloat16)
+                    state["ema_squared"] = torch.zeros_like(p.data, dtype=torch.bfloat16)
+
+                state["step"] += 1
+
+                # gradient centralization: mean over all but the first dim, in fp32
+                # (muon_sr/triton_adamw.py:179-187), on the device
+                if centralization != 0:
+                    grad = grad.to(torch.float32)
+                    grad.sub_(grad.mean(dim=tuple(range(1, grad.dim())), keepdim=True).mul_(centralization))
+                    grad = grad.to(torch.bfloat16)
+
+                with torch.no_grad():
+                    _adamw_step(p=p.data, g=grad, ema=state["ema"], ema_sq=state["ema_squared"],
+                                lr=lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay,
+                                step=state["step"], param_idx=group_offset + i)
+
+        return loss
+
+
+class TritonSRAccumulator:
+    """
+    Stochastic-rounding gradient accumulation into a BF16 buffer ``p.acc_grad``.
+
+    Mirrors muon_sr/triton_adamw.py:232-280.  One fused kernel per parameter per
+    micro-batch: acc <- SR_bf16(f32(acc) + f32(grad)); on the first micro-batch
+    the zero buffer is folded into the kernel (acc = SR(0 + grad)).
+
+        TritonSRAccumulator.assign_hooks(model)
+
+        for step in range(total_steps):
+            for _ in range(grad_accum):
+                loss = model(x)
+                loss.backward()
+            TritonSRAccumulator.reassign_grad_buffer(model)
+            optimizer.step()
+            optimizer.zero_grad()
+    """
+
+    @staticmethod
+    def _accum_hook(p):
+        grad = p.grad
+        n = grad.numel()
+        seed = random.getrandbits(32)
+        if grad.dtype not in (torch.bfloat16, torch.float32):
+            raise RuntimeError(f"TritonSRAccumulator supports bf16 or fp32 gradients, got {grad.dtype}")
+        _lib.require_gpu(grad, "TritonSRAccumulator", RuntimeError)
+        grad = grad.contiguous()
+        first = not hasattr(p, "acc_grad")
+        if first:
+            p.acc_grad = torch.empty_like(p.data, dtype=torch.bfloat16, memory_format=torch.contiguous_format)
+        acc = p.acc_grad
+        rc = _lib.lib().msr_sr_accum(acc.data_ptr(), grad.data_ptr(), int(grad.dtype == torch.float32), n, seed,
+                                     int(first), _lib.noise_mode(), None, _lib.stream_of(acc))
+        _lib.check(rc, "msr_sr_accum")
+        del p.grad
+
+    @staticmethod
+    def reassign_grad_buffer(model):
+        for _, p in model.named_parameters():
+            if p.requires_grad and hasattr(p, "acc_grad"):
+                p.grad = p.acc_grad
+                del p.acc_grad
+
+    @staticmethod
+    def assign_hooks(model):
+        hooks = []
+        for _, p in model.named_parameters():
+            if p.requires_grad:
+                hooks.append(p.register_post_accumulate_grad_hook(TritonSRAccumulator._accum_hook))
+        return hooks

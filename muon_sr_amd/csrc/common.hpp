@@ -1,0 +1,190 @@
+// Shared device helpers for the muon_sr_amd HIP kernels (gfx950 / CDNA4).
+//
+// bf16 values are handled as raw 16-bit patterns; fp32 arithmetic is IEEE
+// binary32 with one rounding per operation (the library is compiled with
+// -ffp-contract=off and the default correctly rounded division and sqrt).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/muon_sr_amd.h"
+
+namespace msr {
+
+// ---------------------------------------------------------------------------
+// Status plumbing
+// ---------------------------------------------------------------------------
+
+// Error codes are the MSR_ERR_* macros of the public header.
+constexpr int MSR_OK = 0;
+
+void set_error(const char *fmt, ...);
+int check_launch(const char *what);
+
+// ---------------------------------------------------------------------------
+// bf16 helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h16) { return __uint_as_float(h16 << 16); }
+
+// low half of a packed pair / high half of a packed pair
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Stochastic rounding: add 16 noise bits to the fp32 pattern (wrapping) and keep the high half.
+__device__ __forceinline__ uint32_t sr_bf16(float x, uint32_t noise16) {
+    return (__float_as_uint(x) + noise16) >> 16;
+}
+
+// Round-to-nearest-even fp32 -> bf16 (quiet NaN for NaN inputs).
+__device__ __forceinline__ uint32_t rne_bf16(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack2(uint32_t lo16, uint32_t hi16) { return (lo16 & 0xffffu) | (hi16 << 16); }
+
+// ---------------------------------------------------------------------------
+// Philox4x32-10 (Salmon et al., SC'11), the generator Triton's tl.randint uses.
+// ---------------------------------------------------------------------------
+
+constexpr uint32_t PHILOX_KA = 0x9E3779B9u, PHILOX_KB = 0xBB67AE85u;
+constexpr uint32_t PHILOX_RA = 0xD2511F53u, PHILOX_RB = 0xCD9E8D57u;
+
+__device__ __forceinline__ void philox10(uint32_t &c0, uint32_t &c1, uint32_t &c2, uint32_t &c3,
+                                         uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        uint64_t pa = (uint64_t)PHILOX_RA * c0;
+        uint64_t pb = (uint64_t)PHILOX_RB * c2;
+        uint32_t n0 = (uint32_t)(pb >> 32) ^ c1 ^ k0;
+        uint32_t n2 = (uint32_t)(pa >> 32) ^ c3 ^ k1;
+        c1 = (uint32_t)pb;
+        c3 = (uint32_t)pa;
+        c0 = n0;
+        c2 = n2;
+        k0 += PHILOX_KA;
+        k1 += PHILOX_KB;
+    }
+}
+
+// Word 0 of Philox(ctr = (c0, 0, 0, 0), key).  With c1 = c2 = c3 = 0 the first
+// round reduces to c0' = k0, c2' = hi(RA*c0) ^ k1, c1' = 0, c3' = lo(RA*c0).
+__device__ __forceinline__ uint32_t philox_w0(uint32_t ctr, uint32_t k0, uint32_t k1) {
+    uint64_t pa = (uint64_t)PHILOX_RA * ctr;
+    uint32_t c0 = k0, c1 = 0u, c2 = (uint32_t)(pa >> 32) ^ k1, c3 = (uint32_t)pa;
+    k0 += PHILOX_KA;
+    k1 += PHILOX_KB;
+#pragma unroll
+    for (int r = 1; r < 9; ++r) {
+        uint64_t qa = (uint64_t)PHILOX_RA * c0;
+        uint64_t qb = (uint64_t)PHILOX_RB * c2;
+        uint32_t n0 = (uint32_t)(qb >> 32) ^ c1 ^ k0;
+        uint32_t n2 = (uint32_t)(qa >> 32) ^ c3 ^ k1;
+        c1 = (uint32_t)qb;
+        c3 = (uint32_t)qa;
+        c0 = n0;
+        c2 = n2;
+        k0 += PHILOX_KA;
+        k1 += PHILOX_KB;
+    }
+    // last round: only word 0 is needed
+    return (uint32_t)(((uint64_t)PHILOX_RB * c2) >> 32) ^ c1 ^ k0;
+}
+
+// Philox key of Triton's `SEED + k` stream.  A compiled Triton launch types an
+// int argument i32 in [-2^31, 2^31) and i64 in [2^31, 2^63); SEED + k is
+// evaluated in that type, then widened to u64 (sign-extended for i32) and split
+// into (lo, hi) (triton/language/random.py:49-60).
+struct PhiloxKey {
+    uint32_t lo, hi;
+};
+
+__host__ __device__ inline PhiloxKey seed_key(uint32_t seed, uint32_t k) {
+    PhiloxKey key;
+    if (seed < 0x80000000u) {
+        key.lo = seed + k;
+        key.hi = (key.lo >= 0x80000000u) ? 0xffffffffu : 0u;
+    } else {
+        uint64_t v = (uint64_t)seed + k;
+        key.lo = (uint32_t)v;
+        key.hi = (uint32_t)(v >> 32);
+    }
+    return key;
+}
+
+// ---------------------------------------------------------------------------
+// Noise sources for one stochastic-rounding stream
+// ---------------------------------------------------------------------------
+
+enum NoiseMode : int {
+    NOISE_TRITON = 0,   // word 0 of Philox((offset mod 2^32, 0, 0, 0), key): the reference's noise
+    NOISE_PHILOX8 = 1,  // one Philox call per 8 consecutive offsets, 16-bit lane (offset & 7)
+    NOISE_INJECT = 2    // caller-provided uint16 noise, indexed by offset (tests)
+};
+
+struct Noise {
+    PhiloxKey key;
+    const uint16_t *inject;
+};
+
+// 16 noise bits for each of the 8 offsets o0 .. o0+7 (o0 a multiple of 8 when
+// MODE == NOISE_PHILOX8).  `valid` counts the offsets that exist (<= 8).
+template <int MODE>
+__device__ __forceinline__ void noise8(const Noise &ns, int64_t o0, int valid, uint32_t out[8]) {
+    if constexpr (MODE == NOISE_TRITON) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) out[j] = philox_w0((uint32_t)(o0 + j), ns.key.lo, ns.key.hi) & 0xffffu;
+    } else if constexpr (MODE == NOISE_PHILOX8) {
+        uint64_t o = (uint64_t)o0;
+        uint32_t c0 = (uint32_t)(o >> 3), c1 = (uint32_t)(o >> 35), c2 = 0u, c3 = 0u;
+        philox10(c0, c1, c2, c3, ns.key.lo, ns.key.hi);
+        out[0] = c0 & 0xffffu; out[1] = c0 >> 16;
+        out[2] = c1 & 0xffffu; out[3] = c1 >> 16;
+        out[4] = c2 & 0xffffu; out[5] = c2 >> 16;
+        out[6] = c3 & 0xffffu; out[7] = c3 >> 16;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) out[j] = (j < valid) ? (uint32_t)ns.inject[o0 + j] : 0u;
+    }
+}
+
+// Noise for a single offset (scalar fallback paths).
+template <int MODE>
+__device__ __forceinline__ uint32_t noise1(const Noise &ns, int64_t o) {
+    if constexpr (MODE == NOISE_TRITON) {
+        return philox_w0((uint32_t)o, ns.key.lo, ns.key.hi) & 0xffffu;
+    } else if constexpr (MODE == NOISE_PHILOX8) {
+        uint64_t u = (uint64_t)o;
+        uint32_t c0 = (uint32_t)(u >> 3), c1 = (uint32_t)(u >> 35), c2 = 0u, c3 = 0u;
+        philox10(c0, c1, c2, c3, ns.key.lo, ns.key.hi);
+        uint32_t lane = (uint32_t)(u & 7u);
+        uint32_t w = (lane < 2) ? c0 : (lane < 4) ? c1 : (lane < 6) ? c2 : c3;
+        return (w >> (16u * (lane & 1u))) & 0xffffu;
+    } else {
+        return ns.inject[o];
+    }
+}
+
+inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// Grid size for a grid-stride loop over `work` items with `threads` per block.
+inline unsigned grid_for(int64_t work, int threads, int64_t cap = 256 * 32) {
+    int64_t b = (work + threads - 1) / threads;
+    if (b < 1) b = 1;
+    if (b > cap) b = cap;
+    return (unsigned)b;
+}
+
+}  // namespace msr
+
+// Noise-mode dispatch for a templated launcher.
+#define MSR_DISPATCH_NOISE(mode, M, ...)                                        \
+    switch (mode) {                                                             \
+    case msr::NOISE_TRITON: { constexpr int M = msr::NOISE_TRITON; __VA_ARGS__; break; } \
+    case msr::NOISE_PHILOX8: { constexpr int M = msr::NOISE_PHILOX8; __VA_ARGS__; break; } \
+    case msr::NOISE_INJECT: { constexpr int M = msr::NOISE_INJECT; __VA_ARGS__; break; } \
+    default: msr::set_error("unknown noise mode %d", (int)(mode)); return MSR_ERR_ARG; \
+    }

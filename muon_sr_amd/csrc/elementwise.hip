@@ -1,0 +1,772 @@
+// Memory-bound optimizer kernels for gfx950: SR gradient accumulation, bf16-
+// moment AdamW, 8-bit blockwise AdamW and the Muon momentum/update passes.
+//
+// Each thread owns 8 consecutive elements (one 16-byte bf16 vector), so a
+// wave64 streams 1 KiB of every bf16 operand per access.  The quantized AdamW
+// kernel assigns block/8 consecutive threads to one quantization block and
+// reduces the block absmax with cross-lane shuffles (LDS across waves for
+// blocks above 512 elements).
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "common.hpp"
+#include "../../include/muon_sr_amd.h"
+
+namespace msr {
+
+static thread_local char g_err[512];
+
+void set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+int check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e));
+        return (int)e;
+    }
+    return MSR_OK;
+}
+
+constexpr int THREADS = 256;
+
+// ---------------------------------------------------------------------------
+// 8-element vector I/O (aligned fast path, masked scalar path at tails or for
+// unaligned views)
+// ---------------------------------------------------------------------------
+
+template <bool VEC>
+__device__ __forceinline__ void load_bf16x8(const uint16_t *base, int64_t o0, int valid, uint32_t w[4]) {
+    if (VEC && valid == 8) {
+        uint4 v = *reinterpret_cast<const uint4 *>(base + o0);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t lo = (2 * j < valid) ? base[o0 + 2 * j] : 0u;
+            uint32_t hi = (2 * j + 1 < valid) ? base[o0 + 2 * j + 1] : 0u;
+            w[j] = lo | (hi << 16);
+        }
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store_bf16x8(uint16_t *base, int64_t o0, int valid, const uint32_t w[4]) {
+    if (VEC && valid == 8) {
+        *reinterpret_cast<uint4 *>(base + o0) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (2 * j < valid) base[o0 + 2 * j] = (uint16_t)(w[j] & 0xffffu);
+            if (2 * j + 1 < valid) base[o0 + 2 * j + 1] = (uint16_t)(w[j] >> 16);
+        }
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void load_f32x8(const float *base, int64_t o0, int valid, float f[8]) {
+    if (VEC && valid == 8) {
+        float4 a = *reinterpret_cast<const float4 *>(base + o0);
+        float4 b = *reinterpret_cast<const float4 *>(base + o0 + 4);
+        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+        f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = (j < valid) ? base[o0 + j] : 0.0f;
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void load_u8x8(const uint8_t *base, int64_t o0, int valid, uint32_t fill,
+                                          uint32_t c[8]) {
+    if (VEC && valid == 8) {
+        uint2 v = *reinterpret_cast<const uint2 *>(base + o0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            c[j] = (v.x >> (8 * j)) & 0xffu;
+            c[j + 4] = (v.y >> (8 * j)) & 0xffu;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = (j < valid) ? (uint32_t)base[o0 + j] : fill;
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store_u8x8(uint8_t *base, int64_t o0, int valid, const uint32_t c[8]) {
+    if (VEC && valid == 8) {
+        uint32_t x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+        uint32_t y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+        *reinterpret_cast<uint2 *>(base + o0) = make_uint2(x, y);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (j < valid) base[o0 + j] = (uint8_t)c[j];
+    }
+}
+
+__device__ __forceinline__ void unpack8(const uint32_t w[4], float f[8]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[2 * j] = bf16_lo(w[j]);
+        f[2 * j + 1] = bf16_hi(w[j]);
+    }
+}
+
+__device__ __forceinline__ int clamp_valid(int64_t n, int64_t o0) {
+    int64_t r = n - o0;
+    return r <= 0 ? 0 : (r >= 8 ? 8 : (int)r);
+}
+
+// ---------------------------------------------------------------------------
+// (c) SR gradient accumulation   (muon_sr/triton_adamw.py:206-229)
+// ---------------------------------------------------------------------------
+
+template <int MODE, bool GF32, bool ZERO, bool VEC>
+__global__ __launch_bounds__(THREADS) void sr_accum_kernel(uint16_t *__restrict__ acc, const void *__restrict__ grad,
+                                                          int64_t n, Noise ns) {
+    const int64_t groups = (n + 7) >> 3;
+    for (int64_t t = (int64_t)blockIdx.x * THREADS + threadIdx.x; t < groups; t += (int64_t)gridDim.x * THREADS) {
+        const int64_t o0 = t << 3;
+        const int valid = clamp_valid(n, o0);
+        float a[8], g[8];
+        if constexpr (ZERO) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a[j] = 0.0f;
+        } else {
+            uint32_t w[4];
+            load_bf16x8<VEC>(acc, o0, valid, w);
+            unpack8(w, a);
+        }
+        if constexpr (GF32) {
+            load_f32x8<VEC>(static_cast<const float *>(grad), o0, valid, g);
+        } else {
+            uint32_t w[4];
+            load_bf16x8<VEC>(static_cast<const uint16_t *>(grad), o0, valid, w);
+            unpack8(w, g);
+        }
+        uint32_t r[8];
+        noise8<MODE>(ns, o0, valid, r);
+        uint32_t out[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            out[j] = pack2(sr_bf16(a[2 * j] + g[2 * j], r[2 * j]), sr_bf16(a[2 * j + 1] + g[2 * j + 1], r[2 * j + 1]));
+        store_bf16x8<VEC>(acc, o0, valid, out);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// BF16-moment AdamW   (muon_sr/triton_adamw.py:9-72)
+// ---------------------------------------------------------------------------
+
+struct AdamWArgs {
+    uint16_t *p;
+    const uint16_t *g;
+    uint16_t *ema;
+    uint16_t *ema_sq;
+    int64_t n;
+    float lr, beta1, beta2, eps, wd, bc, bcs;
+    Noise ns_ema, ns_ema_sq, ns_p;
+};
+
+template <int MODE, bool VEC>
+__global__ __launch_bounds__(THREADS) void adamw_bf16_kernel(AdamWArgs a) {
+    const float one_m_b1 = 1.0f - a.beta1;
+    const float one_m_b2 = 1.0f - a.beta2;
+    const float step_size = a.lr / a.bc;
+    const float decay = 1.0f - a.lr * a.wd;
+    const int64_t groups = (a.n + 7) >> 3;
+    for (int64_t t = (int64_t)blockIdx.x * THREADS + threadIdx.x; t < groups; t += (int64_t)gridDim.x * THREADS) {
+        const int64_t o0 = t << 3;
+        const int valid = clamp_valid(a.n, o0);
+        uint32_t wp[4], wg[4], we[4], ws[4];
+        load_bf16x8<VEC>(a.p, o0, valid, wp);
+        load_bf16x8<VEC>(a.g, o0, valid, wg);
+        load_bf16x8<VEC>(a.ema, o0, valid, we);
+        load_bf16x8<VEC>(a.ema_sq, o0, valid, ws);
+        float p[8], g[8], e[8], s[8];
+        unpack8(wp, p); unpack8(wg, g); unpack8(we, e); unpack8(ws, s);
+        uint32_t re[8], rs[8], rp[8];
+        noise8<MODE>(a.ns_ema, o0, valid, re);
+        noise8<MODE>(a.ns_ema_sq, o0, valid, rs);
+        noise8<MODE>(a.ns_p, o0, valid, rp);
+        uint32_t oe[8], os[8], op[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float ej = a.beta1 * e[j] + one_m_b1 * g[j];
+            float sj = a.beta2 * s[j] + (one_m_b2 * g[j]) * g[j];
+            float denom = sqrtf(sj) / a.bcs + a.eps;
+            float pj = p[j] * decay;
+            pj = pj - (step_size * ej) / denom;
+            oe[j] = sr_bf16(ej, re[j]);
+            os[j] = sr_bf16(sj, rs[j]);
+            op[j] = sr_bf16(pj, rp[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            we[j] = pack2(oe[2 * j], oe[2 * j + 1]);
+            ws[j] = pack2(os[2 * j], os[2 * j + 1]);
+            wp[j] = pack2(op[2 * j], op[2 * j + 1]);
+        }
+        store_bf16x8<VEC>(a.ema, o0, valid, we);
+        store_bf16x8<VEC>(a.ema_sq, o0, valid, ws);
+        store_bf16x8<VEC>(a.p, o0, valid, wp);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 8-bit blockwise AdamW   (muon_sr/triton_adamw_8bit.py:27-99)
+// ---------------------------------------------------------------------------
+
+// The reference quantizer search (muon_sr/triton_adamw_8bit.py:27-53) over a
+// codebook held in LDS.
+__device__ __forceinline__ uint32_t quantize_search(float x, const float *Q, bool is_signed) {
+    int pivot = 127, lower_pivot = 0, upper_pivot = 255;
+    float lower = is_signed ? -1.0f : 0.0f;
+    float upper = 1.0f;
+    float val = Q[pivot];
+#pragma unroll
+    for (int shift = 0; shift < 7; ++shift) {
+        const int delta = 64 >> shift;
+        const bool right = x > val;
+        lower_pivot = right ? pivot : lower_pivot;
+        upper_pivot = right ? upper_pivot : pivot;
+        lower = right ? val : lower;
+        upper = right ? upper : val;
+        pivot += right ? delta : -delta;
+        val = Q[pivot];
+    }
+    int result;
+    if (x > val) result = (x > (upper + val) * 0.5f) ? upper_pivot : pivot;
+    else result = (x < (lower + val) * 0.5f) ? lower_pivot : pivot;
+    if (is_signed) {
+        const float decoded = Q[result];
+        const bool mismatch = (decoded < 0.0f) != (x < 0.0f);
+        result += mismatch ? ((x > 0.0f) ? 1 : -1) : 0;
+    }
+    return (uint32_t)result;
+}
+
+struct Adam8Args {
+    uint16_t *p;
+    const uint16_t *g;
+    void *s1;
+    void *s2;
+    float *absmax1;
+    float *absmax2;
+    const float *qmap1;
+    const float *qmap2;
+    int64_t n;
+    float lr, b1, b2, eps, wd, bc1, bc2;
+    Noise ns_p, ns_m, ns_v;
+};
+
+struct Adam8Consts {
+    float one_m_b1, one_m_b2, step_c, eps_c, decay;
+};
+
+__device__ __forceinline__ Adam8Consts adam8_consts(const Adam8Args &a) {
+    Adam8Consts c;
+    c.one_m_b1 = 1.0f - a.b1;
+    c.one_m_b2 = 1.0f - a.b2;
+    const float sqrt_bc2 = sqrtf(a.bc2);
+    c.step_c = (a.lr * sqrt_bc2) / a.bc1;     // :74  LR * sqrt(BC2) / BC1
+    c.eps_c = sqrt_bc2 * a.eps;               // :74  sqrt(BC2) * EPS
+    c.decay = 1.0f - a.lr * a.wd;             // :74  (1 - LR * WD)
+    return c;
+}
+
+// Threads per quantization block: BLOCK/8.  Work-group size: max(256, BLOCK/8).
+template <int MODE, int BLOCK, bool VEC>
+__global__ __launch_bounds__((BLOCK / 8 > THREADS) ? BLOCK / 8 : THREADS) void adamw8bit_quant_kernel(Adam8Args a) {
+    constexpr int TPB = BLOCK / 8;
+    constexpr int WG = TPB > THREADS ? TPB : THREADS;
+    constexpr int QB_PER_WG = WG / TPB;
+    constexpr int NWAVES = WG / 64;
+    __shared__ float q1s[256], q2s[256];
+    __shared__ float red_m[NWAVES], red_v[NWAVES];
+    for (int i = threadIdx.x; i < 256; i += WG) {
+        q1s[i] = a.qmap1[i];
+        q2s[i] = a.qmap2[i];
+    }
+    __syncthreads();
+    const Adam8Consts c = adam8_consts(a);
+    uint8_t *m8 = static_cast<uint8_t *>(a.s1);
+    uint8_t *v8 = static_cast<uint8_t *>(a.s2);
+    const int64_t nblocks = (a.n + BLOCK - 1) / BLOCK;
+    const int sub = threadIdx.x / TPB;       // quant block within the work-group
+    const int lane_q = threadIdx.x % TPB;    // thread within the quant block
+    for (int64_t qb0 = (int64_t)blockIdx.x * QB_PER_WG; qb0 < nblocks; qb0 += (int64_t)gridDim.x * QB_PER_WG) {
+        const int64_t qb = qb0 + sub;
+        const bool qb_ok = qb < nblocks;
+        const int64_t o0 = qb * BLOCK + lane_q * 8;
+        const int valid = qb_ok ? clamp_valid(a.n, o0) : 0;
+        uint32_t wp[4], wg[4], mc[8], vc[8];
+        load_bf16x8<VEC>(a.p, o0, valid, wp);
+        load_bf16x8<VEC>(a.g, o0, valid, wg);
+        load_u8x8<VEC>(m8, o0, valid, 127u, mc);
+        load_u8x8<VEC>(v8, o0, valid, 0u, vc);
+        const float ms = qb_ok ? a.absmax1[qb] : 0.0f;
+        const float vs = qb_ok ? a.absmax2[qb] : 0.0f;
+        float p[8], g[8], m[8], v[8];
+        unpack8(wp, p);
+        unpack8(wg, g);
+        uint32_t rp[8];
+        noise8<MODE>(a.ns_p, o0, valid, rp);
+        float mmax = 0.0f, vmax = 0.0f;
+        uint32_t op[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float mj = q1s[mc[j]] * ms;                                   // :65
+            float vj = q2s[vc[j]] * vs;                                   // :66
+            const bool fin = fabsf(g[j]) < __builtin_huge_valf();         // :70
+            mj = fin ? a.b1 * mj + c.one_m_b1 * g[j] : 0.0f;              // :71
+            vj = fin ? a.b2 * vj + (c.one_m_b2 * g[j]) * g[j] : 0.0f;     // :72
+            const float upd = (p[j] - (c.step_c * mj) / (sqrtf(vj) + c.eps_c)) * c.decay;  // :74
+            const uint32_t pin = (j & 1) ? (wp[j >> 1] >> 16) : (wp[j >> 1] & 0xffffu);
+            op[j] = fin ? sr_bf16(upd, rp[j]) : pin;                      // :75-78
+            m[j] = mj;
+            v[j] = vj;
+            if (j < valid) {
+                mmax = fmaxf(mmax, fabsf(mj));
+                vmax = fmaxf(vmax, fabsf(vj));
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wp[j] = pack2(op[2 * j], op[2 * j + 1]);
+        store_bf16x8<VEC>(a.p, o0, valid, wp);
+
+        // block absmax (:80-81): shuffles inside the wave, LDS across waves
+#pragma unroll
+        for (int off = (TPB < 64 ? TPB : 64) / 2; off >= 1; off >>= 1) {
+            mmax = fmaxf(mmax, __shfl_xor(mmax, off, 64));
+            vmax = fmaxf(vmax, __shfl_xor(vmax, off, 64));
+        }
+        if constexpr (TPB > 64) {
+            constexpr int WPQ = TPB / 64;  // waves per quant block
+            const int wave = threadIdx.x / 64;
+            if ((threadIdx.x & 63) == 0) {
+                red_m[wave] = mmax;
+                red_v[wave] = vmax;
+            }
+            __syncthreads();
+            const int w0 = (wave / WPQ) * WPQ;
+            mmax = red_m[w0];
+            vmax = red_v[w0];
+#pragma unroll
+            for (int w = 1; w < WPQ; ++w) {
+                mmax = fmaxf(mmax, red_m[w0 + w]);
+                vmax = fmaxf(vmax, red_v[w0 + w]);
+            }
+            __syncthreads();
+        }
+        const float md = mmax > 0.0f ? mmax : 1.0f;                       // :82
+        const float vd = vmax > 0.0f ? vmax : 1.0f;                       // :83
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            mc[j] = quantize_search(m[j] / md, q1s, true);                // :82,84
+            vc[j] = quantize_search(v[j] / vd, q2s, false);               // :83,85
+        }
+        store_u8x8<VEC>(m8, o0, valid, mc);
+        store_u8x8<VEC>(v8, o0, valid, vc);
+        if (qb_ok && lane_q == 0) {
+            a.absmax1[qb] = mmax;                                         // :86
+            a.absmax2[qb] = vmax;                                         // :87
+        }
+    }
+}
+
+// Excluded tensors: bf16 moments with SR on both moment stores (:90-99).
+template <int MODE, bool VEC>
+__global__ __launch_bounds__(THREADS) void adamw8bit_bf16_kernel(Adam8Args a) {
+    const Adam8Consts c = adam8_consts(a);
+    uint16_t *m16 = static_cast<uint16_t *>(a.s1);
+    uint16_t *v16 = static_cast<uint16_t *>(a.s2);
+    const int64_t groups = (a.n + 7) >> 3;
+    for (int64_t t = (int64_t)blockIdx.x * THREADS + threadIdx.x; t < groups; t += (int64_t)gridDim.x * THREADS) {
+        const int64_t o0 = t << 3;
+        const int valid = clamp_valid(a.n, o0);
+        uint32_t wp[4], wg[4], wm[4], wv[4];
+        load_bf16x8<VEC>(a.p, o0, valid, wp);
+        load_bf16x8<VEC>(a.g, o0, valid, wg);
+        load_bf16x8<VEC>(m16, o0, valid, wm);
+        load_bf16x8<VEC>(v16, o0, valid, wv);
+        float p[8], g[8], m[8], v[8];
+        unpack8(wp, p); unpack8(wg, g); unpack8(wm, m); unpack8(wv, v);
+        uint32_t rp[8], rm[8], rv[8];
+        noise8<MODE>(a.ns_p, o0, valid, rp);
+        noise8<MODE>(a.ns_m, o0, valid, rm);
+        noise8<MODE>(a.ns_v, o0, valid, rv);
+        uint32_t op[8], om[8], ov[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bool fin = fabsf(g[j]) < __builtin_huge_valf();
+            const float mj = fin ? a.b1 * m[j] + c.one_m_b1 * g[j] : 0.0f;
+            const float vj = fin ? a.b2 * v[j] + (c.one_m_b2 * g[j]) * g[j] : 0.0f;
+            const float upd = (p[j] - (c.step_c * mj) / (sqrtf(vj) + c.eps_c)) * c.decay;
+            const uint32_t pin = (j & 1) ? (wp[j >> 1] >> 16) : (wp[j >> 1] & 0xffffu);
+            op[j] = fin ? sr_bf16(upd, rp[j]) : pin;
+            om[j] = sr_bf16(mj, rm[j]);
+            ov[j] = sr_bf16(vj, rv[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            wp[j] = pack2(op[2 * j], op[2 * j + 1]);
+            wm[j] = pack2(om[2 * j], om[2 * j + 1]);
+            wv[j] = pack2(ov[2 * j], ov[2 * j + 1]);
+        }
+        store_bf16x8<VEC>(a.p, o0, valid, wp);
+        store_bf16x8<VEC>(m16, o0, valid, wm);
+        store_bf16x8<VEC>(v16, o0, valid, wv);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Muon prepare / apply   (muon_sr/triton_muon_sr.py:18-80)
+// ---------------------------------------------------------------------------
+
+constexpr int MAX_TABLE = 240;  // pointers per launch (kernel-argument table)
+
+struct PrepareArgs {
+    const uint16_t *grads[MAX_TABLE];
+    uint16_t *buf;       // stack base (already offset to the first matrix of this launch)
+    uint16_t *out;
+    int64_t numel;
+    int64_t stack_off0;  // stack offset of matrix 0 of this launch (noise counter base)
+    float beta;
+    Noise ns;
+};
+
+template <int MODE, bool NEST, bool VEC>
+__global__ __launch_bounds__(THREADS) void muon_prepare_kernel(PrepareArgs a) {
+    const int i = blockIdx.y;
+    const uint16_t *g = a.grads[i];
+    uint16_t *buf = a.buf + (int64_t)i * a.numel;
+    uint16_t *out = a.out + (int64_t)i * a.numel;
+    const int64_t base = a.stack_off0 + (int64_t)i * a.numel;
+    const float one_m_beta = 1.0f - a.beta;
+    const int64_t groups = (a.numel + 7) >> 3;
+    for (int64_t t = (int64_t)blockIdx.x * THREADS + threadIdx.x; t < groups; t += (int64_t)gridDim.x * THREADS) {
+        const int64_t o0 = t << 3;
+        const int valid = clamp_valid(a.numel, o0);
+        uint32_t wg[4], wb[4];
+        load_bf16x8<VEC>(g, o0, valid, wg);
+        load_bf16x8<VEC>(buf, o0, valid, wb);
+        float gf[8], bf[8];
+        unpack8(wg, gf);
+        unpack8(wb, bf);
+        uint32_t r[8];
+        if (VEC || MODE != NOISE_PHILOX8) {
+            noise8<MODE>(a.ns, base + o0, valid, r);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) r[j] = (j < valid) ? noise1<MODE>(a.ns, base + o0 + j) : 0u;
+        }
+        uint32_t ob[8], ou[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float nb = bf[j] + one_m_beta * (gf[j] - bf[j]);        // :37
+            const float upd = NEST ? gf[j] + a.beta * (nb - gf[j]) : nb;  // :39-42
+            ob[j] = sr_bf16(nb, r[j]);                                    // :44-49
+            ou[j] = rne_bf16(upd);                                        // :50
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            wb[j] = pack2(ob[2 * j], ob[2 * j + 1]);
+            wg[j] = pack2(ou[2 * j], ou[2 * j + 1]);
+        }
+        store_bf16x8<VEC>(buf, o0, valid, wb);
+        store_bf16x8<VEC>(out, o0, valid, wg);
+    }
+}
+
+struct ApplyArgs {
+    uint16_t *params[MAX_TABLE];
+    uint32_t seeds[MAX_TABLE];
+    const uint16_t *upd;  // [count][numel] for this launch
+    int64_t numel;
+    float lr, wd, scale;
+    const uint16_t *inject;  // [count][numel] for this launch (NOISE_INJECT)
+};
+
+template <int MODE, bool VEC>
+__global__ __launch_bounds__(THREADS) void muon_apply_kernel(ApplyArgs a) {
+    const int i = blockIdx.y;
+    uint16_t *p = a.params[i];
+    const uint16_t *u = a.upd + (int64_t)i * a.numel;
+    Noise ns;
+    ns.key = seed_key(a.seeds[i], 0);
+    ns.inject = a.inject ? a.inject + (int64_t)i * a.numel : nullptr;
+    const float decay = 1.0f - a.lr * a.wd;                               // :72
+    const int64_t groups = (a.numel + 7) >> 3;
+    for (int64_t t = (int64_t)blockIdx.x * THREADS + threadIdx.x; t < groups; t += (int64_t)gridDim.x * THREADS) {
+        const int64_t o0 = t << 3;
+        const int valid = clamp_valid(a.numel, o0);
+        uint32_t wp[4], wu[4];
+        load_bf16x8<VEC>(p, o0, valid, wp);
+        load_bf16x8<VEC>(u, o0, valid, wu);
+        float pf[8], uf[8];
+        unpack8(wp, pf);
+        unpack8(wu, uf);
+        uint32_t r[8];
+        noise8<MODE>(ns, o0, valid, r);
+        uint32_t op[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float t1 = uf[j] * a.scale;                             // :70
+            float pj = pf[j] * decay;                                     // :72
+            pj = pj - a.lr * t1;                                          // :73
+            op[j] = sr_bf16(pj, r[j]);                                    // :75-80
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wp[j] = pack2(op[2 * j], op[2 * j + 1]);
+        store_bf16x8<VEC>(p, o0, valid, wp);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Diagnostics
+// ---------------------------------------------------------------------------
+
+template <int MODE>
+__global__ __launch_bounds__(THREADS) void noise_fill_kernel(uint16_t *out, int64_t n, int64_t off0, Noise ns) {
+    for (int64_t i = (int64_t)blockIdx.x * THREADS + threadIdx.x; i < n; i += (int64_t)gridDim.x * THREADS)
+        out[i] = (uint16_t)noise1<MODE>(ns, off0 + i);
+}
+
+__global__ __launch_bounds__(THREADS) void quantize_kernel(const float *x, uint8_t *out, int64_t n,
+                                                          const float *qmap, int is_signed) {
+    __shared__ float q[256];
+    for (int i = threadIdx.x; i < 256; i += THREADS) q[i] = qmap[i];
+    __syncthreads();
+    for (int64_t i = (int64_t)blockIdx.x * THREADS + threadIdx.x; i < n; i += (int64_t)gridDim.x * THREADS)
+        out[i] = (uint8_t)quantize_search(x[i], q, is_signed != 0);
+}
+
+}  // namespace msr
+
+using namespace msr;
+
+static inline Noise make_noise(uint32_t seed, uint32_t k, const uint16_t *inject, int64_t stream_stride) {
+    Noise ns;
+    ns.key = seed_key(seed, k);
+    ns.inject = inject ? inject + (int64_t)k * stream_stride : nullptr;
+    return ns;
+}
+
+#define MSR_CHECK_MODE(mode, inject)                                                         \
+    do {                                                                                     \
+        if ((mode) < 0 || (mode) > 2) { set_error("noise_mode %d is not 0, 1 or 2", (int)(mode)); return MSR_ERR_ARG; } \
+        if ((mode) == NOISE_INJECT && !(inject)) { set_error("noise_mode INJECT needs an inject buffer"); return MSR_ERR_ARG; } \
+    } while (0)
+
+template <int BLOCK>
+static void launch_quant(int mode, bool vec, const Adam8Args &a, hipStream_t s, int64_t nblocks) {
+    constexpr int TPB = BLOCK / 8;
+    constexpr int WG = TPB > THREADS ? TPB : THREADS;
+    constexpr int QB_PER_WG = WG / TPB;
+    const unsigned grid = grid_for(nblocks, QB_PER_WG, 256 * 16);
+    if (mode == NOISE_TRITON) {
+        if (vec) hipLaunchKernelGGL((adamw8bit_quant_kernel<NOISE_TRITON, BLOCK, true>), dim3(grid), dim3(WG), 0, s, a);
+        else hipLaunchKernelGGL((adamw8bit_quant_kernel<NOISE_TRITON, BLOCK, false>), dim3(grid), dim3(WG), 0, s, a);
+    } else if (mode == NOISE_PHILOX8) {
+        if (vec) hipLaunchKernelGGL((adamw8bit_quant_kernel<NOISE_PHILOX8, BLOCK, true>), dim3(grid), dim3(WG), 0, s, a);
+        else hipLaunchKernelGGL((adamw8bit_quant_kernel<NOISE_PHILOX8, BLOCK, false>), dim3(grid), dim3(WG), 0, s, a);
+    } else {
+        if (vec) hipLaunchKernelGGL((adamw8bit_quant_kernel<NOISE_INJECT, BLOCK, true>), dim3(grid), dim3(WG), 0, s, a);
+        else hipLaunchKernelGGL((adamw8bit_quant_kernel<NOISE_INJECT, BLOCK, false>), dim3(grid), dim3(WG), 0, s, a);
+    }
+}
+
+extern "C" {
+
+int msr_version(void) { return 100; }
+
+const char *msr_last_error(void) { return g_err; }
+
+int msr_sr_accum(uint16_t *acc, const void *grad, int32_t grad_is_f32, int64_t n, uint32_t seed, int32_t zero_init,
+                 int32_t noise_mode, const uint16_t *inject, msr_stream_t stream) {
+    if (n < 0 || (n > 0 && (!acc || !grad))) { set_error("msr_sr_accum: bad arguments"); return MSR_ERR_ARG; }
+    MSR_CHECK_MODE(noise_mode, inject);
+    if (n == 0) return MSR_OK;
+    const Noise ns = make_noise(seed, 0, inject, n);
+    const bool vec = aligned(acc, 16) && aligned(grad, 16);
+    const unsigned grid = grid_for((n + 7) / 8, THREADS);
+    hipStream_t s = (hipStream_t)stream;
+#define LAUNCH_ACC(GF, Z, V)                                                                                   \
+    MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((sr_accum_kernel<M, GF, Z, V>), dim3(grid), dim3(THREADS), 0, s, acc, grad, n, ns))
+    if (grad_is_f32) {
+        if (zero_init) { if (vec) { LAUNCH_ACC(true, true, true); } else { LAUNCH_ACC(true, true, false); } }
+        else { if (vec) { LAUNCH_ACC(true, false, true); } else { LAUNCH_ACC(true, false, false); } }
+    } else {
+        if (zero_init) { if (vec) { LAUNCH_ACC(false, true, true); } else { LAUNCH_ACC(false, true, false); } }
+        else { if (vec) { LAUNCH_ACC(false, false, true); } else { LAUNCH_ACC(false, false, false); } }
+    }
+#undef LAUNCH_ACC
+    return check_launch("msr_sr_accum");
+}
+
+int msr_adamw_bf16_step(uint16_t *p, const uint16_t *g, uint16_t *ema, uint16_t *ema_sq, int64_t n, float lr,
+                        float beta1, float beta2, float eps, float weight_decay, float bias_correction,
+                        float bias_correction_sqrt, uint32_t seed, int32_t noise_mode, const uint16_t *inject,
+                        msr_stream_t stream) {
+    if (n < 0 || (n > 0 && (!p || !g || !ema || !ema_sq))) { set_error("msr_adamw_bf16_step: bad arguments"); return MSR_ERR_ARG; }
+    MSR_CHECK_MODE(noise_mode, inject);
+    if (n == 0) return MSR_OK;
+    AdamWArgs a;
+    a.p = p; a.g = g; a.ema = ema; a.ema_sq = ema_sq; a.n = n;
+    a.lr = lr; a.beta1 = beta1; a.beta2 = beta2; a.eps = eps; a.wd = weight_decay;
+    a.bc = bias_correction; a.bcs = bias_correction_sqrt;
+    a.ns_ema = make_noise(seed, 0, inject, n);
+    a.ns_ema_sq = make_noise(seed, 1, inject, n);
+    a.ns_p = make_noise(seed, 2, inject, n);
+    const bool vec = aligned(p, 16) && aligned(g, 16) && aligned(ema, 16) && aligned(ema_sq, 16);
+    const unsigned grid = grid_for((n + 7) / 8, THREADS);
+    hipStream_t s = (hipStream_t)stream;
+    if (vec) { MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((adamw_bf16_kernel<M, true>), dim3(grid), dim3(THREADS), 0, s, a)); }
+    else { MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((adamw_bf16_kernel<M, false>), dim3(grid), dim3(THREADS), 0, s, a)); }
+    return check_launch("msr_adamw_bf16_step");
+}
+
+int msr_adamw8bit_step(uint16_t *p, const uint16_t *g, void *state1, void *state2, float *absmax1, float *absmax2,
+                       const float *qmap1, const float *qmap2, int64_t n, int32_t block, int32_t quantized, float lr,
+                       float beta1, float beta2, float eps, float weight_decay, float bc1, float bc2, uint32_t seed,
+                       int32_t noise_mode, const uint16_t *inject, msr_stream_t stream) {
+    if (n < 0 || (n > 0 && (!p || !g || !state1 || !state2))) { set_error("msr_adamw8bit_step: bad arguments"); return MSR_ERR_ARG; }
+    if (block < 32 || block > 4096 || (block & (block - 1))) {
+        set_error("msr_adamw8bit_step: block %d is not a power of two in [32, 4096]", (int)block);
+        return MSR_ERR_ARG;
+    }
+    if (quantized && (!absmax1 || !absmax2 || !qmap1 || !qmap2)) { set_error("msr_adamw8bit_step: quantized state needs absmax and qmaps"); return MSR_ERR_ARG; }
+    MSR_CHECK_MODE(noise_mode, inject);
+    if (n == 0) return MSR_OK;
+    Adam8Args a;
+    a.p = p; a.g = g; a.s1 = state1; a.s2 = state2; a.absmax1 = absmax1; a.absmax2 = absmax2;
+    a.qmap1 = qmap1; a.qmap2 = qmap2; a.n = n;
+    a.lr = lr; a.b1 = beta1; a.b2 = beta2; a.eps = eps; a.wd = weight_decay; a.bc1 = bc1; a.bc2 = bc2;
+    a.ns_p = make_noise(seed, 0, inject, n);
+    a.ns_m = make_noise(seed, 1, inject, n);
+    a.ns_v = make_noise(seed, 2, inject, n);
+    hipStream_t s = (hipStream_t)stream;
+    if (quantized) {
+        const bool vec = aligned(p, 16) && aligned(g, 16) && aligned(state1, 8) && aligned(state2, 8);
+        const int64_t nblocks = (n + block - 1) / block;
+        switch (block) {
+        case 32: launch_quant<32>(noise_mode, vec, a, s, nblocks); break;
+        case 64: launch_quant<64>(noise_mode, vec, a, s, nblocks); break;
+        case 128: launch_quant<128>(noise_mode, vec, a, s, nblocks); break;
+        case 256: launch_quant<256>(noise_mode, vec, a, s, nblocks); break;
+        case 512: launch_quant<512>(noise_mode, vec, a, s, nblocks); break;
+        case 1024: launch_quant<1024>(noise_mode, vec, a, s, nblocks); break;
+        case 2048: launch_quant<2048>(noise_mode, vec, a, s, nblocks); break;
+        default: launch_quant<4096>(noise_mode, vec, a, s, nblocks); break;
+        }
+    } else {
+        const bool vec = aligned(p, 16) && aligned(g, 16) && aligned(state1, 16) && aligned(state2, 16);
+        const unsigned grid = grid_for((n + 7) / 8, THREADS);
+        if (vec) { MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((adamw8bit_bf16_kernel<M, true>), dim3(grid), dim3(THREADS), 0, s, a)); }
+        else { MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((adamw8bit_bf16_kernel<M, false>), dim3(grid), dim3(THREADS), 0, s, a)); }
+    }
+    return check_launch("msr_adamw8bit_step");
+}
+
+int msr_muon_prepare(const uint16_t *const *grads, uint16_t *buf, uint16_t *out, int64_t numel_each, int32_t count,
+                     float beta, int32_t nesterov, uint32_t seed, int32_t noise_mode, const uint16_t *inject,
+                     msr_stream_t stream) {
+    if (numel_each < 0 || count < 0 || (numel_each > 0 && count > 0 && (!grads || !buf || !out))) {
+        set_error("msr_muon_prepare: bad arguments");
+        return MSR_ERR_ARG;
+    }
+    MSR_CHECK_MODE(noise_mode, inject);
+    if (numel_each == 0 || count == 0) return MSR_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const bool rows_aligned = (numel_each % 8) == 0 && aligned(buf, 16) && aligned(out, 16);
+    for (int32_t c0 = 0; c0 < count; c0 += MAX_TABLE) {
+        const int32_t cnt = (count - c0) < MAX_TABLE ? (count - c0) : MAX_TABLE;
+        PrepareArgs a;
+        bool vec = rows_aligned;
+        for (int32_t i = 0; i < cnt; ++i) {
+            if (!grads[c0 + i]) { set_error("msr_muon_prepare: null gradient pointer %d", (int)(c0 + i)); return MSR_ERR_ARG; }
+            a.grads[i] = grads[c0 + i];
+            vec = vec && aligned(grads[c0 + i], 16);
+        }
+        a.buf = buf + (int64_t)c0 * numel_each;
+        a.out = out + (int64_t)c0 * numel_each;
+        a.numel = numel_each;
+        a.stack_off0 = (int64_t)c0 * numel_each;
+        a.beta = beta;
+        a.ns = make_noise(seed, 0, inject, 0);
+        const unsigned gx = grid_for((numel_each + 7) / 8, THREADS, (256 * 32 + cnt - 1) / cnt);
+        const dim3 grid(gx, (unsigned)cnt);
+#define LAUNCH_PREP(NEST, V) MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((muon_prepare_kernel<M, NEST, V>), grid, dim3(THREADS), 0, s, a))
+        if (nesterov) { if (vec) { LAUNCH_PREP(true, true); } else { LAUNCH_PREP(true, false); } }
+        else { if (vec) { LAUNCH_PREP(false, true); } else { LAUNCH_PREP(false, false); } }
+#undef LAUNCH_PREP
+        int rc = check_launch("msr_muon_prepare");
+        if (rc) return rc;
+    }
+    return MSR_OK;
+}
+
+int msr_muon_apply(uint16_t *const *params, const uint16_t *upd, int64_t numel_each, int32_t count, float lr,
+                   float weight_decay, float scale, const uint32_t *seeds, int32_t noise_mode, const uint16_t *inject,
+                   msr_stream_t stream) {
+    if (numel_each < 0 || count < 0 || (numel_each > 0 && count > 0 && (!params || !upd || !seeds))) {
+        set_error("msr_muon_apply: bad arguments");
+        return MSR_ERR_ARG;
+    }
+    MSR_CHECK_MODE(noise_mode, inject);
+    if (numel_each == 0 || count == 0) return MSR_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const bool rows_aligned = (numel_each % 8) == 0 && aligned(upd, 16);
+    for (int32_t c0 = 0; c0 < count; c0 += MAX_TABLE) {
+        const int32_t cnt = (count - c0) < MAX_TABLE ? (count - c0) : MAX_TABLE;
+        ApplyArgs a;
+        bool vec = rows_aligned;
+        for (int32_t i = 0; i < cnt; ++i) {
+            if (!params[c0 + i]) { set_error("msr_muon_apply: null parameter pointer %d", (int)(c0 + i)); return MSR_ERR_ARG; }
+            a.params[i] = params[c0 + i];
+            a.seeds[i] = seeds[c0 + i];
+            vec = vec && aligned(params[c0 + i], 16);
+        }
+        a.upd = upd + (int64_t)c0 * numel_each;
+        a.numel = numel_each;
+        a.lr = lr; a.wd = weight_decay; a.scale = scale;
+        a.inject = inject ? inject + (int64_t)c0 * numel_each : nullptr;
+        const unsigned gx = grid_for((numel_each + 7) / 8, THREADS, (256 * 32 + cnt - 1) / cnt);
+        const dim3 grid(gx, (unsigned)cnt);
+        if (vec) { MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((muon_apply_kernel<M, true>), grid, dim3(THREADS), 0, s, a)); }
+        else { MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((muon_apply_kernel<M, false>), grid, dim3(THREADS), 0, s, a)); }
+        int rc = check_launch("msr_muon_apply");
+        if (rc) return rc;
+    }
+    return MSR_OK;
+}
+
+int msr_noise_fill(uint16_t *out, int64_t n, int64_t offset0, uint32_t seed, uint32_t k, int32_t noise_mode,
+                   msr_stream_t stream) {
+    if (n < 0 || (n > 0 && !out) || offset0 < 0) { set_error("msr_noise_fill: bad arguments"); return MSR_ERR_ARG; }
+    if (noise_mode != NOISE_TRITON && noise_mode != NOISE_PHILOX8) { set_error("msr_noise_fill: mode must be 0 or 1"); return MSR_ERR_ARG; }
+    if (n == 0) return MSR_OK;
+    const Noise ns = make_noise(seed, k, nullptr, 0);
+    const unsigned grid = grid_for(n, THREADS);
+    hipStream_t s = (hipStream_t)stream;
+    if (noise_mode == NOISE_TRITON) hipLaunchKernelGGL((noise_fill_kernel<NOISE_TRITON>), dim3(grid), dim3(THREADS), 0, s, out, n, offset0, ns);
+    else hipLaunchKernelGGL((noise_fill_kernel<NOISE_PHILOX8>), dim3(grid), dim3(THREADS), 0, s, out, n, offset0, ns);
+    return check_launch("msr_noise_fill");
+}
+
+int msr_quantize(const float *x, uint8_t *out, int64_t n, const float *qmap, int32_t is_signed, msr_stream_t stream) {
+    if (n < 0 || (n > 0 && (!x || !out || !qmap))) { set_error("msr_quantize: bad arguments"); return MSR_ERR_ARG; }
+    if (n == 0) return MSR_OK;
+    hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(n, THREADS)), dim3(THREADS), 0, (hipStream_t)stream, x, out, n,
+                       qmap, is_signed);
+    return check_launch("msr_quantize");
+}
+
+}  // extern "C"

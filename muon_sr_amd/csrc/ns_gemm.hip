@@ -1,0 +1,435 @@
+// Batched Newton-Schulz orthogonalisation on gfx950 bf16 MFMA.
+//
+// Every product of the iteration is written as an "NT" GEMM,
+//     D[m][n] = alpha * sum_k P[m][k] * Q[n][k] + beta * C[m][n],
+// with both operands K-contiguous, so each MFMA operand fragment is one
+// 16-byte LDS read.  The iterate X (m x n, m <= n) is kept in two layouts,
+// X (row-major m x n) and XT (row-major n x m):
+//     A  = X X^T          P = X,  Q = X      (symmetric: upper tiles + mirror)
+//     B  = c A A + b A    P = A,  Q = A      (A symmetric, so A A = A A^T)
+//     X' = B X + a X      P = B,  Q = XT     (writes X' and X'^T)
+// Workspace matrices are zero-padded to multiples of 256; zero padding is
+// preserved exactly by all three products, so only the final store is
+// bounds-checked.
+//
+// Kernel shape: 256 threads (4 wave64s in a 2x2 grid), a 256x256 output tile
+// per work-group, K staged through LDS in 64-wide slabs, double buffered
+// (2 x 64 KiB).  Each wave owns a 128x128 sub-tile = 4x4 tiles of the 32x32x16
+// bf16 MFMA (fp32 accumulators).  LDS rows are XOR-swizzled by (row & 7) in
+// 16-byte units so the fragment reads of 8 consecutive rows hit 8 distinct
+// bank groups.
+#include "common.hpp"
+#include "../../include/muon_sr_amd.h"
+
+namespace msr {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int GEMM_THREADS = 256;
+constexpr int CHUNKS = BM * BK / 8;  // 16-byte chunks per operand slab (2048)
+
+struct GemmArgs {
+    const uint16_t *P; int64_t ldp, sP;
+    const uint16_t *Q; int64_t ldq, sQ;
+    const uint16_t *C; int64_t ldc, sC;
+    uint16_t *D; int64_t ldd, sD;
+    uint16_t *DT; int64_t lddt, sDT;
+    int M, N, K;       // padded extents (multiples of 256, 256, 64)
+    int Mv, Nv;        // stores are limited to m < Mv, n < Nv
+    float alpha, beta;
+    int tiles_m, tiles_n;
+    int symmetric;     // M == N, P == Q: only tiles ti <= tj, mirrored into D
+    int d_vec;         // D rows allow 8-byte stores (set by launch_gemm)
+};
+
+__device__ __forceinline__ void decode_tile(const GemmArgs &a, int t, int &ti, int &tj) {
+    if (a.symmetric) {
+        const int T = a.tiles_m;
+        int row = 0;
+        int start = 0;
+        while (start + (T - row) <= t) {
+            start += T - row;
+            ++row;
+        }
+        ti = row;
+        tj = row + (t - start);
+    } else {
+        ti = t / a.tiles_n;
+        tj = t - ti * a.tiles_n;
+    }
+}
+
+__global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
+    __shared__ bf16x8_t smem[2][2][CHUNKS];  // [stage][P/Q][row*8 + swizzled chunk]
+
+    int ti, tj;
+    decode_tile(a, blockIdx.x, ti, tj);
+    const int64_t bz = blockIdx.y;
+    const int m0 = ti * BM, n0 = tj * BN;
+    const uint16_t *Pb = a.P + bz * a.sP + (int64_t)m0 * a.ldp;
+    const uint16_t *Qb = a.Q + bz * a.sQ + (int64_t)n0 * a.ldq;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    bf16x8_t rp[8], rq[8];
+    const int lc = tid & 7;  // 16-byte chunk within the 64-wide K slab
+
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int row = (i * GEMM_THREADS + tid) >> 3;
+            rp[i] = *reinterpret_cast<const bf16x8_t *>(Pb + (int64_t)row * a.ldp + k0 + lc * 8);
+            rq[i] = *reinterpret_cast<const bf16x8_t *>(Qb + (int64_t)row * a.ldq + k0 + lc * 8);
+        }
+    };
+    auto lstore = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int row = (i * GEMM_THREADS + tid) >> 3;
+            const int idx = row * 8 + (lc ^ (row & 7));
+            smem[st][0][idx] = rp[i];
+            smem[st][1][idx] = rq[i];
+        }
+    };
+
+    f32x16_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int KT = a.K / BK;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+
+    const int r32 = lane & 31;
+    const int khalf = lane >> 5;
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < KT) gload((kt + 1) * BK);
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const int c = ks * 2 + khalf;
+            bf16x8_t pa[4], qb[4];
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+                const int row = wm * 128 + mi * 32 + r32;
+                pa[mi] = smem[cur][0][row * 8 + (c ^ (row & 7))];
+            }
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const int row = wn * 128 + ni * 32 + r32;
+                qb[ni] = smem[cur][1][row * 8 + (c ^ (row & 7))];
+            }
+            // MFMA A-operand = Q rows (n), B-operand = P rows (m): lane l then
+            // holds D[m = l % 32][n = 8r + 4(l / 32) + q] for accumulator 4r + q.
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qb[ni], pa[mi], acc[mi][ni], 0, 0, 0);
+        }
+        if (kt + 1 < KT) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // ---------------- epilogue ----------------
+    const bool mirror = a.symmetric && ti != tj;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+        const int m = m0 + wm * 128 + mi * 32 + r32;
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int n = n0 + wn * 128 + ni * 32 + 8 * r + 4 * khalf;
+                float v[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = a.alpha * acc[mi][ni][4 * r + q];
+                if (a.C) {
+                    const uint2 cw = *reinterpret_cast<const uint2 *>(a.C + bz * a.sC + (int64_t)m * a.ldc + n);
+                    v[0] = v[0] + a.beta * bf16_lo(cw.x);
+                    v[1] = v[1] + a.beta * bf16_hi(cw.x);
+                    v[2] = v[2] + a.beta * bf16_lo(cw.y);
+                    v[3] = v[3] + a.beta * bf16_hi(cw.y);
+                }
+                uint32_t h[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) h[q] = rne_bf16(v[q]);
+                const bool m_ok = m < a.Mv;
+                if (a.D && m_ok) {
+                    uint16_t *dp = a.D + bz * a.sD + (int64_t)m * a.ldd + n;
+                    if (a.d_vec && n + 3 < a.Nv) {
+                        *reinterpret_cast<uint2 *>(dp) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            if (n + q < a.Nv) dp[q] = (uint16_t)h[q];
+                    }
+                }
+                if (mirror) {
+                    uint16_t *dp = a.D + bz * a.sD + (int64_t)n * a.ldd + m;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) dp[(int64_t)q * a.ldd] = (uint16_t)h[q];
+                }
+                if (a.DT && m_ok) {
+                    uint16_t *tp = a.DT + bz * a.sDT + (int64_t)n * a.lddt + m;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (n + q < a.Nv) tp[(int64_t)q * a.lddt] = (uint16_t)h[q];
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// NS prologue: deterministic Frobenius norm and normalise + transpose
+// ---------------------------------------------------------------------------
+
+constexpr int NPART = 64;         // partial sums per matrix (fixed: deterministic order)
+constexpr int NORM_THREADS = 256;
+
+__global__ __launch_bounds__(NORM_THREADS) void sumsq_kernel(const uint16_t *in, int64_t numel, float *partial) {
+    const int64_t b = blockIdx.y;
+    const uint16_t *x = in + b * numel;
+    float s = 0.0f;
+    for (int64_t i = (int64_t)blockIdx.x * NORM_THREADS + threadIdx.x; i < numel; i += (int64_t)NPART * NORM_THREADS) {
+        const float v = bf16_to_f32(x[i]);
+        s = s + v * v;
+    }
+    __shared__ float red[NORM_THREADS];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = NORM_THREADS / 2; w > 0; w >>= 1) {
+        if (threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partial[b * NPART + blockIdx.x] = red[0];
+}
+
+// Writes S = x0 in the input layout (Rp x Cp, ld ldS) and T = x0^T (Cp x Rp, ld ldT),
+// x0 = bf16(u / d), d = bf16(bf16(||u||_F) + 1e-7), zeros outside rows x cols.
+// S or T may be null.  64 x 64 tiles, transposed through LDS.
+__global__ __launch_bounds__(256) void normalize_kernel(const uint16_t *in, int64_t rows, int64_t cols,
+                                                        const float *partial, uint16_t *S, int64_t ldS, int64_t sS,
+                                                        uint16_t *T, int64_t ldT, int64_t sT, int64_t Rp,
+                                                        int64_t Cp) {
+    __shared__ uint16_t tile[64][66];
+    __shared__ float dsh;
+    const int64_t b = blockIdx.z;
+    if (threadIdx.x == 0) {
+        float s = 0.0f;
+        for (int i = 0; i < NPART; ++i) s = s + partial[b * NPART + i];
+        const float nrm = __uint_as_float(rne_bf16(sqrtf(s)) << 16);
+        dsh = __uint_as_float(rne_bf16(nrm + 1e-7f) << 16);
+    }
+    __syncthreads();
+    const float d = dsh;
+    const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+    const uint16_t *x = in + b * rows * cols;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int i = ty; i < 64; i += 4) {
+        const int64_t r = r0 + i, c = c0 + tx;
+        uint16_t h = 0;
+        if (r < rows && c < cols) h = (uint16_t)rne_bf16(bf16_to_f32(x[r * cols + c]) / d);
+        tile[i][tx] = h;
+        if (S && r < Rp && c < Cp) S[b * sS + r * ldS + c] = h;
+    }
+    __syncthreads();
+    if (T) {
+        for (int i = ty; i < 64; i += 4) {
+            const int64_t c = c0 + i, r = r0 + tx;  // T[c][r]
+            if (c < Cp && r < Rp) T[b * sT + c * ldT + r] = tile[tx][i];
+        }
+    }
+}
+
+static inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+struct NSLayout {
+    int64_t m, n, mp, np;
+    bool transposed;
+    size_t off_x[2], off_xt[2], off_a, off_b, off_part, total;
+};
+
+static NSLayout ns_layout(int64_t batch, int64_t rows, int64_t cols) {
+    NSLayout L;
+    L.transposed = rows > cols;
+    L.m = L.transposed ? cols : rows;
+    L.n = L.transposed ? rows : cols;
+    L.mp = round_up(L.m, 256);
+    L.np = round_up(L.n, 256);
+    const size_t xs = (size_t)batch * L.mp * L.np * 2;
+    const size_t as = (size_t)batch * L.mp * L.mp * 2;
+    size_t o = 0;
+    auto take = [&](size_t s) { size_t r = o; o += (s + 255) & ~(size_t)255; return r; };
+    L.off_x[0] = take(xs);
+    L.off_xt[0] = take(xs);
+    L.off_x[1] = take(xs);
+    L.off_xt[1] = take(xs);
+    L.off_a = take(as);
+    L.off_b = take(as);
+    L.off_part = take((size_t)batch * NPART * 4);
+    L.total = o;
+    return L;
+}
+
+static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
+    GemmArgs a = a0;
+    a.tiles_m = a.M / BM;
+    a.tiles_n = a.N / BN;
+    a.d_vec = a.D && aligned(a.D, 8) && (a.ldd % 4) == 0 && (a.sD % 4) == 0;
+    const int64_t tiles = a.symmetric ? (int64_t)a.tiles_m * (a.tiles_m + 1) / 2 : (int64_t)a.tiles_m * a.tiles_n;
+    for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
+        const int64_t nb = (batch - b0) < 65535 ? (batch - b0) : 65535;
+        GemmArgs ab = a;
+        ab.P += b0 * a.sP;
+        ab.Q += b0 * a.sQ;
+        if (ab.C) ab.C += b0 * a.sC;
+        if (ab.D) ab.D += b0 * a.sD;
+        if (ab.DT) ab.DT += b0 * a.sDT;
+        hipLaunchKernelGGL(gemm_nt_kernel, dim3((unsigned)tiles, (unsigned)nb), dim3(GEMM_THREADS), 0, s, ab);
+        int rc = check_launch("gemm_nt_kernel");
+        if (rc) return rc;
+    }
+    return MSR_OK;
+}
+
+}  // namespace msr
+
+using namespace msr;
+
+extern "C" {
+
+int msr_gemm_nt(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q, int64_t ldq, int64_t strideQ,
+                const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D, int64_t ldd, int64_t strideD, int64_t M,
+                int64_t N, int64_t K, int64_t batch, float alpha, float beta, msr_stream_t stream) {
+    if (!P || !Q || !D || batch < 0 || M <= 0 || N <= 0 || K <= 0 || (M % BM) || (N % BN) || (K % BK)) {
+        set_error("msr_gemm_nt: need M, N multiples of 256 and K a multiple of 64 (got %lld, %lld, %lld)",
+                  (long long)M, (long long)N, (long long)K);
+        return MSR_ERR_ARG;
+    }
+    if (!aligned(P, 16) || !aligned(Q, 16) || !aligned(D, 8) || (C && !aligned(C, 8)) || (ldp % 8) || (ldq % 8) ||
+        (ldd % 4) || (C && (ldc % 4)) || (strideP % 8) || (strideQ % 8)) {
+        set_error("msr_gemm_nt: operands must be 16-byte aligned with row strides a multiple of 8 elements");
+        return MSR_ERR_ALIGN;
+    }
+    if (batch == 0) return MSR_OK;
+    GemmArgs a = {};
+    a.P = P; a.ldp = ldp; a.sP = strideP;
+    a.Q = Q; a.ldq = ldq; a.sQ = strideQ;
+    a.C = (beta != 0.0f) ? C : nullptr; a.ldc = ldc; a.sC = strideC;
+    a.D = D; a.ldd = ldd; a.sD = strideD;
+    a.DT = nullptr;
+    a.M = (int)M; a.N = (int)N; a.K = (int)K; a.Mv = (int)M; a.Nv = (int)N;
+    a.alpha = alpha; a.beta = beta; a.symmetric = 0;
+    return launch_gemm(a, batch, (hipStream_t)stream);
+}
+
+int msr_ns_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, size_t *bytes) {
+    if (!bytes || batch < 0 || rows <= 0 || cols <= 0) { set_error("msr_ns_workspace_bytes: bad arguments"); return MSR_ERR_ARG; }
+    *bytes = ns_layout(batch, rows, cols).total;
+    return MSR_OK;
+}
+
+int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows, int64_t cols, int32_t steps,
+                      float a_coef, float b_coef, float c_coef, void *workspace, size_t workspace_bytes,
+                      msr_stream_t stream) {
+    if (!in || !out || batch < 0 || rows <= 0 || cols <= 0 || steps < 0) { set_error("msr_newton_schulz: bad arguments"); return MSR_ERR_ARG; }
+    if (batch == 0) return MSR_OK;
+    const NSLayout L = ns_layout(batch, rows, cols);
+    if (!workspace || workspace_bytes < L.total) {
+        set_error("msr_newton_schulz: workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
+        return MSR_ERR_WORKSPACE;
+    }
+    if (L.mp > (1 << 30) || L.np > (1 << 30)) { set_error("msr_newton_schulz: matrix too large"); return MSR_ERR_ARG; }
+    hipStream_t s = (hipStream_t)stream;
+    char *ws = static_cast<char *>(workspace);
+    uint16_t *X[2] = {(uint16_t *)(ws + L.off_x[0]), (uint16_t *)(ws + L.off_x[1])};
+    uint16_t *XT[2] = {(uint16_t *)(ws + L.off_xt[0]), (uint16_t *)(ws + L.off_xt[1])};
+    uint16_t *A = (uint16_t *)(ws + L.off_a);
+    uint16_t *B = (uint16_t *)(ws + L.off_b);
+    float *part = (float *)(ws + L.off_part);
+    const int64_t numel = rows * cols;
+    const int64_t xs = L.mp * L.np, as = L.mp * L.mp;
+
+    hipLaunchKernelGGL(sumsq_kernel, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
+    int rc = check_launch("sumsq_kernel");
+    if (rc) return rc;
+
+    // Padded extents of the input layout: wide -> X is (mp x np); tall -> XT is (np x mp).
+    const int64_t Rp = L.transposed ? L.np : L.mp;
+    const int64_t Cp = L.transposed ? L.mp : L.np;
+    if (steps == 0) {
+        hipLaunchKernelGGL(normalize_kernel, dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch),
+                           dim3(256), 0, s, in, rows, cols, part, out, cols, numel, (uint16_t *)nullptr, (int64_t)0,
+                           (int64_t)0, rows, cols);
+        return check_launch("normalize_kernel");
+    }
+    uint16_t *Sx = L.transposed ? XT[0] : X[0];
+    uint16_t *Tx = L.transposed ? X[0] : XT[0];
+    const int64_t ldS = Cp, ldT = Rp;
+    hipLaunchKernelGGL(normalize_kernel, dim3((unsigned)(Cp / 64), (unsigned)(Rp / 64), (unsigned)batch), dim3(256), 0, s,
+                       in, rows, cols, part, Sx, ldS, xs, Tx, ldT, xs, Rp, Cp);
+    rc = check_launch("normalize_kernel");
+    if (rc) return rc;
+
+    const int mp = (int)L.mp, np = (int)L.np;
+    int cur = 0;
+    for (int it = 0; it < steps; ++it) {
+        const bool last = it == steps - 1;
+        GemmArgs g = {};
+        // A = X X^T
+        g.P = X[cur]; g.ldp = np; g.sP = xs;
+        g.Q = X[cur]; g.ldq = np; g.sQ = xs;
+        g.C = nullptr;
+        g.D = A; g.ldd = mp; g.sD = as;
+        g.DT = nullptr;
+        g.M = mp; g.N = mp; g.K = np; g.Mv = mp; g.Nv = mp;
+        g.alpha = 1.0f; g.beta = 0.0f; g.symmetric = 1;
+        if ((rc = launch_gemm(g, batch, s))) return rc;
+        // B = c (A A) + b A
+        g = GemmArgs{};
+        g.P = A; g.ldp = mp; g.sP = as;
+        g.Q = A; g.ldq = mp; g.sQ = as;
+        g.C = A; g.ldc = mp; g.sC = as;
+        g.D = B; g.ldd = mp; g.sD = as;
+        g.M = mp; g.N = mp; g.K = mp; g.Mv = mp; g.Nv = mp;
+        g.alpha = c_coef; g.beta = b_coef; g.symmetric = 1;
+        if ((rc = launch_gemm(g, batch, s))) return rc;
+        // X' = (B X) + a X
+        g = GemmArgs{};
+        g.P = B; g.ldp = mp; g.sP = as;
+        g.Q = XT[cur]; g.ldq = mp; g.sQ = xs;
+        g.C = X[cur]; g.ldc = np; g.sC = xs;
+        g.M = mp; g.N = np; g.K = mp;
+        g.alpha = 1.0f; g.beta = a_coef; g.symmetric = 0;
+        if (!last) {
+            g.D = X[cur ^ 1]; g.ldd = np; g.sD = xs;
+            g.DT = XT[cur ^ 1]; g.lddt = mp; g.sDT = xs;
+            g.Mv = mp; g.Nv = np;
+        } else if (!L.transposed) {
+            g.D = out; g.ldd = cols; g.sD = numel;  // out[m][n], m = rows, n = cols
+            g.DT = nullptr;
+            g.Mv = (int)L.m; g.Nv = (int)L.n;
+        } else {
+            g.D = nullptr;
+            g.DT = out; g.lddt = cols; g.sDT = numel;  // out[n][m], n = rows, m = cols
+            g.Mv = (int)L.m; g.Nv = (int)L.n;
+        }
+        if ((rc = launch_gemm(g, batch, s))) return rc;
+        cur ^= 1;
+    }
+    return MSR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,405 @@
+"""Muon with BF16 stochastic rounding on gfx950 (bf16 MFMA Newton-Schulz).
+
+Drop-in for ``muon_sr.triton_muon_sr`` (bab2min/muon_sr 0.1.2): the classes
+``TritonMuonSR`` and ``TritonMuonSRWithAuxAdam`` keep the reference's
+constructor signatures, param-group keys, state keys (``step``,
+``momentum_buffer``; ``ema``/``ema_squared`` for AdamW groups), seeds,
+shape-group order and checkpoint behaviour.
+
+One Muon step of a shape group runs three library calls:
+  prepare  momentum lerp + nesterov, SR store of the momentum stack, RNE bf16
+           update (grads read through a pointer table: no stack copy);
+  NS       batched Newton-Schulz on bf16 MFMA (msr_newton_schulz);
+  apply    p <- SR(p*(1-lr*wd) - lr*scale*update) for every matrix of a chunk.
+
+Extension (additive, off by default): an AdamW group of the hybrid optimizer
+with ``optim_bits=8`` runs the blockwise 8-bit AdamW of TritonAdamW8bit
+(keys ``block_size``/``min_8bit_size`` as there; state format v2).
+"""
+from __future__ import annotations
+
+from collections import defaultdict
+
+import torch
+from torch.optim import Optimizer
+
+from . import _lib
+from .adamw import _adamw_step
+from .adamw_8bit import adamw8bit_launch, init_8bit_state, TritonAdamW8bit
+
+NS_COEFFS = (3.4445, -4.7750, 2.0315)
+
+# Max elements per batched Newton-Schulz call (muon_sr/triton_muon_sr.py:123-125).
+# The library's Newton-Schulz is batch-invariant, so the chunking only bounds
+# the transient workspace; results do not depend on it.
+NS_CHUNK_NUMEL = 1 << 28
+
+
+def _restore_global_step(state, groups):
+    """`_global_step` of batch_ns groups from per-param steps (muon_sr/triton_muon_sr.py:13-15)."""
+    return max((state[p].get("step", 0) for g in groups for p in g["params"]), default=0)
+
+
+def _deterministic_seed(step, param_idx, salt=0):
+    """Seed from step + param index, identical on every data-parallel replica
+    (muon_sr/triton_muon_sr.py:83-85)."""
+    return (step * 2654435761 ^ param_idx * 1234567891 ^ salt) & 0xFFFFFFFF
+
+
+def _ns_scale(shape):
+    """sqrt(max(1, rows/cols)) (muon_sr/triton_muon_sr.py:101-102)."""
+    return max(1.0, shape[-2] / shape[-1]) ** 0.5
+
+
+def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
+    """Batched NS of a bf16 tensor [..., rows, cols] on the GPU; returns bf16 of the same shape.
+
+    Replaces ``_newton_schulz(G, steps, out_dtype=None)`` (muon_sr/muon_sr.py:82-98).
+    """
+    assert G.ndim >= 2
+    _lib.require_gpu(G, "newton_schulz", RuntimeError)
+    X = G.to(torch.bfloat16).contiguous()
+    rows, cols = X.shape[-2], X.shape[-1]
+    batch = X.numel() // (rows * cols) if X.numel() else 0
+    out = torch.empty_like(X)
+    if batch == 0:
+        return out
+    L = _lib.lib()
+    nbytes = _lib.ctypes.c_size_t(0)
+    _lib.check(L.msr_ns_workspace_bytes(batch, rows, cols, _lib.ctypes.byref(nbytes)), "msr_ns_workspace_bytes")
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=X.device)
+    a, b, c = NS_COEFFS
+    rc = L.msr_newton_schulz(X.data_ptr(), out.data_ptr(), batch, rows, cols, steps, a, b, c,
+                             ws.data_ptr(), nbytes.value, _lib.stream_of(X))
+    _lib.check(rc, "msr_newton_schulz")
+    return out
+
+
+def _bf16_contig(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        t = t.to(torch.bfloat16)
+    return t.contiguous()
+
+
+def _run_prepare(grads, buf_stack, out, beta, nesterov, seed):
+    """Momentum + nesterov for `len(grads)` matrices whose momenta are rows of
+    `buf_stack`; writes the bf16 pre-NS update rows into `out`
+    (muon_sr/triton_muon_sr.py:18-50, 88-98, 150-159)."""
+    n = grads[0].numel() if len(grads) else 0
+    table = _lib.ptr_array([g.data_ptr() for g in grads])
+    rc = _lib.lib().msr_muon_prepare(table, buf_stack.data_ptr(), out.data_ptr(), n, len(grads), beta,
+                                     int(bool(nesterov)), seed, _lib.noise_mode(), None, _lib.stream_of(buf_stack))
+    _lib.check(rc, "msr_muon_prepare")
+
+
+def _run_apply(params, upd_stack, lr, weight_decay, scale, seeds):
+    """Decay + update + SR store for every matrix of `params` (muon_sr/triton_muon_sr.py:53-80, 105-113)."""
+    n = params[0].numel()
+    table = _lib.ptr_array([p.data_ptr() for p in params])
+    seed_arr = _lib.ptr_array(seeds, _lib.ctypes.c_uint32)
+    rc = _lib.lib().msr_muon_apply(table, upd_stack.data_ptr(), n, len(params), lr, weight_decay, scale, seed_arr,
+                                   _lib.noise_mode(), None, _lib.stream_of(upd_stack))
+    _lib.check(rc, "msr_muon_apply")
+
+
+def _check_param(p, name):
+    _lib.require_gpu(p, name, RuntimeError)
+    if not p.is_contiguous():
+        raise RuntimeError(f"{name} requires contiguous parameters")
+
+
+def _muon_step(p, grad, buf, beta, nesterov, ns_steps, lr, weight_decay, step, param_idx):
+    """Single-param Muon step (muon_sr/triton_muon_sr.py:116-120)."""
+    grad = _bf16_contig(grad)
+    update = torch.empty(p.shape, dtype=torch.bfloat16, device=p.device)
+    _run_prepare([grad], buf, update, beta, nesterov, _deterministic_seed(step, param_idx, salt=0))
+    update_ns = newton_schulz(update, steps=ns_steps)
+    _run_apply([p.data], update_ns, lr, weight_decay, _ns_scale(update_ns.shape),
+               [_deterministic_seed(step, param_idx, salt=1)])
+
+
+def _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns_steps, lr, weight_decay, step):
+    """Shape-batched Muon step (muon_sr/triton_muon_sr.py:128-177).
+
+    Per shape group (first-occurrence order) with every gradient present: one
+    prepare over the whole momentum stack (seed salt 0, index shape_idx), then
+    NS + apply per chunk (seed salt 1, index shape_idx*10000 + i).  A group with
+    missing gradients falls back to per-parameter steps with index
+    shape_idx*10000 + i.
+    """
+    for shape_idx, (shape, grp_params) in enumerate(shape_groups.items()):
+        active = [p for p in grp_params if p.grad is not None]
+        if not active:
+            continue
+        stacked_buf = stacked_bufs[shape]
+        Na = len(active)
+        if Na == len(grp_params):
+            for p in active:
+                _check_param(p, "TritonMuonSR")
+            ordered = sorted(active, key=lambda q: buf_indices[id(q)])
+            grads = [_bf16_contig(p.grad) for p in ordered]
+            work = torch.empty(Na, *shape, dtype=torch.bfloat16, device=active[0].device)
+            _run_prepare(grads, stacked_buf, work, beta, nesterov, _deterministic_seed(step, shape_idx, salt=0))
+            del grads
+            k = max(1, NS_CHUNK_NUMEL // work[0].numel())
+            scale = _ns_scale(shape)
+            for start in range(0, Na, k):
+                update_ns = newton_schulz(work[start:start + k], steps=ns_steps)
+                chunk = ordered[start:start + k]
+                seeds = [_deterministic_seed(step, shape_idx * 10000 + start + j, salt=1) for j in range(len(chunk))]
+                _run_apply([p.data for p in chunk], update_ns, lr, weight_decay, scale, seeds)
+                del update_ns
+            del work
+        else:
+            for p in active:
+                _check_param(p, "TritonMuonSR")
+                idx = buf_indices[id(p)]
+                _muon_step(p, p.grad, stacked_buf[idx], beta, nesterov, ns_steps, lr, weight_decay, step,
+                           shape_idx * 10000 + idx)
+
+
+def _init_stacked_bufs(params, device, state):
+    """Stacked BF16 momentum buffers per parameter shape (muon_sr/muon_sr.py:112-146).
+
+    ``state[p]["momentum_buffer"]`` becomes a view of row i of its shape's
+    stack; a momentum already in ``state`` (e.g. from load_state_dict) is
+    copied into the stack.  Returns (shape_groups, stacked_bufs, buf_indices).
+    """
+    shape_groups = defaultdict(list)
+    for p in params:
+        shape_groups[p.shape].append(p)
+    stacked_bufs = {}
+    buf_indices = {}
+    for shape, grp in shape_groups.items():
+        stacked = torch.zeros(len(grp), *shape, dtype=torch.bfloat16, device=device)
+        for i, p in enumerate(grp):
+            buf_indices[id(p)] = i
+            p_state = state[p]
+            if "momentum_buffer" in p_state:
+                stacked[i].copy_(p_state["momentum_buffer"])
+            p_state["momentum_buffer"] = stacked[i]
+        stacked_bufs[shape] = stacked
+    return dict(shape_groups), stacked_bufs, buf_indices
+
+
+class _StackedBufsMixin:
+    """Makes batch_ns optimizers resumable: the stacks and the global step live
+    outside ``self.state`` and are rebuilt on the next step (muon_sr/muon_sr.py:149-158)."""
+
+    def load_state_dict(self, state_dict):
+        super().load_state_dict(state_dict)
+        self._batch_state = {}
+        self.__dict__.pop("_global_step", None)
+
+
+class TritonMuonSR(_StackedBufsMixin, Optimizer):
+    r"""
+    Muon with BF16 stochastic rounding (drop-in for SingleDeviceMuon).
+
+    Only for hidden weight matrices (ndim >= 2). For embeddings, heads, biases
+    and gains use a separate optimizer (e.g. TritonAdamW).
+
+    Arguments:
+        params: ndim >= 2 parameters to optimize
+        lr (float): learning rate (default: 0.02)
+        weight_decay (float): weight decay (default: 0)
+        momentum (float): momentum coefficient (default: 0.95)
+        nesterov (bool): Nesterov momentum (default: True)
+        ns_steps (int): Newton-Schulz iterations (default: 5)
+        batch_ns (bool): stacked momentum buffers, NS batched by shape (default: False)
+
+    Mirrors muon_sr/triton_muon_sr.py:180-255.
+    """
+
+    def __init__(self, params, lr=0.02, weight_decay=0, momentum=0.95, nesterov=True, ns_steps=5, batch_ns=False):
+        defaults = dict(lr=lr, weight_decay=weight_decay, momentum=momentum, nesterov=nesterov,
+                        ns_steps=ns_steps, batch_ns=batch_ns)
+        super().__init__(params, defaults)
+        self._batch_state = {}
+
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            loss = closure()
+
+        for group in self.param_groups:
+            lr = group["lr"]
+            weight_decay = group["weight_decay"]
+            beta = group["momentum"]
+            nesterov = group["nesterov"]
+            ns_steps = group["ns_steps"]
+
+            if group["batch_ns"]:
+                gid = id(group)
+                if gid not in self._batch_state:
+                    device = group["params"][0].device
+                    self._batch_state[gid] = _init_stacked_bufs(group["params"], device, self.state)
+                shape_groups, stacked_bufs, buf_indices = self._batch_state[gid]
+
+                for p in group["params"]:
+                    assert p.dtype == torch.bfloat16, "only bfloat16 is supported."
+                    if p.grad is not None and p.grad.is_sparse:
+                        raise RuntimeError("TritonMuonSR does not support sparse gradients")
+
+                if not hasattr(self, "_global_step"):
+                    self._global_step = _restore_global_step(
+                        self.state, [g for g in self.param_groups if g["batch_ns"]])
+                self._global_step += 1
+                for p in group["params"]:
+                    self.state[p]["step"] = self._global_step
+                _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns_steps, lr,
+                                 weight_decay, self._global_step)
+            else:
+                for param_idx, p in enumerate(group["params"]):
+                    assert p.dtype == torch.bfloat16, "only bfloat16 is supported."
+                    if p.grad is None:
+                        continue
+                    if p.grad.is_sparse:
+                        raise RuntimeError("TritonMuonSR does not support sparse gradients")
+                    _check_param(p, "TritonMuonSR")
+                    state = self.state[p]
+                    if len(state) == 0:
+                        state["step"] = 0
+                        state["momentum_buffer"] = torch.zeros_like(p, dtype=torch.bfloat16,
+                                                                    memory_format=torch.contiguous_format)
+                    state["step"] += 1
+                    _muon_step(p, p.grad, state["momentum_buffer"], beta, nesterov, ns_steps, lr, weight_decay,
+                               state["step"], param_idx)
+
+        return loss
+
+
+class TritonMuonSRWithAuxAdam(_StackedBufsMixin, Optimizer):
+    r"""
+    Muon (use_muon=True groups) plus AdamW (use_muon=False groups) with BF16
+    stochastic rounding (drop-in for SingleDeviceMuonWithAuxAdam).
+
+    Arguments:
+        param_groups: list of param group dicts with a 'use_muon' flag
+        batch_ns (bool): stacked momentum buffers, NS batched by shape (default: False)
+
+    AdamW groups use bf16 moments in PyTorch order (as the reference).  An
+    AdamW group with ``optim_bits=8`` instead uses the blockwise 8-bit states of
+    TritonAdamW8bit (``block_size`` 256, ``min_8bit_size`` 4096 by default).
+
+    Mirrors muon_sr/triton_muon_sr.py:258-373.
+    """
+
+    def __init__(self, param_groups, batch_ns=False):
+        for group in param_groups:
+            assert "use_muon" in group
+            if group["use_muon"]:
+                group.setdefault("lr", 0.02)
+                group.setdefault("momentum", 0.95)
+                group.setdefault("nesterov", True)
+                group.setdefault("ns_steps", 5)
+                group.setdefault("weight_decay", 0)
+            else:
+                group.setdefault("lr", 3e-4)
+                group.setdefault("betas", (0.9, 0.95))
+                group.setdefault("eps", 1e-10)
+                group.setdefault("weight_decay", 0)
+                if group.get("optim_bits", 16) == 8:
+                    group.setdefault("block_size", 256)
+                    group.setdefault("min_8bit_size", 4096)
+                    TritonAdamW8bit._validate_group(group)
+        self.batch_ns = batch_ns
+        self._batch_state = {}
+        self._maps = {}
+        super().__init__(param_groups, {})
+
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            loss = closure()
+
+        param_offset = 0
+        for group in self.param_groups:
+            group_offset = param_offset
+            param_offset += len(group["params"])
+            if group["use_muon"]:
+                lr = group["lr"]
+                weight_decay = group["weight_decay"]
+                beta = group["momentum"]
+                nesterov = group["nesterov"]
+                ns_steps = group["ns_steps"]
+
+                if group["params"]:
+                    if self.batch_ns:
+                        gid = id(group)
+                        if gid not in self._batch_state:
+                            device = group["params"][0].device
+                            self._batch_state[gid] = _init_stacked_bufs(group["params"], device, self.state)
+                        shape_groups, stacked_bufs, buf_indices = self._batch_state[gid]
+
+                        for p in group["params"]:
+                            assert p.dtype == torch.bfloat16, "only bfloat16 is supported."
+                            if p.grad is not None and p.grad.is_sparse:
+                                raise RuntimeError("TritonMuonSRWithAuxAdam does not support sparse gradients")
+
+                        if not hasattr(self, "_global_step"):
+                            self._global_step = _restore_global_step(
+                                self.state, [g for g in self.param_groups if g["use_muon"]])
+                        self._global_step += 1
+                        for p in group["params"]:
+                            self.state[p]["step"] = self._global_step
+                        _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns_steps, lr,
+                                         weight_decay, self._global_step)
+                    else:
+                        for param_idx, p in enumerate(group["params"]):
+                            assert p.dtype == torch.bfloat16, "only bfloat16 is supported."
+                            if p.grad is None:
+                                continue
+                            if p.grad.is_sparse:
+                                raise RuntimeError("TritonMuonSRWithAuxAdam does not support sparse gradients")
+                            _check_param(p, "TritonMuonSRWithAuxAdam")
+                            state = self.state[p]
+                            if len(state) == 0:
+                                state["step"] = 0
+                                state["momentum_buffer"] = torch.zeros_like(p, dtype=torch.bfloat16,
+                                                                            memory_format=torch.contiguous_format)
+                            state["step"] += 1
+                            _muon_step(p, p.grad, state["momentum_buffer"], beta, nesterov, ns_steps, lr,
+                                       weight_decay, state["step"], param_idx)
+            else:
+                lr = group["lr"]
+                beta1, beta2 = group["betas"]
+                eps = group["eps"]
+                weight_decay = group["weight_decay"]
+                eight_bit = group.get("optim_bits", 16) == 8
+
+                for i, p in enumerate(group["params"]):
+                    assert p.dtype == torch.bfloat16, "only bfloat16 is supported."
+                    if p.grad is None:
+                        continue
+                    if p.grad.is_sparse:
+                        raise RuntimeError("TritonMuonSRWithAuxAdam does not support sparse gradients")
+                    state = self.state[p]
+                    if eight_bit:
+                        self._step_8bit(p, group, state, lr, beta1, beta2, eps, weight_decay, group_offset + i)
+                        continue
+                    if len(state) == 0:
+                        state["step"] = 0
+                        state["ema"] = torch.zeros_like(p, dtype=torch.bfloat16, memory_format=torch.contiguous_format)
+                        state["ema_squared"] = torch.zeros_like(p, dtype=torch.bfloat16,
+                                                                memory_format=torch.contiguous_format)
+                    state["step"] += 1
+                    _adamw_step(p=p.data, g=p.grad, ema=state["ema"], ema_sq=state["ema_squared"],
+                                lr=lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay,
+                                step=state["step"], param_idx=group_offset + i)
+
+        return loss
+
+    def _step_8bit(self, p, group, state, lr, beta1, beta2, eps, weight_decay, param_index):
+        """8-bit AdamW group step: the TritonAdamW8bit update with seed index group_offset + i."""
+        _lib.require_gpu(p, "TritonMuonSRWithAuxAdam", ValueError)
+        g = p.grad
+        if not p.is_contiguous() or not g.is_contiguous():
+            raise ValueError("Parameters/gradients must be contiguous and dense")
+        if not p.numel():
+            return
+        if not state:
+            state.update(init_8bit_state(p, group["block_size"], 8, group["min_8bit_size"], self._maps))
+        state["step"] += 1
+        seed = (state["step"] * 2654435761 ^ param_index * 1234567891) & 0xFFFFFFFF
+        adamw8bit_launch(p.data, g, state, lr, beta1, beta2, eps, weight_decay, seed)

@@ -1,0 +1,62 @@
+"""CPU checks of the C ABI: the library loads and exports every declared symbol.
+
+No kernel is launched (no GPU here); argument validation paths that return
+before any HIP call are exercised.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "muon_sr_amd.h")
+LIB = os.path.join(ROOT, "muon_sr_amd", "libmuon_sr_amd.so")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(msr_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} is not built; run __graft_entry__.build()")
+    from muon_sr_amd import _lib
+    return _lib.lib()
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for s in ("msr_sr_accum", "msr_adamw8bit_step", "msr_adamw_bf16_step", "msr_muon_prepare", "msr_muon_apply",
+              "msr_newton_schulz", "msr_ns_workspace_bytes", "msr_last_error", "msr_version"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(LIB)
+    for s in declared_symbols():
+        assert hasattr(raw, s), s
+
+
+def test_python_signatures_cover_header(lib):
+    from muon_sr_amd import _lib
+    assert sorted(_lib.SIGNATURES) == declared_symbols()
+
+
+def test_argument_validation_without_gpu(lib):
+    assert lib.msr_version() >= 100
+    # bad block size / negative sizes / bad noise mode are rejected before any HIP call
+    rc = lib.msr_adamw8bit_step(1, 1, 1, 1, 1, 1, 1, 1, 100, 48, 1, 1e-3, 0.9, 0.99, 1e-8, 0.0, 0.1, 0.01, 0, 1,
+                                None, None)
+    assert rc == 1001 and b"block" in lib.msr_last_error()
+    assert lib.msr_sr_accum(None, None, 0, -1, 0, 0, 1, None, None) == 1001
+    assert lib.msr_sr_accum(1, 1, 0, 10, 0, 0, 7, None, None) == 1001
+    assert lib.msr_sr_accum(1, 1, 0, 10, 0, 0, 2, None, None) == 1001   # INJECT without a buffer
+    size = ctypes.c_size_t(0)
+    assert lib.msr_ns_workspace_bytes(2, 100, 60, ctypes.byref(size)) == 0
+    # two 256x256-padded X layouts x2 (ping-pong) + A + B, bf16, plus partial sums
+    assert size.value >= 2 * (4 * 256 * 256 * 2 + 2 * 256 * 256 * 2)
+    assert lib.msr_newton_schulz(1, 1, 1, 300, 300, 5, 1.0, 1.0, 1.0, 1, 16, None) == 1004
+    assert lib.msr_gemm_nt(1, 64, 0, 1, 64, 0, None, 0, 0, 1, 256, 0, 255, 256, 64, 1, 1.0, 0.0, None) == 1001

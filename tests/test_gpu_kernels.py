@@ -1,0 +1,398 @@
+"""GPU parity tests: each kernel through the C ABI against the CPU oracle.
+
+Bar: bit-exact for every stochastic-rounding kernel (same noise bits: injected,
+the reference's Philox word-0 stream, or this library's Philox8 stream, all of
+which the oracle also produces), bit-exact quantizer codes and block scales;
+Newton-Schulz within 1e-2 relative Frobenius of an fp32 emulation of the same
+bf16-storage op.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from _gpu import DEV, check, dev_to_u16, need_gpu, np_to_dev, ptr, ptr_array, rel_fro, stream, u16_to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def L():
+    return need_gpu()
+
+
+def rng_bf16(rng, n, std):
+    return O.f32_to_bf16_rne((rng.standard_normal(n) * std).astype(np.float32))
+
+
+def unaligned(t):
+    """A view of t starting one element in (breaks 16-byte alignment)."""
+    big = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    v = big[1:]
+    v.copy_(t.flatten())
+    return v
+
+
+# ---------------------------------------------------------------------------
+# RNG
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("mode", [O.NOISE_TRITON, O.NOISE_PHILOX8])
+def test_noise_streams_match_oracle(L, mode):
+    n = 4096
+    for seed, k in [(12345, 0), (0x7FFFFFFF, 1), (0x7FFFFFFE, 2), (0xFFFFFFFF, 2), (0xDEADBEEF, 0)]:
+        for off0 in (0, 2**31 - 100, 2**32 - 50, 2**40 + 8):
+            out = torch.empty(n, dtype=torch.int16, device=DEV)
+            check(L, L.msr_noise_fill(out.data_ptr(), n, off0, seed, k, mode, stream()), "noise_fill")
+            got = out.cpu().numpy().view(np.uint16)
+            exp = O.noise16(mode, seed, np.arange(off0, off0 + n, dtype=np.int64), k)
+            assert np.array_equal(got, exp), (mode, seed, k, off0)
+
+
+# ---------------------------------------------------------------------------
+# (c) SR accumulate
+# ---------------------------------------------------------------------------
+
+def test_sr_accum_reference_vectors(L, golden):
+    z = golden("elementwise")
+    acc = u16_to_dev(z["accum/in_acc"])
+    g = u16_to_dev(z["accum/in_g"])
+    check(L, L.msr_sr_accum(acc.data_ptr(), g.data_ptr(), 0, acc.numel(), 777, 0, O.NOISE_TRITON, None, stream()))
+    assert np.array_equal(dev_to_u16(acc), z["accum/out_bf16g"])
+    acc = u16_to_dev(z["accum/in_acc"])
+    g32 = np_to_dev(z["accum/in_g32"])
+    check(L, L.msr_sr_accum(acc.data_ptr(), g32.data_ptr(), 1, acc.numel(), 0x9E3779B9, 0, O.NOISE_TRITON, None,
+                            stream()))
+    assert np.array_equal(dev_to_u16(acc), z["accum/out_f32g"])
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 1000, 4099, 65536 + 13])
+@pytest.mark.parametrize("mode", [O.NOISE_TRITON, O.NOISE_PHILOX8, O.NOISE_INJECT])
+def test_sr_accum_vs_oracle(L, n, mode):
+    rng = np.random.default_rng(n * 7 + mode)
+    acc0 = rng_bf16(rng, n, 1e-3)
+    g16 = rng_bf16(rng, n, 1e-4)
+    g32 = (rng.standard_normal(n) * 1e-4).astype(np.float32)
+    inj = rng.integers(0, 65536, n).astype(np.uint16)
+    seed = int(rng.integers(0, 2**32))
+    spec = O.NoiseSpec(mode, seed, 0, inj if mode == O.NOISE_INJECT else None)
+    inj_d = np_to_dev(inj.view(np.int16)) if mode == O.NOISE_INJECT else None
+    for gname, gnp in (("bf16", g16), ("f32", g32)):
+        for zero in (0, 1):
+            for misalign in (False, True):
+                acc = u16_to_dev(acc0)
+                g = u16_to_dev(gnp) if gname == "bf16" else np_to_dev(gnp)
+                if misalign:
+                    acc, g = unaligned(acc), unaligned(g)
+                check(L, L.msr_sr_accum(acc.data_ptr(), g.data_ptr(), int(gname == "f32"), n, seed, zero, mode,
+                                        ptr(inj_d), stream()))
+                start = np.zeros(n, np.uint16) if zero else acc0
+                exp = O.sr_accum(start, gnp, spec)
+                assert np.array_equal(dev_to_u16(acc), exp), (gname, zero, misalign)
+
+
+# ---------------------------------------------------------------------------
+# BF16-moment AdamW
+# ---------------------------------------------------------------------------
+
+def test_adamw_bf16_reference_vectors(L, golden):
+    z = golden("elementwise")
+    for tag in ("s_small", "s_wrap", "s_wrap2", "s_u32", "s_i64wrap"):
+        k = lambda s: z[f"adamw/{tag}/{s}"]  # noqa: E731
+        lr, b1, b2, eps, wd, bc, bcs = (float(v) for v in k("hyper"))
+        p, g, e, s = (u16_to_dev(k(x)) for x in ("in_p", "in_g", "in_e", "in_s"))
+        check(L, L.msr_adamw_bf16_step(p.data_ptr(), g.data_ptr(), e.data_ptr(), s.data_ptr(), p.numel(),
+                                       lr, b1, b2, eps, wd, bc, bcs, int(k("seed")), O.NOISE_TRITON, None, stream()))
+        assert np.array_equal(dev_to_u16(p), k("out_p")), tag
+        assert np.array_equal(dev_to_u16(e), k("out_e")), tag
+        assert np.array_equal(dev_to_u16(s), k("out_s")), tag
+
+
+@pytest.mark.parametrize("mode", [O.NOISE_PHILOX8, O.NOISE_INJECT, O.NOISE_TRITON])
+@pytest.mark.parametrize("misalign", [False, True])
+def test_adamw_bf16_vs_oracle(L, mode, misalign):
+    rng = np.random.default_rng(11 + mode)
+    n = 5003
+    p0, g0, e0 = rng_bf16(rng, n, 0.02), rng_bf16(rng, n, 1e-3), rng_bf16(rng, n, 1e-4)
+    s0 = O.f32_to_bf16_rne((rng.standard_normal(n) * 1e-4).astype(np.float32) ** 2)
+    inj = rng.integers(0, 65536, 3 * n).astype(np.uint16)
+    seed = 0x7FFFFFFE
+    lr, b1, b2, eps, wd = 1e-3, 0.9, 0.999, 1e-8, 0.01
+    bc, bcs = O.adamw_bias_corrections(b1, b2, 7)
+    specs = [O.NoiseSpec(mode, seed, k, inj[k * n:(k + 1) * n] if mode == O.NOISE_INJECT else None) for k in range(3)]
+    ep, ee, es = O.adamw_bf16(p0, g0, e0, s0, lr, b1, b2, eps, wd, bc, bcs, specs[0], specs[1], specs[2])
+    p, g, e, s = (u16_to_dev(x) for x in (p0, g0, e0, s0))
+    if misalign:
+        p, g, e, s = (unaligned(x) for x in (p, g, e, s))
+    inj_d = np_to_dev(inj.view(np.int16)) if mode == O.NOISE_INJECT else None
+    check(L, L.msr_adamw_bf16_step(p.data_ptr(), g.data_ptr(), e.data_ptr(), s.data_ptr(), n, lr, b1, b2, eps, wd,
+                                   bc, bcs, seed, mode, ptr(inj_d), stream()))
+    assert np.array_equal(dev_to_u16(p), ep)
+    assert np.array_equal(dev_to_u16(e), ee)
+    assert np.array_equal(dev_to_u16(s), es)
+
+
+# ---------------------------------------------------------------------------
+# (a) 8-bit AdamW
+# ---------------------------------------------------------------------------
+
+def _adam8_call(L, p, g, s1, s2, a1, a2, q1, q2, n, block, quant, hyper, seed, mode, inj=None):
+    lr, b1, b2, eps, wd, bc1, bc2 = hyper
+    check(L, L.msr_adamw8bit_step(p.data_ptr(), g.data_ptr(), s1.data_ptr(), s2.data_ptr(), ptr(a1), ptr(a2),
+                                  ptr(q1), ptr(q2), n, block, int(quant), lr, b1, b2, eps, wd, bc1, bc2, seed, mode,
+                                  ptr(inj), stream()), "adamw8bit")
+
+
+def test_adamw8bit_reference_vectors(L, golden):
+    z = golden("adamw8bit")
+    q1 = np_to_dev(O.create_dynamic_map(True))
+    q2 = np_to_dev(O.create_dynamic_map(False))
+    names = sorted({k.split("/")[0] for k in z.files})
+    for name in names:
+        k = lambda s: z[f"{name}/{s}"]  # noqa: E731
+        quant = bool(k("quantized"))
+        n, block = int(k("n")), int(k("block"))
+        lr, b1, b2, eps, wd = (float(k(x)) for x in ("lr", "b1", "b2", "eps", "wd"))
+        p = u16_to_dev(k("p0"))
+        if quant:
+            s1, s2 = np_to_dev(k("s1_0")), np_to_dev(k("s2_0"))
+            a1, a2 = np_to_dev(k("a1_0")), np_to_dev(k("a2_0"))
+        else:
+            s1, s2 = u16_to_dev(k("s1_0")), u16_to_dev(k("s2_0"))
+            a1 = a2 = None
+        for step in range(1, int(k("steps")) + 1):
+            g = u16_to_dev(k(f"g_{step}"))
+            hyper = (lr, b1, b2, eps, wd, 1 - b1 ** step, 1 - b2 ** step)
+            _adam8_call(L, p, g, s1, s2, a1, a2, q1 if quant else None, q2 if quant else None, n, block, quant,
+                        hyper, int(k(f"seed_{step}")), O.NOISE_TRITON)
+            assert np.array_equal(dev_to_u16(p), k(f"p_{step}")), (name, step)
+            if quant:
+                assert np.array_equal(s1.cpu().numpy(), k(f"s1_{step}")), (name, step)
+                assert np.array_equal(s2.cpu().numpy(), k(f"s2_{step}")), (name, step)
+                assert np.array_equal(a1.cpu().numpy().view(np.uint32), k(f"a1_{step}").view(np.uint32)), (name, step)
+                assert np.array_equal(a2.cpu().numpy().view(np.uint32), k(f"a2_{step}").view(np.uint32)), (name, step)
+            else:
+                assert np.array_equal(dev_to_u16(s1), k(f"s1_{step}")), (name, step)
+                assert np.array_equal(dev_to_u16(s2), k(f"s2_{step}")), (name, step)
+
+
+@pytest.mark.parametrize("block", [32, 64, 128, 256, 512, 1024, 2048, 4096])
+@pytest.mark.parametrize("mode", [O.NOISE_PHILOX8, O.NOISE_INJECT])
+def test_adamw8bit_blocks_vs_oracle(L, block, mode):
+    rng = np.random.default_rng(block + mode)
+    n = 5 * block + 77
+    nb = (n + block - 1) // block
+    Q1, Q2 = O.create_dynamic_map(True), O.create_dynamic_map(False)
+    q1, q2 = np_to_dev(Q1), np_to_dev(Q2)
+    p0 = rng_bf16(rng, n, 0.02)
+    s1 = np.full(n, 127, np.uint8)
+    s2 = np.zeros(n, np.uint8)
+    a1 = np.zeros(nb, np.float32)
+    a2 = np.zeros(nb, np.float32)
+    pd, s1d, s2d, a1d, a2d = u16_to_dev(p0), np_to_dev(s1), np_to_dev(s2), np_to_dev(a1), np_to_dev(a2)
+    pe = p0
+    lr, b1, b2, eps, wd = 3e-4, 0.9, 0.95, 1e-10, 0.01
+    for step in range(1, 4):
+        g0 = rng_bf16(rng, n, 1e-3)
+        if step == 1:
+            g0[block:2 * block] = 0          # all-zero block
+        if step == 2:
+            g0[[3, n - 1]] = [0x7FC0, 0xFF80]  # NaN, -inf
+        inj = rng.integers(0, 65536, 3 * n).astype(np.uint16)
+        seed = int(rng.integers(0, 2**32))
+        hyper = (lr, b1, b2, eps, wd, 1 - b1 ** step, 1 - b2 ** step)
+        spec = O.NoiseSpec(mode, seed, 0, inj[:n] if mode == O.NOISE_INJECT else None)
+        pe, s1, s2, a1, a2 = O.adamw8bit(pe, g0, s1, s2, a1, a2, Q1, Q2, block, True, *hyper, spec)
+        inj_d = np_to_dev(inj.view(np.int16)) if mode == O.NOISE_INJECT else None
+        _adam8_call(L, pd, u16_to_dev(g0), s1d, s2d, a1d, a2d, q1, q2, n, block, True, hyper, seed, mode, inj_d)
+        assert np.array_equal(dev_to_u16(pd), pe), step
+        assert np.array_equal(s1d.cpu().numpy(), s1), step
+        assert np.array_equal(s2d.cpu().numpy(), s2), step
+        assert np.array_equal(a1d.cpu().numpy().view(np.uint32), a1.view(np.uint32)), step
+        assert np.array_equal(a2d.cpu().numpy().view(np.uint32), a2.view(np.uint32)), step
+
+
+@pytest.mark.parametrize("mode", [O.NOISE_TRITON, O.NOISE_PHILOX8])
+def test_adamw8bit_unaligned_and_bf16_branch(L, mode):
+    rng = np.random.default_rng(5)
+    n, block = 3000, 256
+    Q1, Q2 = O.create_dynamic_map(True), O.create_dynamic_map(False)
+    p0, g0 = rng_bf16(rng, n, 0.02), rng_bf16(rng, n, 1e-3)
+    nb = (n + block - 1) // block
+    hyper = (1e-3, 0.9, 0.999, 1e-8, 0.1, 0.1, 0.001)
+    seed = 0x7FFFFFFF
+    # quantized state, parameter and gradient views not 16-byte aligned
+    pe, e1, e2, ea1, ea2 = O.adamw8bit(p0, g0, np.full(n, 127, np.uint8), np.zeros(n, np.uint8),
+                                       np.zeros(nb, np.float32), np.zeros(nb, np.float32), Q1, Q2, block, True,
+                                       *hyper, O.NoiseSpec(mode, seed))
+    p, g = unaligned(u16_to_dev(p0)), unaligned(u16_to_dev(g0))
+    s1, s2 = np_to_dev(np.full(n, 127, np.uint8)), np_to_dev(np.zeros(n, np.uint8))
+    a1, a2 = np_to_dev(np.zeros(nb, np.float32)), np_to_dev(np.zeros(nb, np.float32))
+    _adam8_call(L, p, g, s1, s2, a1, a2, np_to_dev(Q1), np_to_dev(Q2), n, block, True, hyper, seed, mode)
+    assert np.array_equal(dev_to_u16(p), pe)
+    assert np.array_equal(s1.cpu().numpy(), e1) and np.array_equal(s2.cpu().numpy(), e2)
+    # bf16-moment branch (seed streams SEED, SEED+1 (wraps the i32 seed), SEED+2)
+    m0, v0 = rng_bf16(rng, n, 1e-4), O.f32_to_bf16_rne((rng.standard_normal(n) * 1e-4).astype(np.float32) ** 2)
+    pe, me, ve = O.adamw8bit(p0, g0, m0, v0, None, None, None, None, block, False, *hyper,
+                             O.NoiseSpec(mode, seed), O.NoiseSpec(mode, seed, 1), O.NoiseSpec(mode, seed, 2))
+    p, g, m, v = (u16_to_dev(x) for x in (p0, g0, m0, v0))
+    _adam8_call(L, p, g, m, v, None, None, None, None, n, block, False, hyper, seed, mode)
+    assert np.array_equal(dev_to_u16(p), pe)
+    assert np.array_equal(dev_to_u16(m), me)
+    assert np.array_equal(dev_to_u16(v), ve)
+
+
+def test_quantizer_device_vs_oracle(L, golden):
+    z = golden("quantize")
+    rng = np.random.default_rng(9)
+    for signed in (True, False):
+        Q = O.create_dynamic_map(signed)
+        name = "signed" if signed else "unsigned"
+        lo = -1.0 if signed else 0.0
+        x = np.concatenate([z[f"x_{name}"], rng.uniform(lo, 1, 1 << 20).astype(np.float32),
+                            (10.0 ** rng.uniform(-12, 0, 1 << 20)).astype(np.float32)
+                            * (rng.choice([-1, 1], 1 << 20) if signed else 1)]).astype(np.float32)
+        xd = np_to_dev(x)
+        out = torch.empty(x.size, dtype=torch.uint8, device=DEV)
+        check(L, L.msr_quantize(xd.data_ptr(), out.data_ptr(), x.size, np_to_dev(Q).data_ptr(), int(signed), stream()))
+        got = out.cpu().numpy()
+        assert np.array_equal(got[:z[f"x_{name}"].size], z[f"code_{name}"])
+        assert np.array_equal(got, O.quantize(x, Q, signed))
+
+
+# ---------------------------------------------------------------------------
+# (b) Muon prepare / apply
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("nest", [1, 0])
+def test_muon_prepare_reference_vectors(L, golden, nest):
+    z = golden("elementwise")
+    k = lambda s: z[f"prepare/{nest}/{s}"]  # noqa: E731
+    g, buf = u16_to_dev(k("in_g")), u16_to_dev(k("in_buf"))
+    out = torch.empty_like(buf)
+    tbl = ptr_array([g.data_ptr()])
+    check(L, L.msr_muon_prepare(tbl, buf.data_ptr(), out.data_ptr(), g.numel(), 1, 0.95, nest, int(k("seed")),
+                                O.NOISE_TRITON, None, stream()))
+    assert np.array_equal(dev_to_u16(buf), k("out_buf"))
+    rne = torch.from_numpy(k("out_upd_f32")).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(dev_to_u16(out), rne)
+
+
+@pytest.mark.parametrize("rows,cols", [(33, 65), (64, 128)])
+@pytest.mark.parametrize("mode", [O.NOISE_TRITON, O.NOISE_PHILOX8, O.NOISE_INJECT])
+def test_muon_prepare_stack_vs_oracle(L, rows, cols, mode):
+    rng = np.random.default_rng(rows + mode)
+    count, numel = 5, rows * cols
+    grads = [rng_bf16(rng, numel, 1e-3) for _ in range(count)]
+    buf0 = rng_bf16(rng, count * numel, 1e-3)
+    inj = rng.integers(0, 65536, count * numel).astype(np.uint16)
+    seed = 0xFFFFFFF0
+    spec = O.NoiseSpec(mode, seed, 0, inj if mode == O.NOISE_INJECT else None)
+    eb, _, eu = O.muon_prepare(np.concatenate(grads), buf0, 0.95, True, spec)
+    gd = [u16_to_dev(g) for g in grads]
+    buf = u16_to_dev(buf0)
+    out = torch.empty_like(buf)
+    inj_d = np_to_dev(inj.view(np.int16)) if mode == O.NOISE_INJECT else None
+    check(L, L.msr_muon_prepare(ptr_array([t.data_ptr() for t in gd]), buf.data_ptr(), out.data_ptr(), numel, count,
+                                0.95, 1, seed, mode, ptr(inj_d), stream()))
+    assert np.array_equal(dev_to_u16(buf), eb)
+    assert np.array_equal(dev_to_u16(out), eu)
+
+
+def test_muon_apply_reference_vectors(L, golden):
+    z = golden("elementwise")
+    p, u = u16_to_dev(z["apply/in_p"]), u16_to_dev(z["apply/in_u"])
+    seeds = ptr_array([int(z["apply/seed"])], __import__("ctypes").c_uint32)
+    check(L, L.msr_muon_apply(ptr_array([p.data_ptr()]), u.data_ptr(), p.numel(), 1, 0.02, 0.01,
+                              float(z["apply/scale"]), seeds, O.NOISE_TRITON, None, stream()))
+    assert np.array_equal(dev_to_u16(p), z["apply/out_p"])
+
+
+@pytest.mark.parametrize("mode", [O.NOISE_TRITON, O.NOISE_PHILOX8, O.NOISE_INJECT])
+def test_muon_apply_multi_vs_oracle(L, mode):
+    import ctypes
+    rng = np.random.default_rng(3 + mode)
+    count, numel = 4, 37 * 41
+    ps = [rng_bf16(rng, numel, 0.02) for _ in range(count)]
+    upd = rng_bf16(rng, count * numel, 0.05)
+    seeds = [int(s) for s in rng.integers(0, 2**32, count)]
+    inj = rng.integers(0, 65536, count * numel).astype(np.uint16)
+    pd = [u16_to_dev(p) for p in ps]
+    ud = u16_to_dev(upd)
+    inj_d = np_to_dev(inj.view(np.int16)) if mode == O.NOISE_INJECT else None
+    check(L, L.msr_muon_apply(ptr_array([t.data_ptr() for t in pd]), ud.data_ptr(), numel, count, 0.02, 0.01, 1.6583,
+                              ptr_array(seeds, ctypes.c_uint32), mode, ptr(inj_d), stream()))
+    for i in range(count):
+        spec = O.NoiseSpec(mode, seeds[i], 0, inj[i * numel:(i + 1) * numel] if mode == O.NOISE_INJECT else None)
+        exp = O.muon_apply(ps[i], upd[i * numel:(i + 1) * numel], 0.02, 0.01, 1.6583, spec)
+        assert np.array_equal(dev_to_u16(pd[i]), exp), i
+
+
+# ---------------------------------------------------------------------------
+# (b) MFMA GEMM and Newton-Schulz
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M,N,K,batch,alpha,beta", [(256, 256, 64, 1, 1.0, 0.0), (512, 768, 320, 2, 0.5, -1.25),
+                                                    (256, 512, 1024, 3, 2.0315, -4.775)])
+def test_gemm_nt_vs_torch_fp32(L, M, N, K, batch, alpha, beta):
+    torch.manual_seed(M + N + K)
+    P = torch.randn(batch, M, K, device=DEV).to(torch.bfloat16)
+    Q = torch.randn(batch, N, K, device=DEV).to(torch.bfloat16)
+    C = torch.randn(batch, M, N, device=DEV).to(torch.bfloat16)
+    D = torch.empty(batch, M, N, device=DEV, dtype=torch.bfloat16)
+    check(L, L.msr_gemm_nt(P.data_ptr(), K, M * K, Q.data_ptr(), K, N * K, C.data_ptr(), N, M * N, D.data_ptr(), N,
+                           M * N, M, N, K, batch, alpha, beta, stream()), "gemm")
+    ref = alpha * torch.matmul(P.float(), Q.float().transpose(1, 2).contiguous()) + beta * C.float()
+    err = (D.float() - ref).abs()
+    tol = 2.0 ** -8 * ref.abs() + 1e-5 * ref.abs().max()
+    assert bool((err <= tol).all()), float((err - tol).max())
+
+
+def ns_same_op_fp32(G):
+    """fp32 emulation of the library's NS: bf16 storage of X, A, B between
+    products, fp32 accumulation, fused fp32 epilogues."""
+    a, b, c = O.NS_COEFFS
+    rb = lambda x: x.to(torch.bfloat16).float()  # noqa: E731
+    X = G.float()
+    tr = X.size(-2) > X.size(-1)
+    if tr:
+        X = X.mT
+    nrm = rb(X.norm(dim=(-2, -1), keepdim=True))
+    X = rb(X / rb(nrm + 1e-7))
+    for _ in range(5):
+        A = rb(X @ X.mT)
+        B = rb(c * (A @ A) + b * A)
+        X = rb((B @ X) + a * X)
+    if tr:
+        X = X.mT
+    return X
+
+
+@pytest.mark.parametrize("shape", [(256, 256), (3, 128, 320), (2, 320, 128), (1024, 256), (256, 1024),
+                                   (100, 60), (61, 99), (2, 512, 1536)])
+def test_newton_schulz_vs_fp32(L, shape):
+    from muon_sr_amd.muon import newton_schulz
+    torch.manual_seed(sum(shape))
+    G = (torch.randn(*shape) * 1e-3).to(torch.bfloat16)
+    out = newton_schulz(G.to(DEV)).cpu().float()
+    same = ns_same_op_fp32(G.double().float())
+    exact = O.ns_fp32(G)
+    ref16 = O.ns_bf16_torch(G).float()
+    e_same, e_exact, e_ref = rel_fro(out, same), rel_fro(out, exact), rel_fro(ref16, exact)
+    print(f"NS {shape}: vs same-op fp32 {e_same:.2e}, vs exact NS {e_exact:.2e} (reference bf16 NS: {e_ref:.2e})")
+    assert e_same < 1e-2
+    assert e_exact <= e_ref + 2e-3   # at least as close to exact NS as the reference's bf16 op sequence
+
+
+def test_newton_schulz_batch_invariant_and_steps0(L):
+    from muon_sr_amd.muon import newton_schulz
+    torch.manual_seed(0)
+    G = (torch.randn(4, 192, 320, device=DEV) * 1e-2).to(torch.bfloat16)
+    full = newton_schulz(G)
+    for i in range(4):
+        one = newton_schulz(G[i:i + 1].clone())
+        assert torch.equal(full[i:i + 1], one), i
+    X0 = newton_schulz(G, steps=0).float()
+    nrm = G.float().norm(dim=(-2, -1), keepdim=True).to(torch.bfloat16).float()
+    exp = (G.float() / (nrm + 1e-7).to(torch.bfloat16).float()).to(torch.bfloat16).float()
+    assert rel_fro(X0, exp) < 1e-2

@@ -1,0 +1,367 @@
+"""Benchmark of the muon_sr optimizer-step hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--configs adamw8bit,sr_accum,ns,full] [--noise philox8|triton]
+
+Prints ONE JSON line.  ``value`` is the headline workload (BASELINE.json
+configs[1]): one fused 8-bit blockwise AdamW step on a flat bf16 parameter of
+2^28 elements, in GB/s of algorithmic traffic (10.0625 B/element: read p, g,
+m, v and write p, m, v, plus 16 B of absmax per 256-element block).  The other
+configs of BASELINE.json are measured in the same run and reported under
+``configs``: SR gradient accumulation (config 3), the Muon Newton-Schulz step
+(config 4, TFLOP/s) and the full Llama-3-8B-shaped hybrid step (config 5, ms).
+
+Inputs are synthetic, seeded, and resident in HBM before the timed region.
+Kernel durations come from HIP events recorded on the stream the kernels run
+on; whole-step times from a synchronised wall clock around exactly K steps.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0       # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, TFLOP/s
+N8 = 1 << 28
+B8_PER_ELEM = 10.0 + 16.0 / 256  # 10.0625
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+class KernelTimer:
+    """Per-launch HIP event pairs on the current stream."""
+
+    def __init__(self):
+        self.pairs = []
+
+    def __enter__(self):
+        import torch
+        self.s = torch.cuda.Event(enable_timing=True)
+        self.e = torch.cuda.Event(enable_timing=True)
+        self.s.record()
+        return self
+
+    def __exit__(self, *exc):
+        self.e.record()
+        self.pairs.append((self.s, self.e))
+
+    def mean_ms(self):
+        return sum(s.elapsed_time(e) for s, e in self.pairs) / max(1, len(self.pairs))
+
+
+# ---------------------------------------------------------------------------
+# config 2: 8-bit AdamW on one flat bf16 parameter of 2^28 elements
+# ---------------------------------------------------------------------------
+
+def bench_adamw8bit(steps, warmup, n=N8):
+    import torch
+    from muon_sr_amd import TritonAdamW8bit
+    dev = "cuda:0"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    p = torch.nn.Parameter((torch.randn(n, device=dev, generator=gen) * 0.02).to(torch.bfloat16))
+    opt = TritonAdamW8bit([p], lr=3e-4, betas=(0.9, 0.95), eps=1e-10, weight_decay=0.01)
+    total = 10 + warmup + steps
+    # distinct seeded gradients per step, generated before any timing (2 B/elem each)
+    grads = []
+    for s in range(total):
+        gen.manual_seed(1000 + s)
+        grads.append((torch.randn(n, device=dev, generator=gen) * 1e-3).to(torch.bfloat16))
+    it = 0
+    for _ in range(10):            # build the uint8 codes and block scales
+        p.grad = grads[it]; it += 1
+        opt.step()
+    for _ in range(warmup):
+        p.grad = grads[it]; it += 1
+        opt.step()
+    sync()
+    kt = KernelTimer()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        p.grad = grads[it]; it += 1
+        with kt:
+            opt.step()
+    sync()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    kms = kt.mean_ms()
+    nbytes = B8_PER_ELEM * n
+    st = opt.state[p]
+    assert st["optim_bits"] == 8 and st["state1"].dtype == torch.uint8
+    out = dict(ms_per_step=wall, kernel_ms=kms, gbps=nbytes / (wall * 1e6), kernel_gbps=nbytes / (kms * 1e6),
+               bytes_per_step=nbytes)
+    del grads, opt, p
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline_adamw8bit(budget_s=12.0):
+    """The oracle's C restatement (one thread) on a bounded sample of config 2."""
+    import numpy as np
+    import oracle as O
+    n = 1 << 22
+    rng = np.random.default_rng(0)
+    p = O.f32_to_bf16_rne((rng.standard_normal(n) * 0.02).astype(np.float32))
+    q1, q2 = O.create_dynamic_map(True), O.create_dynamic_map(False)
+    s1 = np.full(n, 127, np.uint8)
+    s2 = np.zeros(n, np.uint8)
+    a1 = np.zeros(n // 256, np.float32)
+    a2 = np.zeros(n // 256, np.float32)
+    g = O.f32_to_bf16_rne((rng.standard_normal(n) * 1e-3).astype(np.float32))
+    steps, t = 0, 0.0
+    while t < budget_s:
+        step = steps + 1
+        t0 = time.perf_counter()
+        p, s1, s2, a1, a2 = O.adamw8bit(p, g, s1, s2, a1, a2, q1, q2, 256, True, 3e-4, 0.9, 0.95, 1e-10, 0.01,
+                                        1 - 0.9 ** step, 1 - 0.95 ** step,
+                                        O.NoiseSpec(O.NOISE_PHILOX8, step * 2654435761 & 0xFFFFFFFF))
+        t += time.perf_counter() - t0
+        steps += 1
+    gbps = B8_PER_ELEM * n * steps / t / 1e9
+    return dict(value=round(gbps, 4), unit="GB/s", cores=1, kind="port",
+                sample=f"{steps} steps of the C oracle on 2^22 of the 2^28 elements (same per-element work), "
+                       f"{t:.1f} s on {platform.processor() or platform.machine()}, 1 thread")
+
+
+# ---------------------------------------------------------------------------
+# config 3: SR gradient accumulation, 24-layer d=2048 ffn=5632 parameter set
+# ---------------------------------------------------------------------------
+
+def llama_small_shapes():
+    shapes = []
+    for _ in range(24):
+        shapes += [(2048, 2048)] * 4 + [(5632, 2048)] * 2 + [(2048, 5632)] + [(2048,)] * 2
+    shapes.append((32000, 2048))
+    return shapes
+
+
+def bench_sr_accum(micro=16):
+    import torch
+    from muon_sr_amd import TritonSRAccumulator
+    dev = "cuda:0"
+    shapes = llama_small_shapes()
+    params = [torch.nn.Parameter(torch.empty(s, device=dev, dtype=torch.bfloat16)) for s in shapes]
+    numel = sum(p.numel() for p in params)
+    gen = torch.Generator(device=dev)
+    gsets = []
+    for k in range(2):              # two seeded gradient sets, alternated across micro-batches
+        gen.manual_seed(300 + k)
+        gsets.append([(torch.randn(p.shape, device=dev, generator=gen) * 1e-4).to(torch.bfloat16) for p in params])
+
+    class Holder(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.ps = torch.nn.ParameterList(params)
+
+    model = Holder()
+
+    def run():
+        for mb in range(micro):
+            gs = gsets[mb % 2]
+            for p, g in zip(params, gs):
+                p.grad = g
+                TritonSRAccumulator._accum_hook(p)
+        TritonSRAccumulator.reassign_grad_buffer(model)
+        for p in params:
+            p.grad = None
+
+    run()  # warm-up
+    sync()
+    # steady-state accumulate kernels (micro-batches 2..16), timed per micro-batch with events
+    t0 = time.perf_counter()
+    evs = []
+    for mb in range(micro):
+        gs = gsets[mb % 2]
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for p, g in zip(params, gs):
+            p.grad = g
+            TritonSRAccumulator._accum_hook(p)
+        e.record()
+        evs.append((s, e))
+    TritonSRAccumulator.reassign_grad_buffer(model)
+    sync()
+    wall = (time.perf_counter() - t0) * 1e3
+    ms = [s.elapsed_time(e) for s, e in evs]
+    steady = sum(ms[1:]) / (micro - 1)
+    out = dict(tensors=len(params), elements=numel, micro_batches=micro, total_ms=wall,
+               first_microbatch_ms=ms[0], accumulate_ms=steady,
+               accumulate_gbps=6.0 * numel / (steady * 1e6), first_gbps=4.0 * numel / (ms[0] * 1e6))
+    del gsets, params, model
+    torch.cuda.empty_cache()
+    return out
+
+
+# ---------------------------------------------------------------------------
+# config 4: Muon step with batch_ns on 16 layers of d=2048 / ffn=5632 matrices
+# ---------------------------------------------------------------------------
+
+def ns_flops(shapes, steps=5):
+    f = 0
+    for s in shapes:
+        m, n = min(s), max(s)
+        f += steps * (4 * m * m * n + 2 * m ** 3)
+    return f
+
+
+def bench_muon(shapes, steps_timed, warmup, label):
+    import torch
+    from muon_sr_amd import TritonMuonSR
+    dev = "cuda:0"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    params = [torch.nn.Parameter((torch.randn(s, device=dev, generator=gen) * 0.02).to(torch.bfloat16))
+              for s in shapes]
+    gen.manual_seed(5)
+    grads = [(torch.randn(s, device=dev, generator=gen) * 1e-3).to(torch.bfloat16) for s in shapes]
+    opt = TritonMuonSR(params, lr=0.02, weight_decay=0.01, momentum=0.95, nesterov=True, ns_steps=5, batch_ns=True)
+    for p, g in zip(params, grads):
+        p.grad = g
+    for _ in range(warmup):
+        opt.step()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(steps_timed):
+        opt.step()
+    sync()
+    ms = (time.perf_counter() - t0) * 1e3 / steps_timed
+    fl = ns_flops(shapes)
+    out = dict(matrices=len(shapes), ns_tflop=fl / 1e12, ms_per_step=ms, tflops=fl / (ms * 1e9))
+    del opt, params, grads
+    torch.cuda.empty_cache()
+    return out
+
+
+def config4_shapes():
+    return [(2048, 2048)] * 64 + [(5632, 2048)] * 32 + [(2048, 5632)] * 16
+
+
+# ---------------------------------------------------------------------------
+# config 5: full hybrid step on Llama-3-8B shapes (Muon + 8-bit AdamW groups)
+# ---------------------------------------------------------------------------
+
+def bench_full(steps_timed, warmup):
+    import torch
+    from muon_sr_amd import TritonMuonSRWithAuxAdam
+    dev = "cuda:0"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(8)
+    mk = lambda s: torch.nn.Parameter((torch.randn(s, device=dev, generator=gen) * 0.02).to(torch.bfloat16))  # noqa
+    d, ffn, kv, vocab = 4096, 14336, 1024, 128256
+    muon, adam = [], []
+    embed = mk((vocab, d))
+    adam.append(embed)
+    for _ in range(32):
+        muon += [mk((d, d)), mk((kv, d)), mk((kv, d)), mk((d, d)), mk((ffn, d)), mk((ffn, d)), mk((d, ffn))]
+        adam += [mk((d,)), mk((d,))]
+    adam += [mk((d,)), mk((vocab, d))]
+    opt = TritonMuonSRWithAuxAdam([
+        dict(params=muon, use_muon=True, lr=0.02, weight_decay=0.01),
+        dict(params=adam, use_muon=False, lr=3e-4, betas=(0.9, 0.95), eps=1e-10, weight_decay=0.01, optim_bits=8),
+    ], batch_ns=True)
+    gen.manual_seed(9)
+    for p in muon + adam:
+        p.grad = (torch.randn(p.shape, device=dev, generator=gen) * 1e-3).to(torch.bfloat16)
+    for _ in range(warmup):
+        opt.step()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(steps_timed):
+        opt.step()
+    sync()
+    ms = (time.perf_counter() - t0) * 1e3 / steps_timed
+    fl = ns_flops([tuple(p.shape) for p in muon])
+    out = dict(muon_matrices=len(muon), adamw_tensors=len(adam), ns_tflop=fl / 1e12, ms_per_step=ms,
+               ns_tflops_effective=fl / (ms * 1e9))
+    del opt, muon, adam
+    torch.cuda.empty_cache()
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--configs", default="adamw8bit,sr_accum,ns,full")
+    ap.add_argument("--noise", default="philox8", choices=["philox8", "triton"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU: every box has one MI355X and the optimizer step "
+                                   "has no multi-GPU path here; run with --gpus 1"}))
+        sys.exit(2)
+
+    import torch
+    import muon_sr_amd
+    muon_sr_amd.set_sr_noise(args.noise)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    todo = set(args.configs.split(","))
+    log(f"device: {torch.cuda.get_device_name(0)}  noise: {args.noise}")
+
+    r8 = bench_adamw8bit(args.steps, args.warmup)
+    log(f"adamw8bit: {r8}")
+    configs = {"adamw8bit_2^28": {k: round(v, 4) for k, v in r8.items()}}
+    if "sr_accum" in todo:
+        r = bench_sr_accum()
+        log(f"sr_accum: {r}")
+        configs["sr_accum_24L_d2048"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+    if "ns" in todo:
+        r = bench_muon(config4_shapes(), steps_timed=3, warmup=1, label="config4")
+        log(f"muon config4: {r}")
+        configs["muon_ns_16L_d2048"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+    if "full" in todo:
+        r = bench_full(steps_timed=2, warmup=1)
+        log(f"full hybrid: {r}")
+        configs["hybrid_llama3_8b"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline_adamw8bit()
+    kernel_gbps = r8["kernel_gbps"]
+    line = {
+        "metric": "8-bit AdamW step GB/s (% HBM peak); Muon NS bf16 TFLOP/s; full step ms",
+        "value": round(r8["gbps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r8["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 arithmetic (bf16 params/grads, u8 moment codes)",
+        "data": "synthetic (seeded normal params/grads, resident in HBM)",
+        "config": {"workload": "8-bit blockwise AdamW step, one flat bf16 parameter of 2^28 elements "
+                               "(BASELINE.json configs[1])",
+                   "elements": N8, "block_size": 256, "lr": 3e-4, "betas": [0.9, 0.95], "eps": 1e-10,
+                   "weight_decay": 0.01, "sr_noise": args.noise, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(kernel_gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "adamw8bit_quant_kernel", "kernel_ms": round(r8["kernel_ms"], 4),
+                     "bytes_per_launch": r8["bytes_per_step"]},
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    if "muon_ns_16L_d2048" in configs:
+        line["ns_tflops"] = configs["muon_ns_16L_d2048"]["tflops"]
+        line["ns_frac_of_bf16_peak"] = round(configs["muon_ns_16L_d2048"]["tflops"] / BF16_PEAK_TFLOPS, 4)
+    if "hybrid_llama3_8b" in configs:
+        line["full_step_ms"] = configs["hybrid_llama3_8b"]["ms_per_step"]
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

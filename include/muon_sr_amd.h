@@ -76,13 +76,15 @@ int msr_adamw_bf16_step(uint16_t *p, const uint16_t *g, uint16_t *ema, uint16_t 
  * (muon_sr/triton_adamw_8bit.py:56-99, launched at :198-204).
  * quantized != 0: state1/state2 are uint8 codes [n], absmax1/absmax2 fp32
  *   [ceil(n/block)], qmap1 (signed) / qmap2 (unsigned) fp32 [256].
+ *   qtable: NULL, or a device copy of msr_quant_table_build(qmap1, qmap2)
+ *   (16-byte aligned) -- the same codes from a bucketed threshold table.
  * quantized == 0: state1/state2 are bf16 moments [n]; absmax/qmap unused.
  * block: power of two in [32, 4096].  bc1 = 1-b1^step, bc2 = 1-b2^step.
  * Streams: p uses SEED, bf16 m SEED+1, bf16 v SEED+2 (inject: uint16 [3][n]).
  * ------------------------------------------------------------------------- */
 int msr_adamw8bit_step(uint16_t *p, const uint16_t *g, void *state1, void *state2,
                        float *absmax1, float *absmax2, const float *qmap1, const float *qmap2,
-                       int64_t n, int32_t block, int32_t quantized,
+                       const void *qtable, int64_t n, int32_t block, int32_t quantized,
                        float lr, float beta1, float beta2, float eps, float weight_decay,
                        float bc1, float bc2, uint32_t seed,
                        int32_t noise_mode, const uint16_t *inject, msr_stream_t stream);
@@ -139,9 +141,25 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
 int msr_noise_fill(uint16_t *out, int64_t n, int64_t offset0, uint32_t seed, uint32_t k,
                    int32_t noise_mode, msr_stream_t stream);
 
-/* out[i] = quantizer code of x[i] against qmap (reference search rule). */
+/* out[i] = quantizer code of x[i] against qmap (reference search rule), or
+ * through qtable when it is not NULL. */
 int msr_quantize(const float *x, uint8_t *out, int64_t n, const float *qmap, int32_t is_signed,
-                 msr_stream_t stream);
+                 const void *qtable, msr_stream_t stream);
+
+/* Host-side construction of the quantizer table for a (signed, unsigned)
+ * codebook pair (HOST pointers, 256 floats each) into a HOST buffer of
+ * msr_quant_table_bytes() bytes.  Valid for codebooks on which the reference
+ * search is monotone (the bitsandbytes dynamic maps are; proven exhaustively
+ * by msr_quant_table_check). */
+size_t msr_quant_table_bytes(void);
+int msr_quant_table_build(const float *qmap_signed, const float *qmap_unsigned, void *table, size_t table_bytes);
+
+/* Device self-check of a table against the search for every float bit
+ * pattern u in [bits_lo, bits_hi] (<= bits(1.0f)): signed map at +x and -x,
+ * unsigned map at x.  counts[i] = mismatches found by work-group i. */
+int msr_quant_table_check(const void *qtable, const float *qmap_signed, const float *qmap_unsigned,
+                          uint32_t bits_lo, uint32_t bits_hi, uint32_t *counts, int32_t n_counts,
+                          msr_stream_t stream);
 
 /* Batched bf16 GEMM  D[b] = alpha * P[b] Q[b]^T + beta * C[b]  (fp32 accumulate, RNE bf16 out).
  * P: [M][K] (row stride ldp), Q: [N][K] (ldq), C/D: [M][N] (ldc/ldd); C may be NULL when beta == 0.

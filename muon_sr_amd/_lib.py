@@ -28,14 +28,17 @@ SIGNATURES = {
     "msr_last_error": (ctypes.c_char_p, []),
     "msr_sr_accum": (ctypes.c_int, [_P, _P, _I32, _I64, _U32, _I32, _I32, _P, _P]),
     "msr_adamw_bf16_step": (ctypes.c_int, [_P, _P, _P, _P, _I64, _F, _F, _F, _F, _F, _F, _F, _U32, _I32, _P, _P]),
-    "msr_adamw8bit_step": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32,
+    "msr_adamw8bit_step": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32,
                                           _F, _F, _F, _F, _F, _F, _F, _U32, _I32, _P, _P]),
     "msr_muon_prepare": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _F, _I32, _U32, _I32, _P, _P]),
     "msr_muon_apply": (ctypes.c_int, [_P, _P, _I64, _I32, _F, _F, _F, _P, _I32, _P, _P]),
     "msr_ns_workspace_bytes": (ctypes.c_int, [_I64, _I64, _I64, _SIZE_P]),
     "msr_newton_schulz": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _I32, _F, _F, _F, _P, ctypes.c_size_t, _P]),
     "msr_noise_fill": (ctypes.c_int, [_P, _I64, _I64, _U32, _U32, _I32, _P]),
-    "msr_quantize": (ctypes.c_int, [_P, _P, _I64, _P, _I32, _P]),
+    "msr_quantize": (ctypes.c_int, [_P, _P, _I64, _P, _I32, _P, _P]),
+    "msr_quant_table_bytes": (ctypes.c_size_t, []),
+    "msr_quant_table_build": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t]),
+    "msr_quant_table_check": (ctypes.c_int, [_P, _P, _P, _U32, _U32, _P, _I32, _P]),
     "msr_gemm_nt": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
                                    _I64, _I64, _I64, _I64, _F, _F, _P]),
 }

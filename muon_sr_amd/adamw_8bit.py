@@ -8,6 +8,7 @@ step runs one fused gfx950 kernel per tensor (libmuon_sr_amd.so).
 from __future__ import annotations
 
 import math
+import weakref
 
 import torch
 from torch.optim import Optimizer
@@ -38,14 +39,59 @@ def _cdiv(a: int, b: int) -> int:
     return -(-a // b)
 
 
+# Quantizer tables: built once per process on the host from the standard
+# codebooks, copied once per device; used only for states whose codebooks are
+# bit-identical to the standard ones (checked once per codebook tensor).
+_std_maps = None
+_host_table = None
+_dev_tables = {}
+_map_verdict = {}  # id(qmap1) -> (weakref(qmap1), weakref(qmap2), bool)
+
+
+def _standard_maps():
+    global _std_maps
+    if _std_maps is None:
+        _std_maps = (create_dynamic_map(True), create_dynamic_map(False))
+    return _std_maps
+
+
+def quant_table(state):
+    """Device pointer of the quantizer table for this state's codebooks, or None."""
+    global _host_table
+    q1, q2 = state["qmap1"], state["qmap2"]
+    verdict = _map_verdict.get(id(q1))
+    if verdict is None or verdict[0]() is not q1 or verdict[1]() is not q2:
+        s1, s2 = _standard_maps()
+        ok = torch.equal(q1.detach().cpu(), s1) and torch.equal(q2.detach().cpu(), s2)
+        verdict = (weakref.ref(q1), weakref.ref(q2), ok)
+        _map_verdict[id(q1)] = verdict
+    if not verdict[2]:
+        return None
+    dev = q1.device
+    t = _dev_tables.get(dev)
+    if t is None:
+        if _host_table is None:
+            L = _lib.lib()
+            nbytes = L.msr_quant_table_bytes()
+            buf = torch.zeros(nbytes, dtype=torch.uint8)
+            s1, s2 = _standard_maps()
+            _lib.check(L.msr_quant_table_build(s1.data_ptr(), s2.data_ptr(), buf.data_ptr(), nbytes),
+                       "msr_quant_table_build")
+            _host_table = buf
+        t = _host_table.to(dev)
+        _dev_tables[dev] = t
+    return t.data_ptr()
+
+
 def adamw8bit_launch(p, g, state, lr, beta1, beta2, eps, weight_decay, seed):
     """One fused 8-bit (or bf16-moment) step of one tensor with state from ``init_8bit_state``."""
     n = state["step"]
     quant = state["optim_bits"] == 8
     get = lambda k: state[k].data_ptr() if k in state else None  # noqa: E731
+    qt = quant_table(state) if quant else None
     rc = _lib.lib().msr_adamw8bit_step(
         p.data_ptr(), g.data_ptr(), state["state1"].data_ptr(), state["state2"].data_ptr(),
-        get("absmax1"), get("absmax2"), get("qmap1"), get("qmap2"), p.numel(), state["block_size"], int(quant),
+        get("absmax1"), get("absmax2"), get("qmap1"), get("qmap2"), qt, p.numel(), state["block_size"], int(quant),
         lr, beta1, beta2, eps, weight_decay, 1 - beta1 ** n, 1 - beta2 ** n, seed,
         _lib.noise_mode(), None, _lib.stream_of(p))
     _lib.check(rc, "msr_adamw8bit_step")

@@ -168,6 +168,85 @@ __device__ __forceinline__ uint32_t noise1(const Noise &ns, int64_t o) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// 8-bit quantizer
+// ---------------------------------------------------------------------------
+
+// The reference quantizer search (muon_sr/triton_adamw_8bit.py:27-53): seven
+// halvings from pivot 127 against the sorted codebook Q, then the midpoint rule
+// with the last bounds (initial bounds -1/0 and +1), then the sign fix for the
+// signed map.  Compiled for host (table construction) and device.
+__host__ __device__ inline uint32_t quantize_search(float x, const float *Q, bool is_signed) {
+    int pivot = 127, lower_pivot = 0, upper_pivot = 255;
+    float lower = is_signed ? -1.0f : 0.0f;
+    float upper = 1.0f;
+    float val = Q[pivot];
+#pragma unroll
+    for (int shift = 0; shift < 7; ++shift) {
+        const int delta = 64 >> shift;
+        const bool right = x > val;
+        lower_pivot = right ? pivot : lower_pivot;
+        upper_pivot = right ? upper_pivot : pivot;
+        lower = right ? val : lower;
+        upper = right ? upper : val;
+        pivot += right ? delta : -delta;
+        val = Q[pivot];
+    }
+    int result;
+    if (x > val) result = (x > (upper + val) * 0.5f) ? upper_pivot : pivot;
+    else result = (x < (lower + val) * 0.5f) ? lower_pivot : pivot;
+    if (is_signed) {
+        const float decoded = Q[result];
+        const bool mismatch = (decoded < 0.0f) != (x < 0.0f);
+        result += mismatch ? ((x > 0.0f) ? 1 : -1) : 0;
+    }
+    return (uint32_t)result & 0xffu;
+}
+
+// Bucketed threshold table equivalent to quantize_search for one pair of
+// codebooks (built by msr_quant_table_build).  For a float x with bit pattern
+// u (|x| <= 1 or NaN), map base mb (0: signed map, 512: unsigned map), the
+// octave word o = oct[mb + (u >> 23)] (sign and exponent) and
+//     b = (o >> 8) + ((u & 0x7fffff) >> (o & 31)),
+//     code = ((u & 0x7fffffff) >= bkt[b].x) ? bkt[b].y >> 8 : bkt[b].y & 0xff.
+// Each bucket holds at most one point where the code changes; exponent 255
+// (NaN) points at a bucket holding the search's NaN code.
+constexpr int QT_OCT = 2 * 512;
+constexpr int QT_MAX_BKT = 2048;
+
+struct QuantTable {
+    uint32_t n_bkt;
+    uint32_t pad[3];
+    uint32_t oct[QT_OCT];
+    uint2 bkt[QT_MAX_BKT];
+};
+
+__host__ __device__ inline uint32_t quantize_lookup(float x, const uint32_t *oct, const uint2 *bkt, bool is_signed) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const uint32_t o = oct[(is_signed ? 0u : 512u) + (u >> 23)];
+    const uint2 en = bkt[(o >> 8) + ((u & 0x7fffffu) >> (o & 31u))];
+    return (en.y >> (((u & 0x7fffffffu) >= en.x) ? 8u : 0u)) & 0xffu;
+}
+
+// m / d for the signed map: x = RN_f32(m / d) up to the distinction the
+// signed codebook cannot make (every nonzero |x| < FLT_MIN of one sign codes
+// alike), for d > 0 (or +inf), rd = RN_f64(1 / d) and dlim = min(d * 2^-150, DBL_MAX).
+// In the normal range (float)(m * rd) is exact: an fp32 quotient is never an
+// fp32 rounding midpoint (a midpoint needs 25 significant bits) and its
+// distance to one (>= 2^-50 relative) exceeds the double product's error
+// (<= 2^-52 relative).  Whether RN_f32(m / d) is zero is decided exactly:
+// |m| <= d * 2^-150 (ties go to the even zero).
+__device__ __forceinline__ float quotient_signed(float m, double rd, double dlim) {
+    const float x = (float)((double)m * rd);
+    const bool nz = !(fabs((double)m) <= dlim);  // true for NaN and for inf / inf
+    const float tiny = copysignf(0x1p-149f, m);
+    return nz ? ((x == 0.0f) ? tiny : x) : 0.0f;
+}
+
+// v / d for the unsigned map (v >= 0): below FLT_MIN every value, zero
+// included, codes to 0, so the double product alone decides the code.
+__device__ __forceinline__ float quotient_unsigned(float v, double rd) { return (float)((double)v * rd); }
+
 inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
 // Grid size for a grid-stride loop over `work` items with `threads` per block.

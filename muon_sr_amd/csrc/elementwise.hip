@@ -9,6 +9,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
+#include <utility>
+#include <vector>
 
 #include "common.hpp"
 #include "../../include/muon_sr_amd.h"
@@ -223,35 +226,6 @@ __global__ __launch_bounds__(THREADS) void adamw_bf16_kernel(AdamWArgs a) {
 // 8-bit blockwise AdamW   (muon_sr/triton_adamw_8bit.py:27-99)
 // ---------------------------------------------------------------------------
 
-// The reference quantizer search (muon_sr/triton_adamw_8bit.py:27-53) over a
-// codebook held in LDS.
-__device__ __forceinline__ uint32_t quantize_search(float x, const float *Q, bool is_signed) {
-    int pivot = 127, lower_pivot = 0, upper_pivot = 255;
-    float lower = is_signed ? -1.0f : 0.0f;
-    float upper = 1.0f;
-    float val = Q[pivot];
-#pragma unroll
-    for (int shift = 0; shift < 7; ++shift) {
-        const int delta = 64 >> shift;
-        const bool right = x > val;
-        lower_pivot = right ? pivot : lower_pivot;
-        upper_pivot = right ? upper_pivot : pivot;
-        lower = right ? val : lower;
-        upper = right ? upper : val;
-        pivot += right ? delta : -delta;
-        val = Q[pivot];
-    }
-    int result;
-    if (x > val) result = (x > (upper + val) * 0.5f) ? upper_pivot : pivot;
-    else result = (x < (lower + val) * 0.5f) ? lower_pivot : pivot;
-    if (is_signed) {
-        const float decoded = Q[result];
-        const bool mismatch = (decoded < 0.0f) != (x < 0.0f);
-        result += mismatch ? ((x > 0.0f) ? 1 : -1) : 0;
-    }
-    return (uint32_t)result;
-}
-
 struct Adam8Args {
     uint16_t *p;
     const uint16_t *g;
@@ -261,6 +235,7 @@ struct Adam8Args {
     float *absmax2;
     const float *qmap1;
     const float *qmap2;
+    const QuantTable *qtable;
     int64_t n;
     float lr, b1, b2, eps, wd, bc1, bc2;
     Noise ns_p, ns_m, ns_v;
@@ -282,7 +257,9 @@ __device__ __forceinline__ Adam8Consts adam8_consts(const Adam8Args &a) {
 }
 
 // Threads per quantization block: BLOCK/8.  Work-group size: max(256, BLOCK/8).
-template <int MODE, int BLOCK, bool VEC>
+// QTAB: requantize through the bucketed threshold table (standard codebooks),
+// else through the reference search; both give the search's codes.
+template <int MODE, int BLOCK, bool VEC, bool QTAB>
 __global__ __launch_bounds__((BLOCK / 8 > THREADS) ? BLOCK / 8 : THREADS) void adamw8bit_quant_kernel(Adam8Args a) {
     constexpr int TPB = BLOCK / 8;
     constexpr int WG = TPB > THREADS ? TPB : THREADS;
@@ -290,9 +267,16 @@ __global__ __launch_bounds__((BLOCK / 8 > THREADS) ? BLOCK / 8 : THREADS) void a
     constexpr int NWAVES = WG / 64;
     __shared__ float q1s[256], q2s[256];
     __shared__ float red_m[NWAVES], red_v[NWAVES];
+    __shared__ uint32_t s_oct[QTAB ? QT_OCT : 1];
+    __shared__ uint2 s_bkt[QTAB ? QT_MAX_BKT : 1];
     for (int i = threadIdx.x; i < 256; i += WG) {
         q1s[i] = a.qmap1[i];
         q2s[i] = a.qmap2[i];
+    }
+    if constexpr (QTAB) {
+        const uint32_t nb = a.qtable->n_bkt;
+        for (int i = threadIdx.x; i < QT_OCT; i += WG) s_oct[i] = a.qtable->oct[i];
+        for (uint32_t i = threadIdx.x; i < nb; i += WG) s_bkt[i] = a.qtable->bkt[i];
     }
     __syncthreads();
     const Adam8Consts c = adam8_consts(a);
@@ -301,34 +285,62 @@ __global__ __launch_bounds__((BLOCK / 8 > THREADS) ? BLOCK / 8 : THREADS) void a
     const int64_t nblocks = (a.n + BLOCK - 1) / BLOCK;
     const int sub = threadIdx.x / TPB;       // quant block within the work-group
     const int lane_q = threadIdx.x % TPB;    // thread within the quant block
-    for (int64_t qb0 = (int64_t)blockIdx.x * QB_PER_WG; qb0 < nblocks; qb0 += (int64_t)gridDim.x * QB_PER_WG) {
-        const int64_t qb = qb0 + sub;
+    const int64_t stride = (int64_t)gridDim.x * QB_PER_WG;
+
+    // raw inputs of one 8-element group; the next group is fetched while the
+    // current one is computed
+    struct Raw {
+        uint32_t wp[4], wg[4];
+        uint2 mc, vc;
+        float ms, vs;
+    };
+    auto fetch = [&](int64_t qb, Raw &r) {
+        const bool ok = qb < nblocks;
+        const int64_t o0 = qb * BLOCK + lane_q * 8;
+        const int valid = ok ? clamp_valid(a.n, o0) : 0;
+        load_bf16x8<VEC>(a.p, o0, valid, r.wp);
+        load_bf16x8<VEC>(a.g, o0, valid, r.wg);
+        if (VEC && valid == 8) {
+            r.mc = *reinterpret_cast<const uint2 *>(m8 + o0);
+            r.vc = *reinterpret_cast<const uint2 *>(v8 + o0);
+        } else {
+            uint32_t cm[8], cv[8];
+            load_u8x8<false>(m8, o0, valid, 127u, cm);
+            load_u8x8<false>(v8, o0, valid, 0u, cv);
+            r.mc = make_uint2(cm[0] | cm[1] << 8 | cm[2] << 16 | cm[3] << 24, cm[4] | cm[5] << 8 | cm[6] << 16 | cm[7] << 24);
+            r.vc = make_uint2(cv[0] | cv[1] << 8 | cv[2] << 16 | cv[3] << 24, cv[4] | cv[5] << 8 | cv[6] << 16 | cv[7] << 24);
+        }
+        r.ms = ok ? a.absmax1[qb] : 0.0f;
+        r.vs = ok ? a.absmax2[qb] : 0.0f;
+    };
+
+    int64_t qb = (int64_t)blockIdx.x * QB_PER_WG + sub;
+    Raw nxt;
+    fetch(qb, nxt);
+    for (int64_t qb0 = (int64_t)blockIdx.x * QB_PER_WG; qb0 < nblocks; qb0 += stride, qb += stride) {
+        const Raw cur = nxt;
+        if (qb0 + stride < nblocks) fetch(qb + stride, nxt);
         const bool qb_ok = qb < nblocks;
         const int64_t o0 = qb * BLOCK + lane_q * 8;
         const int valid = qb_ok ? clamp_valid(a.n, o0) : 0;
-        uint32_t wp[4], wg[4], mc[8], vc[8];
-        load_bf16x8<VEC>(a.p, o0, valid, wp);
-        load_bf16x8<VEC>(a.g, o0, valid, wg);
-        load_u8x8<VEC>(m8, o0, valid, 127u, mc);
-        load_u8x8<VEC>(v8, o0, valid, 0u, vc);
-        const float ms = qb_ok ? a.absmax1[qb] : 0.0f;
-        const float vs = qb_ok ? a.absmax2[qb] : 0.0f;
         float p[8], g[8], m[8], v[8];
-        unpack8(wp, p);
-        unpack8(wg, g);
+        unpack8(cur.wp, p);
+        unpack8(cur.wg, g);
         uint32_t rp[8];
         noise8<MODE>(a.ns_p, o0, valid, rp);
         float mmax = 0.0f, vmax = 0.0f;
         uint32_t op[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            float mj = q1s[mc[j]] * ms;                                   // :65
-            float vj = q2s[vc[j]] * vs;                                   // :66
+            const uint32_t mcj = ((j < 4 ? cur.mc.x : cur.mc.y) >> (8 * (j & 3))) & 0xffu;
+            const uint32_t vcj = ((j < 4 ? cur.vc.x : cur.vc.y) >> (8 * (j & 3))) & 0xffu;
+            float mj = q1s[mcj] * cur.ms;                                 // :65
+            float vj = q2s[vcj] * cur.vs;                                 // :66
             const bool fin = fabsf(g[j]) < __builtin_huge_valf();         // :70
             mj = fin ? a.b1 * mj + c.one_m_b1 * g[j] : 0.0f;              // :71
             vj = fin ? a.b2 * vj + (c.one_m_b2 * g[j]) * g[j] : 0.0f;     // :72
             const float upd = (p[j] - (c.step_c * mj) / (sqrtf(vj) + c.eps_c)) * c.decay;  // :74
-            const uint32_t pin = (j & 1) ? (wp[j >> 1] >> 16) : (wp[j >> 1] & 0xffffu);
+            const uint32_t pin = (j & 1) ? (cur.wp[j >> 1] >> 16) : (cur.wp[j >> 1] & 0xffffu);
             op[j] = fin ? sr_bf16(upd, rp[j]) : pin;                      // :75-78
             m[j] = mj;
             v[j] = vj;
@@ -337,9 +349,10 @@ __global__ __launch_bounds__((BLOCK / 8 > THREADS) ? BLOCK / 8 : THREADS) void a
                 vmax = fmaxf(vmax, fabsf(vj));
             }
         }
+        uint32_t wo[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) wp[j] = pack2(op[2 * j], op[2 * j + 1]);
-        store_bf16x8<VEC>(a.p, o0, valid, wp);
+        for (int j = 0; j < 4; ++j) wo[j] = pack2(op[2 * j], op[2 * j + 1]);
+        store_bf16x8<VEC>(a.p, o0, valid, wo);
 
         // block absmax (:80-81): shuffles inside the wave, LDS across waves
 #pragma unroll
@@ -367,10 +380,21 @@ __global__ __launch_bounds__((BLOCK / 8 > THREADS) ? BLOCK / 8 : THREADS) void a
         }
         const float md = mmax > 0.0f ? mmax : 1.0f;                       // :82
         const float vd = vmax > 0.0f ? vmax : 1.0f;                       // :83
+        const double rmd = 1.0 / (double)md;
+        const double rvd = 1.0 / (double)vd;
+        const double mlim = fmin((double)md * 0x1p-150, 1.7976931348623157e308);
+        uint32_t mc[8], vc[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            mc[j] = quantize_search(m[j] / md, q1s, true);                // :82,84
-            vc[j] = quantize_search(v[j] / vd, q2s, false);               // :83,85
+            const float xm = quotient_signed(m[j], rmd, mlim);            // m / md, :82
+            const float xv = quotient_unsigned(v[j], rvd);                // v / vd, :83
+            if constexpr (QTAB) {
+                mc[j] = quantize_lookup(xm, s_oct, s_bkt, true);          // :84
+                vc[j] = quantize_lookup(xv, s_oct, s_bkt, false);         // :85
+            } else {
+                mc[j] = quantize_search(xm, q1s, true);
+                vc[j] = quantize_search(xv, q2s, false);
+            }
         }
         store_u8x8<VEC>(m8, o0, valid, mc);
         store_u8x8<VEC>(v8, o0, valid, vc);
@@ -540,12 +564,49 @@ __global__ __launch_bounds__(THREADS) void noise_fill_kernel(uint16_t *out, int6
 }
 
 __global__ __launch_bounds__(THREADS) void quantize_kernel(const float *x, uint8_t *out, int64_t n,
-                                                          const float *qmap, int is_signed) {
+                                                          const float *qmap, int is_signed, const QuantTable *qt) {
     __shared__ float q[256];
+    __shared__ uint32_t s_oct[QT_OCT];
+    __shared__ uint2 s_bkt[QT_MAX_BKT];
     for (int i = threadIdx.x; i < 256; i += THREADS) q[i] = qmap[i];
+    if (qt) {
+        for (int i = threadIdx.x; i < QT_OCT; i += THREADS) s_oct[i] = qt->oct[i];
+        for (uint32_t i = threadIdx.x; i < qt->n_bkt; i += THREADS) s_bkt[i] = qt->bkt[i];
+    }
     __syncthreads();
     for (int64_t i = (int64_t)blockIdx.x * THREADS + threadIdx.x; i < n; i += (int64_t)gridDim.x * THREADS)
-        out[i] = (uint8_t)quantize_search(x[i], q, is_signed != 0);
+        out[i] = (uint8_t)(qt ? quantize_lookup(x[i], s_oct, s_bkt, is_signed != 0)
+                              : quantize_search(x[i], q, is_signed != 0));
+}
+
+// Counts, per work-group, the floats x = bits(u) for u in [lo, hi] where the
+// table disagrees with the search: signed map at x and -x, unsigned map at x.
+__global__ __launch_bounds__(THREADS) void quant_table_check_kernel(const QuantTable *qt, const float *q1,
+                                                                    const float *q2, uint32_t lo, uint32_t hi,
+                                                                    uint32_t *counts) {
+    __shared__ float s1[256], s2[256];
+    __shared__ uint32_t s_oct[QT_OCT];
+    __shared__ uint2 s_bkt[QT_MAX_BKT];
+    __shared__ uint32_t red[THREADS];
+    for (int i = threadIdx.x; i < 256; i += THREADS) { s1[i] = q1[i]; s2[i] = q2[i]; }
+    for (int i = threadIdx.x; i < QT_OCT; i += THREADS) s_oct[i] = qt->oct[i];
+    for (uint32_t i = threadIdx.x; i < qt->n_bkt; i += THREADS) s_bkt[i] = qt->bkt[i];
+    __syncthreads();
+    uint32_t bad = 0;
+    const uint64_t span = (uint64_t)hi - lo + 1;
+    for (uint64_t i = (uint64_t)blockIdx.x * THREADS + threadIdx.x; i < span; i += (uint64_t)gridDim.x * THREADS) {
+        const float x = __uint_as_float(lo + (uint32_t)i);
+        bad += quantize_lookup(x, s_oct, s_bkt, true) != quantize_search(x, s1, true);
+        bad += quantize_lookup(-x, s_oct, s_bkt, true) != quantize_search(-x, s1, true);
+        bad += quantize_lookup(x, s_oct, s_bkt, false) != quantize_search(x, s2, false);
+    }
+    red[threadIdx.x] = bad;
+    __syncthreads();
+    for (int w = THREADS / 2; w > 0; w >>= 1) {
+        if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) counts[blockIdx.x] = red[0];
 }
 
 }  // namespace msr
@@ -565,22 +626,27 @@ static inline Noise make_noise(uint32_t seed, uint32_t k, const uint16_t *inject
         if ((mode) == NOISE_INJECT && !(inject)) { set_error("noise_mode INJECT needs an inject buffer"); return MSR_ERR_ARG; } \
     } while (0)
 
+template <int MODE, int BLOCK>
+static void launch_quant_mode(bool vec, bool qtab, const Adam8Args &a, hipStream_t s, unsigned grid, int wg) {
+    if (qtab) {
+        if (vec) hipLaunchKernelGGL((adamw8bit_quant_kernel<MODE, BLOCK, true, true>), dim3(grid), dim3(wg), 0, s, a);
+        else hipLaunchKernelGGL((adamw8bit_quant_kernel<MODE, BLOCK, false, true>), dim3(grid), dim3(wg), 0, s, a);
+    } else {
+        if (vec) hipLaunchKernelGGL((adamw8bit_quant_kernel<MODE, BLOCK, true, false>), dim3(grid), dim3(wg), 0, s, a);
+        else hipLaunchKernelGGL((adamw8bit_quant_kernel<MODE, BLOCK, false, false>), dim3(grid), dim3(wg), 0, s, a);
+    }
+}
+
 template <int BLOCK>
 static void launch_quant(int mode, bool vec, const Adam8Args &a, hipStream_t s, int64_t nblocks) {
     constexpr int TPB = BLOCK / 8;
     constexpr int WG = TPB > THREADS ? TPB : THREADS;
     constexpr int QB_PER_WG = WG / TPB;
-    const unsigned grid = grid_for(nblocks, QB_PER_WG, 256 * 16);
-    if (mode == NOISE_TRITON) {
-        if (vec) hipLaunchKernelGGL((adamw8bit_quant_kernel<NOISE_TRITON, BLOCK, true>), dim3(grid), dim3(WG), 0, s, a);
-        else hipLaunchKernelGGL((adamw8bit_quant_kernel<NOISE_TRITON, BLOCK, false>), dim3(grid), dim3(WG), 0, s, a);
-    } else if (mode == NOISE_PHILOX8) {
-        if (vec) hipLaunchKernelGGL((adamw8bit_quant_kernel<NOISE_PHILOX8, BLOCK, true>), dim3(grid), dim3(WG), 0, s, a);
-        else hipLaunchKernelGGL((adamw8bit_quant_kernel<NOISE_PHILOX8, BLOCK, false>), dim3(grid), dim3(WG), 0, s, a);
-    } else {
-        if (vec) hipLaunchKernelGGL((adamw8bit_quant_kernel<NOISE_INJECT, BLOCK, true>), dim3(grid), dim3(WG), 0, s, a);
-        else hipLaunchKernelGGL((adamw8bit_quant_kernel<NOISE_INJECT, BLOCK, false>), dim3(grid), dim3(WG), 0, s, a);
-    }
+    const unsigned grid = grid_for(nblocks, QB_PER_WG, 256 * 8);
+    const bool qtab = a.qtable != nullptr;
+    if (mode == NOISE_TRITON) launch_quant_mode<NOISE_TRITON, BLOCK>(vec, qtab, a, s, grid, WG);
+    else if (mode == NOISE_PHILOX8) launch_quant_mode<NOISE_PHILOX8, BLOCK>(vec, qtab, a, s, grid, WG);
+    else launch_quant_mode<NOISE_INJECT, BLOCK>(vec, qtab, a, s, grid, WG);
 }
 
 extern "C" {
@@ -634,7 +700,8 @@ int msr_adamw_bf16_step(uint16_t *p, const uint16_t *g, uint16_t *ema, uint16_t 
 }
 
 int msr_adamw8bit_step(uint16_t *p, const uint16_t *g, void *state1, void *state2, float *absmax1, float *absmax2,
-                       const float *qmap1, const float *qmap2, int64_t n, int32_t block, int32_t quantized, float lr,
+                       const float *qmap1, const float *qmap2, const void *qtable, int64_t n, int32_t block,
+                       int32_t quantized, float lr,
                        float beta1, float beta2, float eps, float weight_decay, float bc1, float bc2, uint32_t seed,
                        int32_t noise_mode, const uint16_t *inject, msr_stream_t stream) {
     if (n < 0 || (n > 0 && (!p || !g || !state1 || !state2))) { set_error("msr_adamw8bit_step: bad arguments"); return MSR_ERR_ARG; }
@@ -648,6 +715,8 @@ int msr_adamw8bit_step(uint16_t *p, const uint16_t *g, void *state1, void *state
     Adam8Args a;
     a.p = p; a.g = g; a.s1 = state1; a.s2 = state2; a.absmax1 = absmax1; a.absmax2 = absmax2;
     a.qmap1 = qmap1; a.qmap2 = qmap2; a.n = n;
+    a.qtable = static_cast<const QuantTable *>(qtable);
+    if (a.qtable && !aligned(a.qtable, 16)) { set_error("msr_adamw8bit_step: qtable must be 16-byte aligned"); return MSR_ERR_ALIGN; }
     a.lr = lr; a.b1 = beta1; a.b2 = beta2; a.eps = eps; a.wd = weight_decay; a.bc1 = bc1; a.bc2 = bc2;
     a.ns_p = make_noise(seed, 0, inject, n);
     a.ns_m = make_noise(seed, 1, inject, n);
@@ -761,12 +830,99 @@ int msr_noise_fill(uint16_t *out, int64_t n, int64_t offset0, uint32_t seed, uin
     return check_launch("msr_noise_fill");
 }
 
-int msr_quantize(const float *x, uint8_t *out, int64_t n, const float *qmap, int32_t is_signed, msr_stream_t stream) {
+int msr_quantize(const float *x, uint8_t *out, int64_t n, const float *qmap, int32_t is_signed, const void *qtable,
+                 msr_stream_t stream) {
     if (n < 0 || (n > 0 && (!x || !out || !qmap))) { set_error("msr_quantize: bad arguments"); return MSR_ERR_ARG; }
     if (n == 0) return MSR_OK;
     hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(n, THREADS)), dim3(THREADS), 0, (hipStream_t)stream, x, out, n,
-                       qmap, is_signed);
+                       qmap, is_signed, static_cast<const QuantTable *>(qtable));
     return check_launch("msr_quantize");
+}
+
+size_t msr_quant_table_bytes(void) { return sizeof(QuantTable); }
+
+int msr_quant_table_build(const float *qmap_signed, const float *qmap_unsigned, void *table, size_t table_bytes) {
+    if (!qmap_signed || !qmap_unsigned || !table || table_bytes < sizeof(QuantTable)) {
+        set_error("msr_quant_table_build: need host codebooks and a host buffer of %zu bytes", sizeof(QuantTable));
+        return MSR_ERR_ARG;
+    }
+    QuantTable *t = static_cast<QuantTable *>(table);
+    memset(t, 0, sizeof(QuantTable));
+    const uint32_t ONE = 0x3f800000u;
+    uint32_t nb = 0;
+    // three sides: signed map x >= 0, signed map x < 0, unsigned map x >= 0
+    for (int side = 0; side < 3; ++side) {
+        const float *Q = side < 2 ? qmap_signed : qmap_unsigned;
+        const bool sgn = side < 2;
+        const bool neg = side == 1;
+        const uint32_t oct_base = (side == 2 ? 512u : 0u) + (neg ? 256u : 0u);
+        auto f = [&](uint32_t a) {
+            const float x = __builtin_bit_cast(float, a | (neg ? 0x80000000u : 0u));
+            return quantize_search(x, Q, sgn);
+        };
+        // change points of the monotone code over |x| bits a in [0, ONE], by bisection
+        std::vector<uint32_t> tr;
+        std::vector<std::pair<uint32_t, uint32_t>> stack{{0u, ONE}};
+        while (!stack.empty()) {
+            auto [lo, hi] = stack.back();
+            stack.pop_back();
+            if (f(lo) == f(hi)) continue;
+            if (hi == lo + 1) { tr.push_back(hi); continue; }
+            const uint32_t mid = lo + (hi - lo) / 2;
+            stack.push_back({mid, hi});
+            stack.push_back({lo, mid});
+        }
+        std::sort(tr.begin(), tr.end());
+        for (uint32_t e = 0; e < 128; ++e) {
+            const uint32_t base = e << 23;
+            std::vector<uint32_t> te;
+            for (uint32_t x : tr)
+                if ((x >> 23) == e) te.push_back(x);
+            int sh = 23;
+            auto ok = [&](int s) {
+                for (size_t i = 1; i < te.size(); ++i)
+                    if ((te[i] >> s) == (te[i - 1] >> s)) return false;
+                return true;
+            };
+            while (sh > 0 && !ok(sh)) --sh;
+            if (!ok(sh)) { set_error("msr_quant_table_build: two code changes one ulp apart"); return MSR_ERR_ARG; }
+            const uint32_t cnt = 1u << (23 - sh);
+            if (nb + cnt + 1 > (uint32_t)QT_MAX_BKT) { set_error("msr_quant_table_build: more than %d buckets", QT_MAX_BKT); return MSR_ERR_ARG; }
+            t->oct[oct_base + e] = (nb << 8) | (uint32_t)sh;
+            for (uint32_t k = 0; k < cnt; ++k) {
+                const uint32_t a0 = base + (k << sh);
+                const uint32_t a1 = a0 + (1u << sh) - 1;
+                uint32_t thr = 0xffffffffu;
+                for (uint32_t x : te)
+                    if (x > a0 && x <= a1) thr = x;
+                const uint32_t lo_code = a0 <= ONE ? f(a0) : f(ONE);
+                const uint32_t hi_code = thr != 0xffffffffu ? f(thr) : lo_code;
+                t->bkt[nb + k] = make_uint2(thr, lo_code | (hi_code << 8));
+            }
+            nb += cnt;
+        }
+        // exponents 128..255 (|x| > 1 cannot occur; 255 is NaN): the search's NaN code
+        const uint32_t nan_code = quantize_search(__builtin_bit_cast(float, 0x7fc00000u), Q, sgn);
+        t->bkt[nb] = make_uint2(0xffffffffu, nan_code | (nan_code << 8));
+        for (uint32_t e = 128; e < 256; ++e) t->oct[oct_base + e] = (nb << 8) | 23u;
+        nb += 1;
+    }
+    // the unsigned map never sees x < 0 (v >= 0); point that half at its NaN bucket
+    for (uint32_t e = 0; e < 256; ++e) t->oct[512 + 256 + e] = t->oct[512 + 255];
+    t->n_bkt = nb;
+    return MSR_OK;
+}
+
+int msr_quant_table_check(const void *qtable, const float *qmap_signed, const float *qmap_unsigned, uint32_t bits_lo,
+                          uint32_t bits_hi, uint32_t *counts, int32_t n_counts, msr_stream_t stream) {
+    if (!qtable || !qmap_signed || !qmap_unsigned || !counts || n_counts <= 0 || bits_hi < bits_lo ||
+        bits_hi > 0x3f800000u) {
+        set_error("msr_quant_table_check: bad arguments");
+        return MSR_ERR_ARG;
+    }
+    hipLaunchKernelGGL(quant_table_check_kernel, dim3((unsigned)n_counts), dim3(THREADS), 0, (hipStream_t)stream,
+                       static_cast<const QuantTable *>(qtable), qmap_signed, qmap_unsigned, bits_lo, bits_hi, counts);
+    return check_launch("msr_quant_table_check");
 }
 
 }  // extern "C"

@@ -16,7 +16,7 @@ LIB = os.path.join(ROOT, "muon_sr_amd", "libmuon_sr_amd.so")
 
 def declared_symbols():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(msr_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char \*)\s*(msr_\w+)\s*\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -48,8 +48,8 @@ def test_python_signatures_cover_header(lib):
 def test_argument_validation_without_gpu(lib):
     assert lib.msr_version() >= 100
     # bad block size / negative sizes / bad noise mode are rejected before any HIP call
-    rc = lib.msr_adamw8bit_step(1, 1, 1, 1, 1, 1, 1, 1, 100, 48, 1, 1e-3, 0.9, 0.99, 1e-8, 0.0, 0.1, 0.01, 0, 1,
-                                None, None)
+    rc = lib.msr_adamw8bit_step(1, 1, 1, 1, 1, 1, 1, 1, None, 100, 48, 1, 1e-3, 0.9, 0.99, 1e-8, 0.0, 0.1, 0.01, 0,
+                                1, None, None)
     assert rc == 1001 and b"block" in lib.msr_last_error()
     assert lib.msr_sr_accum(None, None, 0, -1, 0, 0, 1, None, None) == 1001
     assert lib.msr_sr_accum(1, 1, 0, 10, 0, 0, 7, None, None) == 1001

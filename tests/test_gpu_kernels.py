@@ -136,15 +136,31 @@ def test_adamw_bf16_vs_oracle(L, mode, misalign):
 # (a) 8-bit AdamW
 # ---------------------------------------------------------------------------
 
-def _adam8_call(L, p, g, s1, s2, a1, a2, q1, q2, n, block, quant, hyper, seed, mode, inj=None):
+_QT = {}
+
+
+def qtable_dev(L):
+    """Device copy of the quantizer table of the standard codebooks."""
+    if "t" not in _QT:
+        nbytes = L.msr_quant_table_bytes()
+        buf = np.zeros(nbytes, np.uint8)
+        q1, q2 = O.create_dynamic_map(True), O.create_dynamic_map(False)
+        check(L, L.msr_quant_table_build(q1.ctypes.data, q2.ctypes.data, buf.ctypes.data, nbytes), "table build")
+        _QT["t"] = np_to_dev(buf)
+    return _QT["t"]
+
+
+def _adam8_call(L, p, g, s1, s2, a1, a2, q1, q2, n, block, quant, hyper, seed, mode, inj=None, qt=None):
     lr, b1, b2, eps, wd, bc1, bc2 = hyper
     check(L, L.msr_adamw8bit_step(p.data_ptr(), g.data_ptr(), s1.data_ptr(), s2.data_ptr(), ptr(a1), ptr(a2),
-                                  ptr(q1), ptr(q2), n, block, int(quant), lr, b1, b2, eps, wd, bc1, bc2, seed, mode,
-                                  ptr(inj), stream()), "adamw8bit")
+                                  ptr(q1), ptr(q2), ptr(qt), n, block, int(quant), lr, b1, b2, eps, wd, bc1, bc2,
+                                  seed, mode, ptr(inj), stream()), "adamw8bit")
 
 
-def test_adamw8bit_reference_vectors(L, golden):
+@pytest.mark.parametrize("use_table", [False, True])
+def test_adamw8bit_reference_vectors(L, golden, use_table):
     z = golden("adamw8bit")
+    qt = qtable_dev(L) if use_table else None
     q1 = np_to_dev(O.create_dynamic_map(True))
     q2 = np_to_dev(O.create_dynamic_map(False))
     names = sorted({k.split("/")[0] for k in z.files})
@@ -164,7 +180,7 @@ def test_adamw8bit_reference_vectors(L, golden):
             g = u16_to_dev(k(f"g_{step}"))
             hyper = (lr, b1, b2, eps, wd, 1 - b1 ** step, 1 - b2 ** step)
             _adam8_call(L, p, g, s1, s2, a1, a2, q1 if quant else None, q2 if quant else None, n, block, quant,
-                        hyper, int(k(f"seed_{step}")), O.NOISE_TRITON)
+                        hyper, int(k(f"seed_{step}")), O.NOISE_TRITON, qt=qt if quant else None)
             assert np.array_equal(dev_to_u16(p), k(f"p_{step}")), (name, step)
             if quant:
                 assert np.array_equal(s1.cpu().numpy(), k(f"s1_{step}")), (name, step)
@@ -178,7 +194,8 @@ def test_adamw8bit_reference_vectors(L, golden):
 
 @pytest.mark.parametrize("block", [32, 64, 128, 256, 512, 1024, 2048, 4096])
 @pytest.mark.parametrize("mode", [O.NOISE_PHILOX8, O.NOISE_INJECT])
-def test_adamw8bit_blocks_vs_oracle(L, block, mode):
+@pytest.mark.parametrize("use_table", [True, False])
+def test_adamw8bit_blocks_vs_oracle(L, block, mode, use_table):
     rng = np.random.default_rng(block + mode)
     n = 5 * block + 77
     nb = (n + block - 1) // block
@@ -204,7 +221,8 @@ def test_adamw8bit_blocks_vs_oracle(L, block, mode):
         spec = O.NoiseSpec(mode, seed, 0, inj[:n] if mode == O.NOISE_INJECT else None)
         pe, s1, s2, a1, a2 = O.adamw8bit(pe, g0, s1, s2, a1, a2, Q1, Q2, block, True, *hyper, spec)
         inj_d = np_to_dev(inj.view(np.int16)) if mode == O.NOISE_INJECT else None
-        _adam8_call(L, pd, u16_to_dev(g0), s1d, s2d, a1d, a2d, q1, q2, n, block, True, hyper, seed, mode, inj_d)
+        _adam8_call(L, pd, u16_to_dev(g0), s1d, s2d, a1d, a2d, q1, q2, n, block, True, hyper, seed, mode, inj_d,
+                    qt=qtable_dev(L) if use_table else None)
         assert np.array_equal(dev_to_u16(pd), pe), step
         assert np.array_equal(s1d.cpu().numpy(), s1), step
         assert np.array_equal(s2d.cpu().numpy(), s2), step
@@ -228,7 +246,8 @@ def test_adamw8bit_unaligned_and_bf16_branch(L, mode):
     p, g = unaligned(u16_to_dev(p0)), unaligned(u16_to_dev(g0))
     s1, s2 = np_to_dev(np.full(n, 127, np.uint8)), np_to_dev(np.zeros(n, np.uint8))
     a1, a2 = np_to_dev(np.zeros(nb, np.float32)), np_to_dev(np.zeros(nb, np.float32))
-    _adam8_call(L, p, g, s1, s2, a1, a2, np_to_dev(Q1), np_to_dev(Q2), n, block, True, hyper, seed, mode)
+    _adam8_call(L, p, g, s1, s2, a1, a2, np_to_dev(Q1), np_to_dev(Q2), n, block, True, hyper, seed, mode,
+                qt=qtable_dev(L))
     assert np.array_equal(dev_to_u16(p), pe)
     assert np.array_equal(s1.cpu().numpy(), e1) and np.array_equal(s2.cpu().numpy(), e2)
     # bf16-moment branch (seed streams SEED, SEED+1 (wraps the i32 seed), SEED+2)
@@ -253,11 +272,59 @@ def test_quantizer_device_vs_oracle(L, golden):
                             (10.0 ** rng.uniform(-12, 0, 1 << 20)).astype(np.float32)
                             * (rng.choice([-1, 1], 1 << 20) if signed else 1)]).astype(np.float32)
         xd = np_to_dev(x)
-        out = torch.empty(x.size, dtype=torch.uint8, device=DEV)
-        check(L, L.msr_quantize(xd.data_ptr(), out.data_ptr(), x.size, np_to_dev(Q).data_ptr(), int(signed), stream()))
-        got = out.cpu().numpy()
-        assert np.array_equal(got[:z[f"x_{name}"].size], z[f"code_{name}"])
-        assert np.array_equal(got, O.quantize(x, Q, signed))
+        expect = O.quantize(x, Q, signed)
+        for qt in (None, qtable_dev(L)):
+            out = torch.empty(x.size, dtype=torch.uint8, device=DEV)
+            check(L, L.msr_quantize(xd.data_ptr(), out.data_ptr(), x.size, np_to_dev(Q).data_ptr(), int(signed),
+                                    ptr(qt), stream()))
+            got = out.cpu().numpy()
+            assert np.array_equal(got[:z[f"x_{name}"].size], z[f"code_{name}"])
+            assert np.array_equal(got, expect)
+
+
+def test_quant_table_exhaustive(L):
+    """The table equals the reference search for every float in [-1, 1], both maps."""
+    q1 = np_to_dev(O.create_dynamic_map(True))
+    q2 = np_to_dev(O.create_dynamic_map(False))
+    qt = qtable_dev(L)
+    nblk = 4096
+    counts = torch.zeros(nblk, dtype=torch.int32, device=DEV)
+    check(L, L.msr_quant_table_check(qt.data_ptr(), q1.data_ptr(), q2.data_ptr(), 0, 0x3F800000, counts.data_ptr(),
+                                     nblk, stream()), "table check")
+    assert int(counts.sum().item()) == 0
+
+
+def test_adamw8bit_extreme_moments(L):
+    """Huge gradients (v overflows to inf), denormal-scale moments and -0: the
+    exact-quotient and table paths against the oracle."""
+    Q1, Q2 = O.create_dynamic_map(True), O.create_dynamic_map(False)
+    n, block = 2048, 256
+    nb = n // block
+    rng = np.random.default_rng(17)
+    g = rng.standard_normal(n).astype(np.float32)
+    g[:256] *= 1e-30                 # tiny moments: quotients near the subnormal range
+    g[256:512] *= 3e19               # (1-b2) g^2 overflows to inf in some lanes
+    g[512:520] = -0.0
+    g[520:524] = [1e-38, -1e-38, 1e-45, -1e-45]
+    g0 = O.f32_to_bf16_rne(g)
+    p0 = O.f32_to_bf16_rne((rng.standard_normal(n) * 0.02).astype(np.float32))
+    hyper = (1e-3, 0.9, 0.999, 1e-8, 0.0, 0.1, 0.001)
+    for qt in (None, qtable_dev(L)):
+        pe, e1, e2, ea1, ea2 = O.adamw8bit(p0, g0, np.full(n, 127, np.uint8), np.zeros(n, np.uint8),
+                                           np.zeros(nb, np.float32), np.zeros(nb, np.float32), Q1, Q2, block, True,
+                                           *hyper, O.NoiseSpec(O.NOISE_TRITON, 99))
+        p, gd = u16_to_dev(p0), u16_to_dev(g0)
+        s1, s2 = np_to_dev(np.full(n, 127, np.uint8)), np_to_dev(np.zeros(n, np.uint8))
+        a1, a2 = np_to_dev(np.zeros(nb, np.float32)), np_to_dev(np.zeros(nb, np.float32))
+        _adam8_call(L, p, gd, s1, s2, a1, a2, np_to_dev(Q1), np_to_dev(Q2), n, block, True, hyper, 99,
+                    O.NOISE_TRITON, qt=qt)
+        assert np.array_equal(s1.cpu().numpy(), e1), "m codes"
+        assert np.array_equal(s2.cpu().numpy(), e2), "v codes"
+        assert np.array_equal(a1.cpu().numpy().view(np.uint32), ea1.view(np.uint32))
+        assert np.array_equal(a2.cpu().numpy().view(np.uint32), ea2.view(np.uint32))
+        got = dev_to_u16(p)
+        same = (got == pe) | (np.isnan(O.bf16_to_f32(got)) & np.isnan(O.bf16_to_f32(pe)))
+        assert same.all()
 
 
 # ---------------------------------------------------------------------------

@@ -33,20 +33,42 @@ def hipcc() -> str:
     return cand if os.path.exists(cand) else "hipcc"
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source into one shared library (always recompiles)."""
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *sources()]
+# Per-source extra flags.  The Newton-Schulz GEMM keeps its MFMA operands in
+# VGPRs (the AGPRs then serve as spill space), which removes all scratch
+# traffic from its K loop.
+EXTRA_FLAGS = {
+    "ns_gemm.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=true"],
+}
+
+_NOISE = "is not a recognized feature for this target"  # hipcc host pass; harmless
+
+
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    # hipcc's host pass does not know the packed-fp32 feature and says so; that is harmless.
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(line for line in res.stderr.splitlines() if noise not in line)
+    err = "\n".join(line for line in res.stderr.splitlines() if _NOISE not in line)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
     if verbose and err.strip():
         print(err)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP source (each with its own flags) and link one shared library.
+
+    Always recompiles; objects go to muon_sr_amd/_build/.
+    """
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    objs = []
+    for src in sources():
+        obj = os.path.join(objdir, os.path.basename(src) + ".o")
+        flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+        _run([hipcc(), *flags, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", "-o", obj, src], verbose)
+        objs.append(obj)
+    tmp = LIB + ".tmp"
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB)
     return LIB
 

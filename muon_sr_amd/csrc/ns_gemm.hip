@@ -14,10 +14,10 @@
 //
 // Kernel shape: 256 threads (4 wave64s in a 2x2 grid), a 256x256 output tile
 // per work-group, K staged through LDS in 64-wide slabs, double buffered
-// (2 x 64 KiB).  Each wave owns a 128x128 sub-tile = 4x4 tiles of the 32x32x16
-// bf16 MFMA (fp32 accumulators).  LDS rows are XOR-swizzled by (row & 7) in
-// 16-byte units so the fragment reads of 8 consecutive rows hit 8 distinct
-// bank groups.
+// (2 x 64 KiB) and filled by direct global->LDS loads one slab ahead.  Each
+// wave owns a 128x128 sub-tile = 4x4 tiles of the 32x32x16 bf16 MFMA (fp32
+// accumulators).  LDS rows are XOR-swizzled by (row & 7) in 16-byte units so
+// the fragment reads of 8 consecutive rows hit 8 distinct bank groups.
 #include "common.hpp"
 #include "../../include/muon_sr_amd.h"
 
@@ -44,6 +44,20 @@ struct GemmArgs {
     int d_vec;         // D rows allow 8-byte stores (set by launch_gemm)
 };
 
+// Work-group -> tile.  Consecutive work-group ids are dispatched round-robin
+// over the 8 XCDs (each with its own L2), so the id is first mapped to
+// (xcd, slot) and every XCD receives a contiguous range of the tile order;
+// inside a range, tiles go row-group by row-group (GROUP_M rows, then along
+// the columns), so the work-groups resident on one XCD share operand slabs.
+constexpr int NXCD = 8;
+constexpr int GROUP_M = 4;
+
+__device__ __forceinline__ int xcd_remap(int w, int total) {
+    const int per = total / NXCD;          // full rounds
+    if (w >= per * NXCD) return w;         // tail keeps its order
+    return (w % NXCD) * per + w / NXCD;
+}
+
 __device__ __forceinline__ void decode_tile(const GemmArgs &a, int t, int &ti, int &tj) {
     if (a.symmetric) {
         const int T = a.tiles_m;
@@ -56,44 +70,68 @@ __device__ __forceinline__ void decode_tile(const GemmArgs &a, int t, int &ti, i
         ti = row;
         tj = row + (t - start);
     } else {
-        ti = t / a.tiles_n;
-        tj = t - ti * a.tiles_n;
+        // grouped order: GROUP_M tile-rows at a time, column-major inside a group
+        const int per_group = GROUP_M * a.tiles_n;
+        const int g = t / per_group;
+        const int first = g * GROUP_M;
+        const int rows = min(GROUP_M, a.tiles_m - first);
+        const int r = t - g * per_group;
+        ti = first + r % rows;
+        tj = r / rows;
     }
 }
 
-__global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
-    __shared__ bf16x8_t smem[2][2][CHUNKS];  // [stage][P/Q][row*8 + swizzled chunk]
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef const __attribute__((address_space(1))) void global_void_t;
 
+// LDS slabs: one array per (stage, operand).
+__shared__ bf16x8_t g_sP0[CHUNKS], g_sQ0[CHUNKS], g_sP1[CHUNKS], g_sQ1[CHUNKS];
+
+// SYM: mirror off-diagonal tiles into D; HAS_C: beta * C term; OUT_D / OUT_DT:
+// write D[m][n] / DT[n][m].  Stores honour Mv / Nv and d_vec.
+template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT>
+__global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     int ti, tj;
-    decode_tile(a, blockIdx.x, ti, tj);
+    decode_tile(a, xcd_remap(blockIdx.x, gridDim.x), ti, tj);
     const int64_t bz = blockIdx.y;
     const int m0 = ti * BM, n0 = tj * BN;
-    const uint16_t *Pb = a.P + bz * a.sP + (int64_t)m0 * a.ldp;
-    const uint16_t *Qb = a.Q + bz * a.sQ + (int64_t)n0 * a.ldq;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
+    const int r32 = lane & 31;
+    const int khalf = lane >> 5;
 
-    bf16x8_t rp[8], rq[8];
-    const int lc = tid & 7;  // 16-byte chunk within the 64-wide K slab
-
-    auto gload = [&](int k0) {
+    // Global -> LDS without registers (global_load_lds_dwordx4): one
+    // instruction moves 64 lanes x 16 B into 1 KiB of consecutive LDS, lane l
+    // to byte 16 l.  Instruction i of wave w fills LDS chunks
+    // [(4 i + w) 64, +64) = rows (4 i + w) 8 + l / 8, physical chunk l % 8, so
+    // lane l fetches logical chunk (l % 8) ^ ((l / 8) & 7) of its row.
+    const int lrow = lane >> 3;
+    const int lchunk = (lane & 7) ^ (lrow & 7);
+    const uint16_t *Pl = a.P + bz * a.sP + (int64_t)(m0 + wave * 8 + lrow) * a.ldp + lchunk * 8;
+    const uint16_t *Ql = a.Q + bz * a.sQ + (int64_t)(n0 + wave * 8 + lrow) * a.ldq + lchunk * 8;
+    const int64_t pstep = 32 * a.ldp, qstep = 32 * a.ldq;  // 32 rows per instruction round
+    auto dma = [&](int k0, bf16x8_t *dP, bf16x8_t *dQ) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int row = (i * GEMM_THREADS + tid) >> 3;
-            rp[i] = *reinterpret_cast<const bf16x8_t *>(Pb + (int64_t)row * a.ldp + k0 + lc * 8);
-            rq[i] = *reinterpret_cast<const bf16x8_t *>(Qb + (int64_t)row * a.ldq + k0 + lc * 8);
+            const int base = (i * 4 + wave) * 64;
+            __builtin_amdgcn_global_load_lds((global_void_t *)(Pl + i * pstep + k0), (lds_void_t *)(dP + base), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void_t *)(Ql + i * qstep + k0), (lds_void_t *)(dQ + base), 16, 0, 0);
         }
     };
-    auto lstore = [&](int st) {
+    auto frags = [&](const bf16x8_t *sP, const bf16x8_t *sQ, int ks, bf16x8_t (&pa)[4], bf16x8_t (&qb)[4]) {
+        const int c = ks * 2 + khalf;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int row = (i * GEMM_THREADS + tid) >> 3;
-            const int idx = row * 8 + (lc ^ (row & 7));
-            smem[st][0][idx] = rp[i];
-            smem[st][1][idx] = rq[i];
+        for (int mi = 0; mi < 4; ++mi) {
+            const int row = wm * 128 + mi * 32 + r32;
+            pa[mi] = sP[row * 8 + (c ^ (row & 7))];
+        }
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            const int row = wn * 128 + ni * 32 + r32;
+            qb[ni] = sQ[row * 8 + (c ^ (row & 7))];
         }
     };
 
@@ -106,85 +144,88 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
     const int KT = a.K / BK;
-    gload(0);
-    lstore(0);
+    bf16x8_t fa[2][4], fb[2][4];
+    dma(0, g_sP0, g_sQ0);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    frags(g_sP0, g_sQ0, 0, fa[0], fb[0]);
 
-    const int r32 = lane & 31;
-    const int khalf = lane >> 5;
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) gload((kt + 1) * BK);
+    // One K slab from stage (sP, sQ) while the next slab streams into (nP, nQ);
+    // fragments of substep s+1 are read while substep s multiplies.
+    auto slab = [&](int kt, const bf16x8_t *sP, const bf16x8_t *sQ, bf16x8_t *nP, bf16x8_t *nQ) {
+        const bool has_next = kt + 1 < KT;
+        if (has_next) dma((kt + 1) * BK, nP, nQ);
 #pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            const int c = ks * 2 + khalf;
-            bf16x8_t pa[4], qb[4];
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) {
-                const int row = wm * 128 + mi * 32 + r32;
-                pa[mi] = smem[cur][0][row * 8 + (c ^ (row & 7))];
-            }
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) {
-                const int row = wn * 128 + ni * 32 + r32;
-                qb[ni] = smem[cur][1][row * 8 + (c ^ (row & 7))];
-            }
-            // MFMA A-operand = Q rows (n), B-operand = P rows (m): lane l then
-            // holds D[m = l % 32][n = 8r + 4(l / 32) + q] for accumulator 4r + q.
+        for (int ks = 0; ks < 4; ++ks) {
+            if (ks < 3) frags(sP, sQ, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
 #pragma unroll
             for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < 4; ++ni)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qb[ni], pa[mi], acc[mi][ni], 0, 0, 0);
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][ni], fa[ks & 1][mi],
+                                                                          acc[mi][ni], 0, 0, 0);
         }
-        if (kt + 1 < KT) lstore(cur ^ 1);
-        __syncthreads();
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next slab have landed
+        __syncthreads();                // ... and every wave's; the current stage is free
+        if (has_next) frags(nP, nQ, 0, fa[0], fb[0]);
+    };
+
+    for (int kt = 0; kt < KT; kt += 2) {
+        slab(kt, g_sP0, g_sQ0, g_sP1, g_sQ1);
+        if (kt + 1 < KT) slab(kt + 1, g_sP1, g_sQ1, g_sP0, g_sQ0);
     }
 
     // ---------------- epilogue ----------------
-    const bool mirror = a.symmetric && ti != tj;
+    // Lane l holds D[m = l % 32][n = 8r + 4(l / 32) + q] of each 32x32 tile.
+    // (Written with scalars: the array form of this loop spills registers.)
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
-        const int m = m0 + wm * 128 + mi * 32 + r32;
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
+                const int m = m0 + wm * 128 + mi * 32 + r32;
                 const int n = n0 + wn * 128 + ni * 32 + 8 * r + 4 * khalf;
-                float v[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = a.alpha * acc[mi][ni][4 * r + q];
-                if (a.C) {
+                float v0 = a.alpha * acc[mi][ni][4 * r], v1 = a.alpha * acc[mi][ni][4 * r + 1];
+                float v2 = a.alpha * acc[mi][ni][4 * r + 2], v3 = a.alpha * acc[mi][ni][4 * r + 3];
+                if constexpr (HAS_C) {
                     const uint2 cw = *reinterpret_cast<const uint2 *>(a.C + bz * a.sC + (int64_t)m * a.ldc + n);
-                    v[0] = v[0] + a.beta * bf16_lo(cw.x);
-                    v[1] = v[1] + a.beta * bf16_hi(cw.x);
-                    v[2] = v[2] + a.beta * bf16_lo(cw.y);
-                    v[3] = v[3] + a.beta * bf16_hi(cw.y);
+                    v0 = v0 + a.beta * bf16_lo(cw.x);
+                    v1 = v1 + a.beta * bf16_hi(cw.x);
+                    v2 = v2 + a.beta * bf16_lo(cw.y);
+                    v3 = v3 + a.beta * bf16_hi(cw.y);
                 }
-                uint32_t h[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) h[q] = rne_bf16(v[q]);
-                const bool m_ok = m < a.Mv;
-                if (a.D && m_ok) {
-                    uint16_t *dp = a.D + bz * a.sD + (int64_t)m * a.ldd + n;
-                    if (a.d_vec && n + 3 < a.Nv) {
-                        *reinterpret_cast<uint2 *>(dp) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
-                    } else {
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            if (n + q < a.Nv) dp[q] = (uint16_t)h[q];
+                const uint32_t h0 = rne_bf16(v0), h1 = rne_bf16(v1), h2 = rne_bf16(v2), h3 = rne_bf16(v3);
+                if constexpr (OUT_D) {
+                    if (m < a.Mv) {
+                        uint16_t *dp = a.D + bz * a.sD + (int64_t)m * a.ldd + n;
+                        if (a.d_vec && n + 3 < a.Nv) {
+                            *reinterpret_cast<uint2 *>(dp) = make_uint2(pack2(h0, h1), pack2(h2, h3));
+                        } else {
+                            if (n < a.Nv) dp[0] = (uint16_t)h0;
+                            if (n + 1 < a.Nv) dp[1] = (uint16_t)h1;
+                            if (n + 2 < a.Nv) dp[2] = (uint16_t)h2;
+                            if (n + 3 < a.Nv) dp[3] = (uint16_t)h3;
+                        }
+                    }
+                    if constexpr (SYM) {
+                        if (ti != tj) {  // mirror of an off-diagonal tile (M == N, no bounds)
+                            uint16_t *dp = a.D + bz * a.sD + (int64_t)n * a.ldd + m;
+                            dp[0] = (uint16_t)h0;
+                            dp[a.ldd] = (uint16_t)h1;
+                            dp[2 * a.ldd] = (uint16_t)h2;
+                            dp[3 * a.ldd] = (uint16_t)h3;
+                        }
                     }
                 }
-                if (mirror) {
-                    uint16_t *dp = a.D + bz * a.sD + (int64_t)n * a.ldd + m;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) dp[(int64_t)q * a.ldd] = (uint16_t)h[q];
-                }
-                if (a.DT && m_ok) {
-                    uint16_t *tp = a.DT + bz * a.sDT + (int64_t)n * a.lddt + m;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (n + q < a.Nv) tp[(int64_t)q * a.lddt] = (uint16_t)h[q];
+                if constexpr (OUT_DT) {
+                    if (m < a.Mv) {
+                        uint16_t *tp = a.DT + bz * a.sDT + (int64_t)n * a.lddt + m;
+                        if (n < a.Nv) tp[0] = (uint16_t)h0;
+                        if (n + 1 < a.Nv) tp[a.lddt] = (uint16_t)h1;
+                        if (n + 2 < a.Nv) tp[2 * a.lddt] = (uint16_t)h2;
+                        if (n + 3 < a.Nv) tp[3 * a.lddt] = (uint16_t)h3;
+                    }
                 }
             }
         }
@@ -297,7 +338,15 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
         if (ab.C) ab.C += b0 * a.sC;
         if (ab.D) ab.D += b0 * a.sD;
         if (ab.DT) ab.DT += b0 * a.sDT;
-        hipLaunchKernelGGL(gemm_nt_kernel, dim3((unsigned)tiles, (unsigned)nb), dim3(GEMM_THREADS), 0, s, ab);
+        const dim3 grid((unsigned)tiles, (unsigned)nb), block(GEMM_THREADS);
+        const bool c = ab.C != nullptr, d = ab.D != nullptr, dt = ab.DT != nullptr;
+        if (ab.symmetric && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false>), grid, block, 0, s, ab);
+        else if (ab.symmetric && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false>), grid, block, 0, s, ab);
+        else if (!ab.symmetric && c && d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, true>), grid, block, 0, s, ab);
+        else if (!ab.symmetric && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false>), grid, block, 0, s, ab);
+        else if (!ab.symmetric && c && !d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, false, true>), grid, block, 0, s, ab);
+        else if (!ab.symmetric && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false>), grid, block, 0, s, ab);
+        else { set_error("gemm: unsupported epilogue combination"); return MSR_ERR_ARG; }
         int rc = check_launch("gemm_nt_kernel");
         if (rc) return rc;
     }

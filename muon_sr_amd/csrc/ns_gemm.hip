@@ -16,8 +16,9 @@
 // per work-group, K staged through LDS in 64-wide slabs, double buffered
 // (2 x 64 KiB) and filled by direct global->LDS loads one slab ahead.  Each
 // wave owns a 128x128 sub-tile = 4x4 tiles of the 32x32x16 bf16 MFMA (fp32
-// accumulators).  LDS rows are XOR-swizzled by (row & 7) in 16-byte units so
-// the fragment reads of 8 consecutive rows hit 8 distinct bank groups.
+// accumulators).  LDS rows are 128 B; chunk c of row r is stored at
+// c ^ ((r >> 1) & 7), so the 16 consecutive rows of one 16-lane quarter of a
+// fragment read (256 B) cover all 64 banks once.
 #include "common.hpp"
 #include "../../include/muon_sr_amd.h"
 
@@ -106,10 +107,11 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     // Global -> LDS without registers (global_load_lds_dwordx4): one
     // instruction moves 64 lanes x 16 B into 1 KiB of consecutive LDS, lane l
     // to byte 16 l.  Instruction i of wave w fills LDS chunks
-    // [(4 i + w) 64, +64) = rows (4 i + w) 8 + l / 8, physical chunk l % 8, so
-    // lane l fetches logical chunk (l % 8) ^ ((l / 8) & 7) of its row.
+    // [(4 i + w) 64, +64) = rows r = (4 i + w) 8 + l / 8, physical chunk l % 8,
+    // so lane l fetches logical chunk (l % 8) ^ ((r >> 1) & 7)
+    // = (l % 8) ^ (4 (w & 1) + l / 16) of its row.
     const int lrow = lane >> 3;
-    const int lchunk = (lane & 7) ^ (lrow & 7);
+    const int lchunk = (lane & 7) ^ (4 * (wave & 1) + (lane >> 4));
     const uint16_t *Pl = a.P + bz * a.sP + (int64_t)(m0 + wave * 8 + lrow) * a.ldp + lchunk * 8;
     const uint16_t *Ql = a.Q + bz * a.sQ + (int64_t)(n0 + wave * 8 + lrow) * a.ldq + lchunk * 8;
     const int64_t pstep = 32 * a.ldp, qstep = 32 * a.ldq;  // 32 rows per instruction round
@@ -126,12 +128,12 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
             const int row = wm * 128 + mi * 32 + r32;
-            pa[mi] = sP[row * 8 + (c ^ (row & 7))];
+            pa[mi] = sP[row * 8 + (c ^ ((row >> 1) & 7))];
         }
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
             const int row = wn * 128 + ni * 32 + r32;
-            qb[ni] = sQ[row * 8 + (c ^ (row & 7))];
+            qb[ni] = sQ[row * 8 + (c ^ ((row >> 1) & 7))];
         }
     };
 

@@ -292,6 +292,36 @@ def bench_full(steps_timed, warmup):
     return out
 
 
+def copy_calibration():
+    """A plain device copy of known size (2^28 fp32: 1 GiB read + 1 GiB written per
+    launch).  Profiled with FETCH_SIZE / WRITE_SIZE, it gives the factor that turns
+    those counters into bytes on this GPU."""
+    import torch
+    n = 1 << 28
+    a = torch.ones(n, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    sync()
+    print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4,
+                      "launches": 3}), flush=True)
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "adamw8bit_2e28_hbm_traffic.txt")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the 8-bit kernel from the committed counter summary
+    (FETCH_SIZE and WRITE_SIZE passes, scaled by the copy calibration), or None."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("hbm_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -300,12 +330,17 @@ def main():
     ap.add_argument("--configs", default="adamw8bit,sr_accum,ns,full")
     ap.add_argument("--noise", default="philox8", choices=["philox8", "triton"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run the plain copy used to calibrate the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU: every box has one MI355X and the optimizer step "
                                    "has no multi-GPU path here; run with --gpus 1"}))
         sys.exit(2)
 
+    if args.copy_calibration:
+        copy_calibration()
+        return
     import torch
     import muon_sr_amd
     muon_sr_amd.set_sr_noise(args.noise)
@@ -349,7 +384,7 @@ def main():
                    "elements": N8, "block_size": 256, "lr": 3e-4, "betas": [0.9, 0.95], "eps": 1e-10,
                    "weight_decay": 0.01, "sr_noise": args.noise, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
                      "kernel": "adamw8bit_quant_kernel", "kernel_ms": round(r8["kernel_ms"], 4),
                      "bytes_per_launch": r8["bytes_per_step"]},
         "cpu_baseline": cpu,

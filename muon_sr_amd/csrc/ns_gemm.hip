@@ -238,25 +238,112 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
 // NS prologue: deterministic Frobenius norm and normalise + transpose
 // ---------------------------------------------------------------------------
 
-constexpr int NPART = 64;         // partial sums per matrix (fixed: deterministic order)
+constexpr int NPART = 128;        // partial sums per matrix (fixed: deterministic order)
 constexpr int NORM_THREADS = 256;
 
+// partial[b][part] = sum of squares over a fixed interleaved slice of matrix b.
+// VEC: 16-byte loads (numel % 8 == 0 and `in` 16-byte aligned), two loads in flight.
+template <bool VEC>
 __global__ __launch_bounds__(NORM_THREADS) void sumsq_kernel(const uint16_t *in, int64_t numel, float *partial) {
     const int64_t b = blockIdx.y;
     const uint16_t *x = in + b * numel;
-    float s = 0.0f;
-    for (int64_t i = (int64_t)blockIdx.x * NORM_THREADS + threadIdx.x; i < numel; i += (int64_t)NPART * NORM_THREADS) {
-        const float v = bf16_to_f32(x[i]);
-        s = s + v * v;
+    float s0 = 0.0f, s1 = 0.0f;
+    const int64_t stride = (int64_t)NPART * NORM_THREADS;
+    int64_t i = (int64_t)blockIdx.x * NORM_THREADS + threadIdx.x;
+    if constexpr (VEC) {
+        const uint4 *xv = reinterpret_cast<const uint4 *>(x);
+        const int64_t nv = numel >> 3;
+        auto acc8 = [](float s, uint4 w) {
+            const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float lo = __uint_as_float(u[k] << 16), hi = __uint_as_float(u[k] & 0xffff0000u);
+                s = s + lo * lo;
+                s = s + hi * hi;
+            }
+            return s;
+        };
+        for (; i + stride < nv; i += 2 * stride) {
+            const uint4 w0 = xv[i], w1 = xv[i + stride];
+            s0 = acc8(s0, w0);
+            s1 = acc8(s1, w1);
+        }
+        if (i < nv) s0 = acc8(s0, xv[i]);
+    } else {
+        for (; i < numel; i += stride) {
+            const float v = bf16_to_f32(x[i]);
+            s0 = s0 + v * v;
+        }
     }
     __shared__ float red[NORM_THREADS];
-    red[threadIdx.x] = s;
+    red[threadIdx.x] = s0 + s1;
     __syncthreads();
     for (int w = NORM_THREADS / 2; w > 0; w >>= 1) {
         if (threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
         __syncthreads();
     }
     if (threadIdx.x == 0) partial[b * NPART + blockIdx.x] = red[0];
+}
+
+// d = bf16(bf16(||u||_F) + 1e-7) from the partial sums of matrix b (fixed order).
+__device__ __forceinline__ float norm_divisor(const float *partial, int64_t b) {
+    float s = 0.0f;
+    for (int i = 0; i < NPART; ++i) s = s + partial[b * NPART + i];
+    const float nrm = __uint_as_float(rne_bf16(sqrtf(s)) << 16);
+    return __uint_as_float(rne_bf16(nrm + 1e-7f) << 16);
+}
+
+// Vector form of normalize_kernel (below) for cols % 8 == 0 with 16-byte aligned
+// `in`, S and T rows: each thread moves 8 consecutive bf16 (16 bytes) per access.
+// Rp and Cp are multiples of 8 here, so an 8-wide chunk is entirely inside or
+// entirely outside every extent it is checked against.
+__global__ __launch_bounds__(256) void normalize_vec_kernel(const uint16_t *in, int64_t rows, int64_t cols,
+                                                            const float *partial, uint16_t *S, int64_t ldS,
+                                                            int64_t sS, uint16_t *T, int64_t ldT, int64_t sT,
+                                                            int64_t Rp, int64_t Cp) {
+    __shared__ __align__(16) uint16_t tile[64][72];
+    __shared__ float dsh;
+    const int64_t b = blockIdx.z;
+    if (threadIdx.x == 0) dsh = norm_divisor(partial, b);
+    __syncthreads();
+    const float d = dsh;
+    const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+    const uint16_t *x = in + b * rows * cols;
+    const int j = threadIdx.x & 7, i0 = threadIdx.x >> 3;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = i0 + 32 * h;
+        const int64_t r = r0 + i, c = c0 + 8 * j;
+        uint4 w = make_uint4(0u, 0u, 0u, 0u);
+        if (r < rows && c < cols) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(x + r * cols + c);
+            const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t lo = rne_bf16(__uint_as_float(u[k] << 16) / d);
+                const uint32_t hi = rne_bf16(__uint_as_float(u[k] & 0xffff0000u) / d);
+                o[k] = lo | (hi << 16);
+            }
+            w = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+        *reinterpret_cast<uint4 *>(&tile[i][8 * j]) = w;
+        if (S && r < Rp && c < Cp) *reinterpret_cast<uint4 *>(S + b * sS + r * ldS + c) = w;
+    }
+    if (!T) return;
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int cc = i0 + 32 * h;            // T row (input column) within the tile
+        const int64_t c = c0 + cc, r = r0 + 8 * j;
+        if (c < Cp && r < Rp) {
+            uint32_t o[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                o[k] = (uint32_t)tile[8 * j + 2 * k][cc] | ((uint32_t)tile[8 * j + 2 * k + 1][cc] << 16);
+            *reinterpret_cast<uint4 *>(T + b * sT + c * ldT + r) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+    }
 }
 
 // Writes S = x0 in the input layout (Rp x Cp, ld ldS) and T = x0^T (Cp x Rp, ld ldT),
@@ -269,12 +356,7 @@ __global__ __launch_bounds__(256) void normalize_kernel(const uint16_t *in, int6
     __shared__ uint16_t tile[64][66];
     __shared__ float dsh;
     const int64_t b = blockIdx.z;
-    if (threadIdx.x == 0) {
-        float s = 0.0f;
-        for (int i = 0; i < NPART; ++i) s = s + partial[b * NPART + i];
-        const float nrm = __uint_as_float(rne_bf16(sqrtf(s)) << 16);
-        dsh = __uint_as_float(rne_bf16(nrm + 1e-7f) << 16);
-    }
+    if (threadIdx.x == 0) dsh = norm_divisor(partial, b);
     __syncthreads();
     const float d = dsh;
     const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
@@ -413,26 +495,40 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
     const int64_t numel = rows * cols;
     const int64_t xs = L.mp * L.np, as = L.mp * L.mp;
 
-    hipLaunchKernelGGL(sumsq_kernel, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
+    // 16-byte accesses when every row of the input starts 16-byte aligned
+    const bool vec = (cols % 8) == 0 && aligned(in, 16);
+    if (vec)
+        hipLaunchKernelGGL(sumsq_kernel<true>, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
+    else
+        hipLaunchKernelGGL(sumsq_kernel<false>, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
     int rc = check_launch("sumsq_kernel");
     if (rc) return rc;
+    auto normalize = [&](dim3 grid, uint16_t *S, int64_t ldS, int64_t sS, uint16_t *T, int64_t ldT, int64_t sT,
+                         int64_t Rp, int64_t Cp) {
+        const bool v = vec && aligned(S, 16) && (!T || aligned(T, 16)) && ldS % 8 == 0 && sS % 8 == 0 &&
+                       ldT % 8 == 0 && sT % 8 == 0 && Rp % 8 == 0 && Cp % 8 == 0;
+        if (v)
+            hipLaunchKernelGGL(normalize_vec_kernel, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, T, ldT,
+                               sT, Rp, Cp);
+        else
+            hipLaunchKernelGGL(normalize_kernel, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, T, ldT, sT,
+                               Rp, Cp);
+        return check_launch("normalize_kernel");
+    };
 
     // Padded extents of the input layout: wide -> X is (mp x np); tall -> XT is (np x mp).
     const int64_t Rp = L.transposed ? L.np : L.mp;
     const int64_t Cp = L.transposed ? L.mp : L.np;
     if (steps == 0) {
-        hipLaunchKernelGGL(normalize_kernel, dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch),
-                           dim3(256), 0, s, in, rows, cols, part, out, cols, numel, (uint16_t *)nullptr, (int64_t)0,
-                           (int64_t)0, rows, cols);
-        return check_launch("normalize_kernel");
+        return normalize(dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch), out, cols,
+                         numel, nullptr, 0, 0, rows, cols);
     }
     uint16_t *Sx = L.transposed ? XT[0] : X[0];
     uint16_t *Tx = L.transposed ? X[0] : XT[0];
     const int64_t ldS = Cp, ldT = Rp;
-    hipLaunchKernelGGL(normalize_kernel, dim3((unsigned)(Cp / 64), (unsigned)(Rp / 64), (unsigned)batch), dim3(256), 0, s,
-                       in, rows, cols, part, Sx, ldS, xs, Tx, ldT, xs, Rp, Cp);
-    rc = check_launch("normalize_kernel");
-    if (rc) return rc;
+    if ((rc = normalize(dim3((unsigned)(Cp / 64), (unsigned)(Rp / 64), (unsigned)batch), Sx, ldS, xs, Tx, ldT, xs, Rp,
+                        Cp)))
+        return rc;
 
     const int mp = (int)L.mp, np = (int)L.np;
     int cur = 0;

@@ -451,6 +451,30 @@ def test_newton_schulz_vs_fp32(L, shape):
     assert e_exact <= e_ref + 2e-3   # at least as close to exact NS as the reference's bf16 op sequence
 
 
+@pytest.mark.parametrize("shape,offset", [((2, 192, 320), 0), ((3, 61, 99), 0), ((2, 320, 128), 0),
+                                          ((2, 192, 320), 1), ((1, 1024, 4096), 0)])
+def test_ns_normalize_exact(L, shape, offset):
+    """steps=0 returns bf16(G / d), d = bf16(bf16(||G||_F) + 1e-7), for the 16-byte and
+    the element-wise prologue (offset 1 makes the input pointer unaligned)."""
+    from muon_sr_amd.muon import newton_schulz
+    torch.manual_seed(7)
+    n = int(np.prod(shape))
+    flat = (torch.randn(n + offset) * 3e-3).to(torch.bfloat16)
+    G = flat[offset:].view(shape)
+    Gd = flat.to(DEV)[offset:].view(shape)
+    X0 = newton_schulz(Gd, steps=0).cpu()
+    g64 = G.double()
+    nrm = g64.pow(2).sum(dim=(-2, -1), keepdim=True).sqrt()
+    nb = nrm.float().to(torch.bfloat16).double()
+    # the device sums in fp32 in its own order: keep clear of bf16 rounding ties of the norm
+    ulp = torch.ldexp(torch.ones_like(nb), torch.frexp(nb).exponent - 8)   # bf16 spacing at nb
+    mid = (nrm - nb).abs() - ulp / 2
+    assert bool((mid.abs() > 1e-4 * nb).all()), "input too close to a bf16 rounding boundary of the norm"
+    d = (nb.float() + 1e-7).to(torch.bfloat16).float()
+    exp = (G.float() / d).to(torch.bfloat16)
+    assert torch.equal(X0.view(torch.int16), exp.view(torch.int16))
+
+
 def test_newton_schulz_batch_invariant_and_steps0(L):
     from muon_sr_amd.muon import newton_schulz
     torch.manual_seed(0)

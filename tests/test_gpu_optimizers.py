@@ -1,0 +1,404 @@
+"""GPU parity of the drop-in optimizer classes against the reference.
+
+The reference's own trajectories (tests/golden/ns_traj.npz, written by
+tests/golden/make_golden.py from bab2min/muon_sr 0.1.2's classes) pin the
+composed steps: seeds, parameter indexing, shape grouping, state keys.  With
+the reference's noise stream selected (``set_sr_noise("triton")``) every
+stochastically rounded tensor that does not pass through Newton-Schulz must be
+bit-identical; Muon parameters move by the Newton-Schulz output, which is a
+floating-point product computed differently (fp32-accumulating MFMA vs the
+reference's torch bf16 matmuls), and are compared through their step deltas.
+
+With this library's own Philox8 stream, results stay within 1 bf16 ulp of the
+reference-noise result per element, and the rounding is unbiased.
+"""
+import copy
+import random
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from _gpu import DEV, check, dev_to_u16, need_gpu, rel_fro, stream, u16_to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def L():
+    return need_gpu()
+
+
+@pytest.fixture
+def noise():
+    """Select the SR noise stream for one test and restore it afterwards."""
+    import muon_sr_amd
+    old = muon_sr_amd.get_sr_noise()
+    yield muon_sr_amd.set_sr_noise
+    muon_sr_amd.set_sr_noise(old)
+
+
+def u16_abs_ulps(a, b):
+    """Distance in bf16 ulps between bit patterns of equal sign (inf if signs differ)."""
+    a = a.astype(np.int64)
+    b = b.astype(np.int64)
+    same = (a >> 15) == (b >> 15)
+    d = np.abs((a & 0x7fff) - (b & 0x7fff))
+    return np.where(same | ((a & 0x7fff) == 0) & ((b & 0x7fff) == 0), d, 1 << 20)
+
+
+def step_delta(z, key, step, p_prev, p_now):
+    """(our step delta, the reference's step delta) of one parameter."""
+    ref_prev = torch.from_numpy(z[f"{key}_{step - 1}"].view(np.int16).copy()).view(torch.bfloat16).float()
+    ref = torch.from_numpy(z[f"{key}_{step}"].view(np.int16).copy()).view(torch.bfloat16).float()
+    return p_now.detach().float().cpu() - p_prev, ref - ref_prev
+
+
+# ---------------------------------------------------------------------------
+# TritonAdamW: the reference's 3-step trajectory (two groups, a missing grad)
+# ---------------------------------------------------------------------------
+
+def test_triton_adamw_reference_trajectory(L, golden, noise):
+    from muon_sr_amd import TritonAdamW
+    noise("triton")
+    z = golden("ns_traj")
+    ps = [torch.nn.Parameter(u16_to_dev(z[f"traj_adamw/p{j}_0"])) for j in range(3)]
+    opt = TritonAdamW([{"params": ps[:2]}, {"params": ps[2:], "lr": 2e-3, "weight_decay": 0.1}],
+                      lr=1e-3, betas=(0.9, 0.95), eps=1e-8)
+    for step in range(1, 4):
+        for j, p in enumerate(ps):
+            g = z[f"traj_adamw/g{j}_{step}"]
+            p.grad = u16_to_dev(g).view(p.shape) if g.size else None
+        opt.step()
+        for j, p in enumerate(ps):
+            st = opt.state[p]
+            assert np.array_equal(dev_to_u16(p.data), z[f"traj_adamw/p{j}_{step}"]), (step, j)
+            assert np.array_equal(dev_to_u16(st["ema"]), z[f"traj_adamw/e{j}_{step}"]), (step, j)
+            assert np.array_equal(dev_to_u16(st["ema_squared"]), z[f"traj_adamw/s{j}_{step}"]), (step, j)
+
+
+# ---------------------------------------------------------------------------
+# Muon: batch_ns trajectory and the hybrid without batch_ns
+# ---------------------------------------------------------------------------
+
+# Tolerance on the relative Frobenius distance between the two step deltas.
+# Two parts: the reference's bf16 Newton-Schulz is itself 2-3% away from exact
+# NS on these inputs (this library's is closer), and a small difference in the
+# value before stochastic rounding flips a whole-ulp rounding decision with
+# probability proportional to that difference, although the noise bits are the
+# same.  At these magnitudes a step moves a weight by about 25 ulps, so the
+# flips add a few percent more.
+MUON_DELTA_TOL = 1e-1
+
+
+def _check_muon_param(z, tag, j, step, p_prev, p):
+    d_ours, d_ref = step_delta(z, f"{tag}/p{j}", step, p_prev, p)
+    e = rel_fro(d_ours, d_ref)
+    print(f"{tag} param {j} step {step}: step-delta rel Frobenius {e:.3e}")
+    assert e < MUON_DELTA_TOL, (tag, j, step, e)
+
+
+@pytest.mark.parametrize("tag", ["muon_batch", "hybrid_nobatch"])
+def test_muon_reference_trajectory(L, golden, noise, tag):
+    from muon_sr_amd import TritonMuonSR, TritonMuonSRWithAuxAdam
+    noise("triton")
+    z = golden("ns_traj")
+    nparams = 5 if tag == "hybrid_nobatch" else 3
+    ps = [torch.nn.Parameter(u16_to_dev(z[f"{tag}/p{j}_0"]).view(*z[f"{tag}/shape{j}"].tolist()))
+          for j in range(nparams)]
+    if tag == "muon_batch":
+        opt = TritonMuonSR(ps, lr=0.02, weight_decay=0.01, batch_ns=True)
+    else:
+        opt = TritonMuonSRWithAuxAdam(
+            [{"params": ps[:3], "use_muon": True, "weight_decay": 0.01},
+             {"params": ps[3:], "use_muon": False, "lr": 3e-4, "betas": (0.9, 0.95), "eps": 1e-10}],
+            batch_ns=False)
+    for step in range(1, 3):
+        for j, p in enumerate(ps):
+            p.grad = u16_to_dev(z[f"{tag}/g{j}_{step}"]).view(p.shape)
+        prev = [p.detach().float().cpu() for p in ps]
+        opt.step()
+        for j, p in enumerate(ps):
+            st = opt.state[p]
+            if f"{tag}/buf{j}_{step}" in z:
+                # momentum: SR of (buf, grad) only -> bit-exact with the reference noise
+                assert np.array_equal(dev_to_u16(st["momentum_buffer"]), z[f"{tag}/buf{j}_{step}"]), (step, j)
+                _check_muon_param(z, tag, j, step, prev[j], p)
+            else:
+                assert np.array_equal(dev_to_u16(p.data), z[f"{tag}/p{j}_{step}"]), (step, j)
+                assert np.array_equal(dev_to_u16(st["ema"]), z[f"{tag}/e{j}_{step}"]), (step, j)
+                assert np.array_equal(dev_to_u16(st["ema_squared"]), z[f"{tag}/s{j}_{step}"]), (step, j)
+
+
+# ---------------------------------------------------------------------------
+# TritonAdamW8bit: multi-step, 8-bit and 16-bit states, against the oracle
+# ---------------------------------------------------------------------------
+
+def _oracle_8bit_chain(p0, grads, block, quantized, lr, b1, b2, eps, wd, idx, mode):
+    n = p0.size
+    nb = -(-n // block)
+    Q1, Q2 = O.create_dynamic_map(True), O.create_dynamic_map(False)
+    p = p0
+    if quantized:
+        s1, s2 = np.full(n, 127, np.uint8), np.zeros(n, np.uint8)
+        a1, a2 = np.zeros(nb, np.float32), np.zeros(nb, np.float32)
+    else:
+        s1, s2 = np.zeros(n, np.uint16), np.zeros(n, np.uint16)
+    out = []
+    for step, g in enumerate(grads, start=1):
+        seed = O.deterministic_seed(step, idx)
+        bc1, bc2 = 1 - b1 ** step, 1 - b2 ** step
+        if quantized:
+            p, s1, s2, a1, a2 = O.adamw8bit(p, g, s1, s2, a1, a2, Q1, Q2, block, True, lr, b1, b2, eps, wd,
+                                            bc1, bc2, O.NoiseSpec(mode, seed))
+            out.append((p, s1, s2, a1, a2))
+        else:
+            p, s1, s2 = O.adamw8bit(p, g, s1, s2, None, None, None, None, block, False, lr, b1, b2, eps, wd,
+                                    bc1, bc2, O.NoiseSpec(mode, seed), O.NoiseSpec(mode, seed, 1),
+                                    O.NoiseSpec(mode, seed, 2))
+            out.append((p, s1, s2))
+    return out
+
+
+@pytest.mark.parametrize("mode_name", ["triton", "philox8"])
+def test_adamw8bit_class_vs_oracle(L, noise, mode_name):
+    from muon_sr_amd import TritonAdamW8bit
+    noise(mode_name)
+    mode = O.NOISE_TRITON if mode_name == "triton" else O.NOISE_PHILOX8
+    rng = np.random.default_rng(11)
+    shapes = [(70, 100), (300,), (33, 129)]     # 8-bit, 16-bit (< min_8bit_size), 8-bit ragged last block
+    p0 = [O.f32_to_bf16_rne((rng.standard_normal(int(np.prod(s))) * 0.02).astype(np.float32)) for s in shapes]
+    grads = [[O.f32_to_bf16_rne((rng.standard_normal(x.size) * 1e-3).astype(np.float32)) for _ in range(3)]
+             for x in p0]
+    ps = [torch.nn.Parameter(u16_to_dev(x).view(s)) for x, s in zip(p0, shapes)]
+    hyper = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-10, weight_decay=0.01)
+    opt = TritonAdamW8bit(ps, **hyper)
+    for step in range(3):
+        for p, gs in zip(ps, grads):
+            p.grad = u16_to_dev(gs[step]).view(p.shape)
+        opt.step()
+    for idx, (p, x, gs) in enumerate(zip(ps, p0, grads)):
+        quant = x.size >= 4096
+        exp = _oracle_8bit_chain(x, gs, 256, quant, 3e-4, 0.9, 0.95, 1e-10, 0.01, idx, mode)[-1]
+        st = opt.state[p]
+        assert st["optim_bits"] == (8 if quant else 16)
+        assert np.array_equal(dev_to_u16(p.data).ravel(), exp[0]), idx
+        if quant:
+            assert np.array_equal(st["state1"].cpu().numpy().ravel(), exp[1]), idx
+            assert np.array_equal(st["state2"].cpu().numpy().ravel(), exp[2]), idx
+            assert np.array_equal(st["absmax1"].cpu().numpy(), exp[3]), idx
+            assert np.array_equal(st["absmax2"].cpu().numpy(), exp[4]), idx
+        else:
+            assert np.array_equal(dev_to_u16(st["state1"]).ravel(), exp[1]), idx
+            assert np.array_equal(dev_to_u16(st["state2"]).ravel(), exp[2]), idx
+
+
+def test_adamw8bit_state_dict_round_trip(L):
+    """Resume from state_dict(): the next step equals the uninterrupted one
+    (muon_sr/triton_adamw_8bit.py:207-241 format_version 2)."""
+    from muon_sr_amd import TritonAdamW8bit
+    torch.manual_seed(5)
+    base = [(torch.randn(64, 96) * 0.02).to(torch.bfloat16), (torch.randn(200) * 0.02).to(torch.bfloat16)]
+    grads = [[(torch.randn(t.shape) * 1e-3).to(torch.bfloat16) for t in base] for _ in range(3)]
+
+    def make():
+        ps = [torch.nn.Parameter(t.clone().to(DEV)) for t in base]
+        return ps, TritonAdamW8bit(ps, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+
+    pa, oa = make()
+    for s in range(2):
+        for p, g in zip(pa, grads[s]):
+            p.grad = g.to(DEV)
+        oa.step()
+    sd = copy.deepcopy(oa.state_dict())
+    pb, ob = make()
+    for p, q in zip(pb, pa):
+        p.data.copy_(q.data)
+    ob.load_state_dict(sd)
+    for opt, ps in ((oa, pa), (ob, pb)):
+        for p, g in zip(ps, grads[2]):
+            p.grad = g.to(DEV)
+        opt.step()
+    for p, q in zip(pa, pb):
+        assert torch.equal(p.data, q.data)
+        for k in oa.state[p]:
+            a, b = oa.state[p][k], ob.state[q][k]
+            assert (torch.equal(a, b) if torch.is_tensor(a) else a == b), k
+    assert ob.state[pb[0]]["state1"].dtype == torch.uint8 and ob.state[pb[1]]["state1"].dtype == torch.bfloat16
+
+
+def test_muon_batch_state_dict_round_trip(L):
+    """batch_ns resume: stacks are rebuilt from the restored per-param momenta
+    and the global step is restored (muon_sr/muon_sr.py:149-158)."""
+    from muon_sr_amd import TritonMuonSR
+    torch.manual_seed(6)
+    shapes = [(64, 96), (96, 64), (64, 96)]
+    base = [(torch.randn(s) * 0.02).to(torch.bfloat16) for s in shapes]
+    grads = [[(torch.randn(s) * 1e-3).to(torch.bfloat16) for s in shapes] for _ in range(3)]
+
+    def make():
+        ps = [torch.nn.Parameter(t.clone().to(DEV)) for t in base]
+        return ps, TritonMuonSR(ps, lr=0.02, weight_decay=0.01, batch_ns=True)
+
+    pa, oa = make()
+    for s in range(2):
+        for p, g in zip(pa, grads[s]):
+            p.grad = g.to(DEV)
+        oa.step()
+    # a saved checkpoint does not alias the live stacks (state_dict() returns views of them)
+    sd = copy.deepcopy(oa.state_dict())
+    pb, ob = make()
+    for p, q in zip(pb, pa):
+        p.data.copy_(q.data)
+    ob.load_state_dict(sd)
+    for opt, ps in ((oa, pa), (ob, pb)):
+        for p, g in zip(ps, grads[2]):
+            p.grad = g.to(DEV)
+        opt.step()
+    for p, q in zip(pa, pb):
+        assert torch.equal(p.data, q.data)
+        assert torch.equal(oa.state[p]["momentum_buffer"], ob.state[q]["momentum_buffer"])
+        assert ob.state[q]["step"] == 3
+
+
+# ---------------------------------------------------------------------------
+# TritonSRAccumulator: hooks through a real backward, against the oracle
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("mode_name", ["triton", "philox8"])
+def test_sr_accumulator_hooks_vs_oracle(L, noise, mode_name):
+    from muon_sr_amd import TritonSRAccumulator
+    noise(mode_name)
+    mode = O.NOISE_TRITON if mode_name == "triton" else O.NOISE_PHILOX8
+    torch.manual_seed(9)
+    model = torch.nn.Sequential(torch.nn.Linear(64, 200), torch.nn.GELU(), torch.nn.Linear(200, 7))
+    model = model.to(device=DEV, dtype=torch.bfloat16)
+    seen = []      # (param name, grad bits) in hook order, captured before the accumulator runs
+    names = {id(p): n for n, p in model.named_parameters()}
+    capture = [p.register_post_accumulate_grad_hook(lambda p: seen.append((names[id(p)], dev_to_u16(p.grad))))
+               for p in model.parameters()]
+    hooks = TritonSRAccumulator.assign_hooks(model)
+    assert len(hooks) == 4
+    random.seed(1234)
+    for mb in range(3):
+        x = torch.randn(16, 64, device=DEV, dtype=torch.bfloat16)
+        model(x).float().square().mean().backward()
+        for p in model.parameters():
+            assert p.grad is None and hasattr(p, "acc_grad")
+    TritonSRAccumulator.reassign_grad_buffer(model)
+    # replay: one getrandbits(32) per hook call, in hook order
+    rs = random.Random(1234)
+    acc = {}
+    for name, g in seen:
+        seed = rs.getrandbits(32)
+        prev = acc.get(name, np.zeros_like(g))
+        acc[name] = O.sr_accum(prev, g, O.NoiseSpec(mode, seed))
+    assert len(seen) == 12
+    for name, p in model.named_parameters():
+        assert not hasattr(p, "acc_grad")
+        assert np.array_equal(dev_to_u16(p.grad).ravel(), acc[name].ravel()), name
+    for h in hooks + capture:
+        h.remove()
+
+
+# ---------------------------------------------------------------------------
+# Own RNG: within 1 ulp of the reference-noise result, and unbiased
+# ---------------------------------------------------------------------------
+
+def test_own_rng_within_one_ulp(L):
+    """One step of each SR kernel with the Philox8 stream vs the oracle with the
+    reference's stream: every rounded element differs by at most 1 bf16 ulp;
+    8-bit codes and block scales (not stochastically rounded) are identical."""
+    rng = np.random.default_rng(21)
+    n, block = 50_000, 256
+    nb = -(-n // block)
+    p = O.f32_to_bf16_rne((rng.standard_normal(n) * 0.02).astype(np.float32))
+    g = O.f32_to_bf16_rne((rng.standard_normal(n) * 1e-3).astype(np.float32))
+    Q1, Q2 = O.create_dynamic_map(True), O.create_dynamic_map(False)
+    s1 = rng.integers(0, 256, n).astype(np.uint8)
+    s2 = rng.integers(0, 256, n).astype(np.uint8)
+    a1 = np.abs(rng.standard_normal(nb)).astype(np.float32) * 1e-3
+    a2 = np.abs(rng.standard_normal(nb)).astype(np.float32) * 1e-6
+    hyper = (3e-4, 0.9, 0.95, 1e-10, 0.01, 1 - 0.9 ** 4, 1 - 0.95 ** 4)
+    seed = 987654321
+    exp = O.adamw8bit(p, g, s1, s2, a1, a2, Q1, Q2, block, True, *hyper, O.NoiseSpec(O.NOISE_TRITON, seed))
+    td = [u16_to_dev(p), u16_to_dev(g)] + [torch.from_numpy(x.copy()).to(DEV) for x in (s1, s2, a1, a2, Q1, Q2)]
+    check(L, L.msr_adamw8bit_step(*[t.data_ptr() for t in td], None, n, block, 1, *[float(np.float32(h)) for h in hyper],
+                                  seed, O.NOISE_PHILOX8, None, stream()))
+    assert u16_abs_ulps(dev_to_u16(td[0]), exp[0]).max() <= 1
+    for t, e in zip(td[2:6], exp[1:]):
+        assert np.array_equal(t.cpu().numpy(), e)
+    # bf16-moment AdamW: p, ema, ema_sq each within 1 ulp
+    e0 = O.f32_to_bf16_rne((rng.standard_normal(n) * 1e-3).astype(np.float32))
+    v0 = O.f32_to_bf16_rne((np.abs(rng.standard_normal(n)) * 1e-6).astype(np.float32))
+    bc, bcs = O.adamw_bias_corrections(0.9, 0.999, 3)
+    ns = [O.NoiseSpec(O.NOISE_TRITON, seed, k) for k in range(3)]   # ema, ema_sq, p
+    exp = O.adamw_bf16(p, g, e0, v0, 1e-3, 0.9, 0.999, 1e-8, 0.1, bc, bcs, *ns)
+    tp, tg, te, tv = (u16_to_dev(x) for x in (p, g, e0, v0))
+    check(L, L.msr_adamw_bf16_step(tp.data_ptr(), tg.data_ptr(), te.data_ptr(), tv.data_ptr(), n, 1e-3, 0.9, 0.999,
+                                   1e-8, 0.1, bc, bcs, seed, O.NOISE_PHILOX8, None, stream()))
+    for t, e in zip((tp, te, tv), exp):
+        assert u16_abs_ulps(dev_to_u16(t), e).max() <= 1
+
+
+@pytest.mark.parametrize("mode", [O.NOISE_TRITON, O.NOISE_PHILOX8])
+def test_sr_unbiased(L, mode):
+    """Mean of 10^4 stochastic roundings of a + g (a = 1.0, g a fraction of the
+    bf16 ulp there) is within 3 sigma of the exact fp32 sum."""
+    draws = 10_000
+    fracs = [1, 5, 8, 13]                       # sixteenths of the ulp at 1.0 (2^-7)
+    ulp = 2.0 ** -7
+    g = np.concatenate([np.full(draws, np.float32(f * ulp / 16)) for f in fracs]).astype(np.float32)
+    acc0 = np.full(g.size, O.f32_to_bf16_rne(np.float32([1.0]))[0], np.uint16)
+    acc = u16_to_dev(acc0)
+    gd = torch.from_numpy(g).to(DEV)
+    check(L, L.msr_sr_accum(acc.data_ptr(), gd.data_ptr(), 1, g.size, 4242, 0, mode, None, stream()))
+    out = O.bf16_to_f32(dev_to_u16(acc)).astype(np.float64)
+    for i, f in enumerate(fracs):
+        x = out[i * draws:(i + 1) * draws]
+        t = 1.0 + f * ulp / 16
+        prob = f / 16
+        assert set(np.unique(x)) <= {1.0, 1.0 + ulp}
+        sigma = ulp * np.sqrt(prob * (1 - prob) / draws)
+        assert abs(x.mean() - t) <= 3 * sigma, (f, x.mean() - t, sigma)
+
+
+# ---------------------------------------------------------------------------
+# Llama-3-8B shapes: NS at the real matrix shapes vs a same-op fp32 reference
+# ---------------------------------------------------------------------------
+
+def _ns_same_op_fp32_gpu(G):
+    """fp32 products on the GPU with bf16 storage between them, as the kernel
+    stores X, A and B; TF32 disabled."""
+    a, b, c = O.NS_COEFFS
+    rb = lambda x: x.to(torch.bfloat16).float()  # noqa: E731
+    X = G.float()
+    tr = X.size(-2) > X.size(-1)
+    if tr:
+        X = X.mT.contiguous()
+    nrm = rb(X.norm(dim=(-2, -1), keepdim=True))
+    X = rb(X / rb(nrm + 1e-7))
+    for _ in range(5):
+        A = rb(X @ X.mT.contiguous())
+        B = rb(c * (A @ A) + b * A)
+        X = rb((B @ X) + a * X)
+    return X.mT if tr else X
+
+
+@pytest.mark.parametrize("shape", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
+def test_newton_schulz_llama_shapes(L, shape):
+    from muon_sr_amd.muon import newton_schulz
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        gen = torch.Generator(device=DEV)
+        gen.manual_seed(sum(shape))
+        G = (torch.randn(*shape, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16)
+        out = newton_schulz(G)
+        ref = _ns_same_op_fp32_gpu(G)
+        e = rel_fro(out.float(), ref)
+        print(f"NS {shape}: rel Frobenius vs same-op fp32 {e:.3e}")
+        assert e < 1e-2
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev

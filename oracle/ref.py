@@ -25,6 +25,7 @@ __all__ = [
     "create_dynamic_map", "quantize", "deterministic_seed",
     "sr_accum", "adamw_bf16", "adamw8bit", "muon_prepare", "muon_apply",
     "adamw_bias_corrections", "ns_fp32", "ns_bf16_torch", "ns_scalar_map", "NS_COEFFS", "NoiseSpec",
+    "NS_CHUNK_NUMEL", "ns_scale", "muon_batch_step", "muon_param_step",
 ]
 
 
@@ -247,6 +248,72 @@ def muon_apply(p, upd, lr, weight_decay, scale, noise: NoiseSpec):
     upd = np.ascontiguousarray(upd, dtype=np.uint16)
     lib().orc_muon_apply(_ptr(p), _ptr(upd), p.size, _f(lr), _f(weight_decay), _f(scale), noise.ref())
     return p
+
+
+# ---------------------------------------------------------------------------
+# Muon step composition (seeds, stacking, chunking, scale)
+# ---------------------------------------------------------------------------
+
+NS_CHUNK_NUMEL = 1 << 28
+
+
+def ns_scale(shape) -> float:
+    """muon_sr/triton_muon_sr.py:101-102."""
+    return max(1.0, shape[-2] / shape[-1]) ** 0.5
+
+
+def _pre_ns(u32, u16, rounding):
+    # rounding "rne": the compiled kernel's fp32->bf16 store; "trunc": what the
+    # Triton interpreter (which wrote the golden trajectories) stores instead
+    return u16 if rounding == "rne" else f32_to_bf16_trunc(u32)
+
+
+def muon_batch_step(params, grads, bufs, step, lr, weight_decay, beta, nesterov, ns, mode, rounding="rne"):
+    """One batch_ns Muon step with every gradient present (muon_sr/triton_muon_sr.py:123-168).
+
+    params, grads: lists of uint16 (bf16 bits) arrays shaped like the parameters,
+    in parameter-group order; bufs: dict shape -> uint16 momentum stack
+    [count, *shape], rows in first-occurrence order (muon_sr/muon_sr.py:112-146);
+    ns: callable mapping a uint16 stack [k, *shape] to its Newton-Schulz output.
+    Shape groups are visited in first-occurrence order (shape_idx); prepare runs
+    over the whole stack with seed (step, shape_idx, salt 0); NS runs per chunk
+    of at most NS_CHUNK_NUMEL elements; apply runs per matrix with seed
+    (step, shape_idx * 10000 + i, salt 1).  Returns (new params, new bufs).
+    """
+    groups = {}
+    for i, p in enumerate(params):
+        groups.setdefault(tuple(p.shape), []).append(i)
+    new_p = [np.array(p, copy=True) for p in params]
+    new_b = {}
+    for shape_idx, (shape, idxs) in enumerate(groups.items()):
+        g = np.concatenate([np.ascontiguousarray(grads[i]).ravel() for i in idxs])
+        buf, u32, u16 = muon_prepare(g, np.ascontiguousarray(bufs[shape]).ravel(), beta, nesterov,
+                                     NoiseSpec(mode, deterministic_seed(step, shape_idx, 0)))
+        new_b[shape] = buf.reshape(len(idxs), *shape)
+        work = _pre_ns(u32, u16, rounding).reshape(len(idxs), *shape)
+        numel = int(np.prod(shape))
+        k = max(1, NS_CHUNK_NUMEL // numel)
+        for start in range(0, len(idxs), k):
+            X = ns(work[start:start + k])
+            for j in range(X.shape[0]):
+                i = start + j
+                seed = deterministic_seed(step, shape_idx * 10000 + i, 1)
+                new_p[idxs[i]] = muon_apply(params[idxs[i]].ravel(), X[j].ravel(), lr, weight_decay, ns_scale(shape),
+                                            NoiseSpec(mode, seed)).reshape(shape)
+    return new_p, new_b
+
+
+def muon_param_step(p, g, buf, step, param_idx, lr, weight_decay, beta, nesterov, ns, mode, rounding="rne"):
+    """One per-parameter Muon step (muon_sr/triton_muon_sr.py:88-120): prepare with
+    seed (step, param_idx, salt 0), NS, apply with seed (step, param_idx, salt 1).
+    Returns (new p, new buf)."""
+    shape = p.shape
+    nbuf, u32, u16 = muon_prepare(np.ascontiguousarray(g).ravel(), np.ascontiguousarray(buf).ravel(), beta, nesterov,
+                                  NoiseSpec(mode, deterministic_seed(step, param_idx, 0)))
+    X = ns(_pre_ns(u32, u16, rounding).reshape(shape))
+    newp = muon_apply(p.ravel(), np.ascontiguousarray(X).ravel(), lr, weight_decay, ns_scale(shape),
+                      NoiseSpec(mode, deterministic_seed(step, param_idx, 1)))
+    return newp.reshape(shape), nbuf.reshape(shape)
 
 
 # ---------------------------------------------------------------------------

@@ -10,6 +10,7 @@ import pytest
 import torch
 
 import oracle as O
+import oracle.ref  # noqa: F401  (module whose seed function the slip test swaps)
 
 
 def bf(u16):
@@ -297,3 +298,69 @@ def test_ns_fp32_closed_form():
         out = O.ns_fp32(G.float()).double()
         exp = (U * torch.from_numpy(O.ns_scalar_map(s.numpy()))) @ V.T
         assert (torch.linalg.norm(out - exp) / torch.linalg.norm(exp)).item() < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# Muon step composition (seeds, stacking, NS, scale) against the reference's
+# own two-step trajectories
+# ---------------------------------------------------------------------------
+
+def _ref_ns_bits(U):
+    """The reference's bf16 Newton-Schulz (reproduced bit-exactly on CPU by
+    O.ns_bf16_torch, see test_ns_bf16_matches_reference_golden) on bf16 bits."""
+    X = O.ns_bf16_torch(bf(U).view(U.shape))
+    return X.view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("tag", ["muon_batch", "hybrid_nobatch"])
+def test_muon_composition_matches_reference_trajectory(golden, tag):
+    z = golden("ns_traj")
+    assert str(z["prepare_rounding"]) == "trunc"
+    nmuon = 3
+    shapes = [tuple(int(s) for s in z[f"{tag}/shape{j}"]) for j in range(nmuon)]
+    params = [z[f"{tag}/p{j}_0"].reshape(shapes[j]) for j in range(nmuon)]
+    if tag == "muon_batch":
+        bufs = {}
+        for s in shapes:
+            bufs.setdefault(s, 0)
+            bufs[s] += 1
+        bufs = {s: np.zeros((c, *s), np.uint16) for s, c in bufs.items()}
+    else:
+        bufs = [np.zeros(s, np.uint16) for s in shapes]
+    for step in (1, 2):
+        grads = [z[f"{tag}/g{j}_{step}"].reshape(shapes[j]) for j in range(nmuon)]
+        if tag == "muon_batch":
+            params, bufs = O.muon_batch_step(params, grads, bufs, step, 0.02, 0.01, 0.95, True, _ref_ns_bits,
+                                             O.NOISE_TRITON, rounding="trunc")
+            rows = {}
+            got_bufs = []
+            for s in shapes:
+                got_bufs.append(bufs[s][rows.get(s, 0)])
+                rows[s] = rows.get(s, 0) + 1
+        else:
+            out = [O.muon_param_step(params[j], grads[j], bufs[j], step, j, 0.02, 0.01, 0.95, True, _ref_ns_bits,
+                                     O.NOISE_TRITON, rounding="trunc") for j in range(nmuon)]
+            params = [o[0] for o in out]
+            bufs = got_bufs = [o[1] for o in out]
+        for j in range(nmuon):
+            assert np.array_equal(got_bufs[j].ravel(), z[f"{tag}/buf{j}_{step}"].ravel()), (tag, step, j)
+            assert np.array_equal(params[j].ravel(), z[f"{tag}/p{j}_{step}"].ravel()), (tag, step, j)
+
+
+def test_muon_composition_detects_seed_slip(golden):
+    """The trajectory pins the apply seeds: a composition that indexes the
+    apply seed by the shape group instead of the matrix fails it."""
+    z = golden("ns_traj")
+    tag = "muon_batch"
+    shapes = [tuple(int(s) for s in z[f"{tag}/shape{j}"]) for j in range(3)]
+    params = [z[f"{tag}/p{j}_0"].reshape(shapes[j]) for j in range(3)]
+    grads = [z[f"{tag}/g{j}_1"].reshape(shapes[j]) for j in range(3)]
+    bufs = {(32, 48): np.zeros((2, 32, 48), np.uint16), (48, 32): np.zeros((1, 48, 32), np.uint16)}
+    real = O.ref.deterministic_seed
+    try:
+        O.ref.deterministic_seed = lambda step, idx, salt=0: real(step, idx // 10000 if salt else idx, salt)
+        slipped, _ = O.ref.muon_batch_step(params, grads, bufs, 1, 0.02, 0.01, 0.95, True, _ref_ns_bits,
+                                           O.NOISE_TRITON, rounding="trunc")
+    finally:
+        O.ref.deterministic_seed = real
+    assert not np.array_equal(slipped[2].ravel(), z[f"{tag}/p2_1"].ravel())

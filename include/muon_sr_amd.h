@@ -163,7 +163,7 @@ int msr_quant_table_check(const void *qtable, const float *qmap_signed, const fl
 
 /* Batched bf16 GEMM  D[b] = alpha * P[b] Q[b]^T + beta * C[b]  (fp32 accumulate, RNE bf16 out).
  * P: [M][K] (row stride ldp), Q: [N][K] (ldq), C/D: [M][N] (ldc/ldd); C may be NULL when beta == 0.
- * M, N multiples of 256 and K a multiple of 64 (the NS workspace is padded to these). */
+ * M, N multiples of 256 and K a multiple of 128 (the NS workspace is padded to these). */
 int msr_gemm_nt(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q, int64_t ldq,
                 int64_t strideQ, const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D, int64_t ldd,
                 int64_t strideD, int64_t M, int64_t N, int64_t K, int64_t batch, float alpha, float beta,

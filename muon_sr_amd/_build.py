@@ -33,12 +33,8 @@ def hipcc() -> str:
     return cand if os.path.exists(cand) else "hipcc"
 
 
-# Per-source extra flags.  The Newton-Schulz GEMM keeps its MFMA operands in
-# VGPRs (the AGPRs then serve as spill space), which removes all scratch
-# traffic from its K loop.
-EXTRA_FLAGS = {
-    "ns_gemm.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form=true"],
-}
+# Per-source extra flags (none at present; kept so a source can get its own).
+EXTRA_FLAGS = {}
 
 _NOISE = "is not a recognized feature for this target"  # hipcc host pass; harmless
 

@@ -14,11 +14,13 @@
 //
 // Kernel shape: 256 threads (4 wave64s in a 2x2 grid), a 256x256 output tile
 // per work-group, K staged through LDS in 64-wide slabs, double buffered
-// (2 x 64 KiB) and filled by direct global->LDS loads one slab ahead.  Each
-// wave owns a 128x128 sub-tile = 4x4 tiles of the 32x32x16 bf16 MFMA (fp32
-// accumulators).  LDS rows are 128 B; chunk c of row r is stored at
-// c ^ ((r >> 1) & 7), so the 16 consecutive rows of one 16-lane quarter of a
-// fragment read (256 B) cover all 64 banks once.
+// (2 x 64 KiB) and filled by buffer loads that write LDS directly, one slab
+// ahead.  Each wave owns a 128x128 sub-tile = 4x4 tiles of the 32x32x16 bf16
+// MFMA (fp32 accumulators in AGPRs).  LDS rows are 128 B; chunk c of row r is
+// stored at c ^ ((r >> 1) & 7), so the 16 consecutive rows of one 16-lane
+// quarter of a fragment read (256 B) cover all 64 banks once.  Each K substep
+// is one scheduling region in which the 16 MFMAs are interleaved with the
+// next substep's fragment reads and a share of the next slab's loads.
 #include "common.hpp"
 #include "../../include/muon_sr_amd.h"
 
@@ -37,7 +39,7 @@ struct GemmArgs {
     const uint16_t *C; int64_t ldc, sC;
     uint16_t *D; int64_t ldd, sD;
     uint16_t *DT; int64_t lddt, sDT;
-    int M, N, K;       // padded extents (multiples of 256, 256, 64)
+    int M, N, K;       // padded extents (multiples of 256, 256, 128)
     int Mv, Nv;        // stores are limited to m < Mv, n < Nv
     float alpha, beta;
     int tiles_m, tiles_n;
@@ -83,13 +85,10 @@ __device__ __forceinline__ void decode_tile(const GemmArgs &a, int t, int &ti, i
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef const __attribute__((address_space(1))) void global_void_t;
 
-// LDS slabs: one array per (stage, operand).
-__shared__ bf16x8_t g_sP0[CHUNKS], g_sQ0[CHUNKS], g_sP1[CHUNKS], g_sQ1[CHUNKS];
+// LDS: four 32 KiB slabs, P stage 0/1 at 0/32K, Q stage 0/1 at 64K/96K.
+__shared__ __attribute__((aligned(1024))) char g_lds[4 * 32768];
 
-// SYM: mirror off-diagonal tiles into D; HAS_C: beta * C term; OUT_D / OUT_DT:
-// write D[m][n] / DT[n][m].  Stores honour Mv / Nv and d_vec.
 template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     int ti, tj;
@@ -99,42 +98,55 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int r32 = lane & 31;
     const int khalf = lane >> 5;
 
-    // Global -> LDS without registers (global_load_lds_dwordx4): one
-    // instruction moves 64 lanes x 16 B into 1 KiB of consecutive LDS, lane l
-    // to byte 16 l.  Instruction i of wave w fills LDS chunks
-    // [(4 i + w) 64, +64) = rows r = (4 i + w) 8 + l / 8, physical chunk l % 8,
-    // so lane l fetches logical chunk (l % 8) ^ ((r >> 1) & 7)
-    // = (l % 8) ^ (4 (w & 1) + l / 16) of its row.
+    // Global -> LDS: buffer loads with the lds flag move 64 lanes x 16 B into
+    // 1 KiB of consecutive LDS (lane l to byte 16 l, base in M0).  Load i of
+    // wave w fills LDS chunks [(4 i + w) 64, +64) = rows (4 i + w) 8 + l / 8,
+    // physical chunk l % 8, i.e. logical chunk (l % 8) ^ ((row >> 1) & 7)
+    // = (l % 8) ^ (4 (w & 1) + l / 16).  Per-lane byte offsets are fixed; the
+    // row block (i) and the K slab go into the scalar offset.
     const int lrow = lane >> 3;
     const int lchunk = (lane & 7) ^ (4 * (wave & 1) + (lane >> 4));
-    const uint16_t *Pl = a.P + bz * a.sP + (int64_t)(m0 + wave * 8 + lrow) * a.ldp + lchunk * 8;
-    const uint16_t *Ql = a.Q + bz * a.sQ + (int64_t)(n0 + wave * 8 + lrow) * a.ldq + lchunk * 8;
-    const int64_t pstep = 32 * a.ldp, qstep = 32 * a.ldq;  // 32 rows per instruction round
-    auto dma = [&](int k0, bf16x8_t *dP, bf16x8_t *dQ) {
+    const __amdgpu_buffer_rsrc_t rP = __builtin_amdgcn_make_buffer_rsrc((void *)(a.P + bz * a.sP), (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rQ = __builtin_amdgcn_make_buffer_rsrc((void *)(a.Q + bz * a.sQ), (short)0, 0x7fffffff, 0x00020000);
+    const uint32_t voP = (uint32_t)(((int64_t)(m0 + wave * 8 + lrow) * a.ldp + lchunk * 8) * 2);
+    const uint32_t voQ = (uint32_t)(((int64_t)(n0 + wave * 8 + lrow) * a.ldq + lchunk * 8) * 2);
+    const uint32_t rowbP = (uint32_t)(32 * a.ldp * 2), rowbQ = (uint32_t)(32 * a.ldq * 2);
+    // Load j (0..15) of a slab: P row block j/2 for even j, Q row block j/2 for odd j.
+    auto dma_part = [&](int stage, int k0, int j0, int j1) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int base = (i * 4 + wave) * 64;
-            __builtin_amdgcn_global_load_lds((global_void_t *)(Pl + i * pstep + k0), (lds_void_t *)(dP + base), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((global_void_t *)(Ql + i * qstep + k0), (lds_void_t *)(dQ + base), 16, 0, 0);
+        for (int j = j0; j < j1; ++j) {
+            const int i = j >> 1;
+            const int dst = (4 * i + wave) * 1024 + stage * 32768;
+            if (j & 1)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_void_t *)(g_lds + 65536 + dst), 16, voQ, i * rowbQ + k0 * 2, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rP, (lds_void_t *)(g_lds + dst), 16, voP, i * rowbP + k0 * 2, 0, 0);
         }
     };
-    auto frags = [&](const bf16x8_t *sP, const bf16x8_t *sQ, int ks, bf16x8_t (&pa)[4], bf16x8_t (&qb)[4]) {
-        const int c = ks * 2 + khalf;
+    auto dma = [&](int stage, int k0) { dma_part(stage, k0, 0, 16); };
+    // Fragment reads: chunk (2 ks + khalf) ^ ((row >> 1) & 7) of row; bits 1-3 of
+    // row come from r32 only, so one byte offset per (operand, ks) serves all
+    // four 32-row blocks and both stages through the instruction offset.
+    const int sw = (r32 >> 1) & 7;
+    uint32_t offP[4], offQ[4];
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
-            const int row = wm * 128 + mi * 32 + r32;
-            pa[mi] = sP[row * 8 + (c ^ ((row >> 1) & 7))];
-        }
+    for (int ks = 0; ks < 4; ++ks) {
+        const int ch = (2 * ks) ^ khalf ^ sw;
+        offP[ks] = (uint32_t)((wm * 128 + r32) * 128 + ch * 16);
+        offQ[ks] = (uint32_t)(65536 + (wn * 128 + r32) * 128 + ch * 16);
+    }
+    auto frags = [&](int stage, int ks, bf16x8_t (&pa)[4], bf16x8_t (&qb)[4]) {
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
-            const int row = wn * 128 + ni * 32 + r32;
-            qb[ni] = sQ[row * 8 + (c ^ ((row >> 1) & 7))];
-        }
+        for (int mi = 0; mi < 4; ++mi)
+            pa[mi] = *reinterpret_cast<const bf16x8_t *>(g_lds + offP[ks] + stage * 32768 + mi * 4096);
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+            qb[ni] = *reinterpret_cast<const bf16x8_t *>(g_lds + offQ[ks] + stage * 32768 + ni * 4096);
     };
 
     f32x16_t acc[4][4];
@@ -145,36 +157,68 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    const int KT = a.K / BK;
     bf16x8_t fa[2][4], fb[2][4];
-    dma(0, g_sP0, g_sQ0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    frags(g_sP0, g_sQ0, 0, fa[0], fb[0]);
-
-    // One K slab from stage (sP, sQ) while the next slab streams into (nP, nQ);
-    // fragments of substep s+1 are read while substep s multiplies.
-    auto slab = [&](int kt, const bf16x8_t *sP, const bf16x8_t *sQ, bf16x8_t *nP, bf16x8_t *nQ) {
-        const bool has_next = kt + 1 < KT;
-        if (has_next) dma((kt + 1) * BK, nP, nQ);
+    auto mm = [&](int b) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            if (ks < 3) frags(sP, sQ, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+        for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
+            for (int ni = 0; ni < 4; ++ni)
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], fa[b][mi], acc[mi][ni], 0, 0, 0);
+    };
+    // One K slab from `stage`; with `next`, the following slab streams into the
+    // other stage, and its first fragments are read after the barrier that ends
+    // this slab, under the last substep's MFMAs.
+    // Each substep is one scheduling region: its 16 MFMAs interleaved with the
+    // 8 fragment reads of the next substep and a share of the next slab's 16
+    // global->LDS loads (so the load queue drains while the MFMAs run).
+    auto pattern = [&](int nvmem) {
 #pragma unroll
-                for (int ni = 0; ni < 4; ++ni)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][ni], fa[ks & 1][mi],
-                                                                          acc[mi][ni], 0, 0, 0);
+        for (int x = 0; x < 8; ++x) {
+            if (x < nvmem) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read (to LDS)
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
         }
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next slab have landed
-        __syncthreads();                // ... and every wave's; the current stage is free
-        if (has_next) frags(nP, nQ, 0, fa[0], fb[0]);
+    };
+    // One K slab from `stage` while slab `knext` streams into the other stage.
+    // The last slab of a tile reloads itself (knext = its own k): the loop
+    // then has a single code path, and the extra stage is never read.
+    auto slab = [&](int stage, int knext) {
+        dma_part(stage ^ 1, knext, 0, 6);
+        frags(stage, 1, fa[1], fb[1]);
+        mm(0);
+        pattern(6);
+        __builtin_amdgcn_sched_barrier(0);
+        dma_part(stage ^ 1, knext, 6, 11);
+        frags(stage, 2, fa[0], fb[0]);
+        mm(1);
+        pattern(5);
+        __builtin_amdgcn_sched_barrier(0);
+        dma_part(stage ^ 1, knext, 11, 16);
+        frags(stage, 3, fa[1], fb[1]);
+        mm(0);
+        pattern(5);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0);   // own loads of the next slab landed, own reads of this stage done
+        __syncthreads();                 // everyone's
+        frags(stage ^ 1, 0, fa[0], fb[0]);
+        mm(1);
+        pattern(0);
+        __builtin_amdgcn_sched_barrier(0);
     };
 
+    const int KT = a.K / BK;
+    dma(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    frags(0, 0, fa[0], fb[0]);
+    // KT is even (K is a multiple of 128): every iteration runs both stages, so
+    // the MFMA code has a single path; only the loads of the slab after the
+    // last and its barrier are skipped.
+    // KT is even (K is a multiple of 128).
     for (int kt = 0; kt < KT; kt += 2) {
-        slab(kt, g_sP0, g_sQ0, g_sP1, g_sQ1);
-        if (kt + 1 < KT) slab(kt + 1, g_sP1, g_sQ1, g_sP0, g_sQ0);
+        slab(0, (kt + 1) * BK);
+        slab(1, (kt + 2 < KT ? kt + 2 : kt + 1) * BK);
     }
 
     // ---------------- epilogue ----------------
@@ -410,6 +454,12 @@ static NSLayout ns_layout(int64_t batch, int64_t rows, int64_t cols) {
 
 static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
     GemmArgs a = a0;
+    // operand loads address one matrix with 32-bit byte offsets
+    if (((int64_t)(a.M - 1) * a.ldp + a.K) * 2 >= (int64_t(1) << 31) ||
+        ((int64_t)(a.N - 1) * a.ldq + a.K) * 2 >= (int64_t(1) << 31)) {
+        set_error("msr_gemm_nt: an operand matrix spans 2 GiB or more");
+        return MSR_ERR_ARG;
+    }
     a.tiles_m = a.M / BM;
     a.tiles_n = a.N / BN;
     a.d_vec = a.D && aligned(a.D, 8) && (a.ldd % 4) == 0 && (a.sD % 4) == 0;
@@ -446,8 +496,8 @@ extern "C" {
 int msr_gemm_nt(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q, int64_t ldq, int64_t strideQ,
                 const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D, int64_t ldd, int64_t strideD, int64_t M,
                 int64_t N, int64_t K, int64_t batch, float alpha, float beta, msr_stream_t stream) {
-    if (!P || !Q || !D || batch < 0 || M <= 0 || N <= 0 || K <= 0 || (M % BM) || (N % BN) || (K % BK)) {
-        set_error("msr_gemm_nt: need M, N multiples of 256 and K a multiple of 64 (got %lld, %lld, %lld)",
+    if (!P || !Q || !D || batch < 0 || M <= 0 || N <= 0 || K <= 0 || (M % BM) || (N % BN) || (K % (2 * BK))) {
+        set_error("msr_gemm_nt: need M, N multiples of 256 and K a multiple of 128 (got %lld, %lld, %lld)",
                   (long long)M, (long long)N, (long long)K);
         return MSR_ERR_ARG;
     }

@@ -399,7 +399,7 @@ def test_muon_apply_multi_vs_oracle(L, mode):
 # (b) MFMA GEMM and Newton-Schulz
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("M,N,K,batch,alpha,beta", [(256, 256, 64, 1, 1.0, 0.0), (512, 768, 320, 2, 0.5, -1.25),
+@pytest.mark.parametrize("M,N,K,batch,alpha,beta", [(256, 256, 128, 1, 1.0, 0.0), (512, 768, 384, 2, 0.5, -1.25),
                                                     (256, 512, 1024, 3, 2.0315, -4.775)])
 def test_gemm_nt_vs_torch_fp32(L, M, N, K, batch, alpha, beta):
     torch.manual_seed(M + N + K)

@@ -29,10 +29,16 @@ from .adamw_8bit import adamw8bit_launch, init_8bit_state, TritonAdamW8bit
 
 NS_COEFFS = (3.4445, -4.7750, 2.0315)
 
-# Max elements per batched Newton-Schulz call (muon_sr/triton_muon_sr.py:123-125).
-# The library's Newton-Schulz is batch-invariant, so the chunking only bounds
-# the transient workspace; results do not depend on it.
+# Max elements per batched Newton-Schulz call in the reference
+# (muon_sr/triton_muon_sr.py:123-125), kept as a module constant.
 NS_CHUNK_NUMEL = 1 << 28
+# Max elements per batched call here.  The library's Newton-Schulz is
+# batch-invariant (each matrix's tiles and reduction order do not depend on
+# the batch), so the chunking changes no result; larger chunks give the
+# symmetric products enough tiles to fill all 256 CUs (a 2^28-element chunk of
+# 14336x4096 matrices holds only 4 of them).  The transient workspace is 9-12
+# bytes per element of the chunk (<= ~13 GB at 2^30, against 288 GB of HBM).
+NS_BATCH_NUMEL = 1 << 30
 
 
 def _restore_global_step(state, groups):
@@ -141,7 +147,7 @@ def _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns
             work = torch.empty(Na, *shape, dtype=torch.bfloat16, device=active[0].device)
             _run_prepare(grads, stacked_buf, work, beta, nesterov, _deterministic_seed(step, shape_idx, salt=0))
             del grads
-            k = max(1, NS_CHUNK_NUMEL // work[0].numel())
+            k = max(1, NS_BATCH_NUMEL // work[0].numel())
             scale = _ns_scale(shape)
             for start in range(0, Na, k):
                 update_ns = newton_schulz(work[start:start + k], steps=ns_steps)

@@ -44,7 +44,8 @@ struct GemmArgs {
     float alpha, beta;
     int tiles_m, tiles_n;
     int symmetric;     // M == N, P == Q: only tiles ti <= tj, mirrored into D
-    int d_vec;         // D rows allow 8-byte stores (set by launch_gemm)
+    int d_vec;         // D rows allow 16-byte stores (set by launch_gemm)
+    int dt_vec;        // DT rows allow 16-byte stores (set by launch_gemm)
 };
 
 // Work-group -> tile.  Consecutive work-group ids are dispatched round-robin
@@ -86,8 +87,12 @@ __device__ __forceinline__ void decode_tile(const GemmArgs &a, int t, int &ti, i
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// LDS: four 32 KiB slabs, P stage 0/1 at 0/32K, Q stage 0/1 at 64K/96K.
-__shared__ __attribute__((aligned(1024))) char g_lds[4 * 32768];
+// LDS: four 32 KiB slabs, P stage 0/1 at 0/32K, Q stage 0/1 at 64K/96K; after
+// the K loop the same memory stages the 256 x 256 bf16 output tile with a row
+// pitch of SPITCH elements (528 B: 16-byte aligned rows; the 8-byte writes of
+// 32 consecutive rows hit each bank at most twice).
+constexpr int SPITCH = 264;
+__shared__ __attribute__((aligned(1024))) char g_lds[256 * SPITCH * 2];
 
 template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
@@ -222,57 +227,99 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     }
 
     // ---------------- epilogue ----------------
-    // Lane l holds D[m = l % 32][n = 8r + 4(l / 32) + q] of each 32x32 tile.
-    // (Written with scalars: the array form of this loop spills registers.)
+    // The output tile is staged through LDS as bf16 (row pitch SPITCH) so that
+    // global traffic is 16-byte row chunks: C is loaded that way, D is stored
+    // that way, and the transposed copies (DT, or the mirror of an off-diagonal
+    // symmetric tile) are gathered column-wise from LDS.
+    // Lane l holds D[m = l % 32][n = 8r + 4(l / 32) + q] of each 32x32 MFMA tile.
+    uint16_t *stg = reinterpret_cast<uint16_t *>(g_lds);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();   // every wave is done with the operand slabs
+    const int ec = tid & 31, er = tid >> 5;   // 16-byte chunk in a row, first row
+    if constexpr (HAS_C) {
+        const uint16_t *Cb = a.C + bz * a.sC + (int64_t)m0 * a.ldc + n0 + 8 * ec;
+#pragma unroll 4
+        for (int it = 0; it < 32; ++it) {
+            const int r = er + 8 * it;
+            *reinterpret_cast<uint4 *>(stg + r * SPITCH + 8 * ec) =
+                *reinterpret_cast<const uint4 *>(Cb + (int64_t)r * a.ldc);
+        }
+        __syncthreads();
+    }
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wm * 128 + mi * 32 + r32;
-                const int n = n0 + wn * 128 + ni * 32 + 8 * r + 4 * khalf;
+                const int ml = wm * 128 + mi * 32 + r32;
+                const int nl = wn * 128 + ni * 32 + 8 * r + 4 * khalf;
+                uint2 *sp = reinterpret_cast<uint2 *>(stg + ml * SPITCH + nl);
                 float v0 = a.alpha * acc[mi][ni][4 * r], v1 = a.alpha * acc[mi][ni][4 * r + 1];
                 float v2 = a.alpha * acc[mi][ni][4 * r + 2], v3 = a.alpha * acc[mi][ni][4 * r + 3];
                 if constexpr (HAS_C) {
-                    const uint2 cw = *reinterpret_cast<const uint2 *>(a.C + bz * a.sC + (int64_t)m * a.ldc + n);
+                    const uint2 cw = *sp;
                     v0 = v0 + a.beta * bf16_lo(cw.x);
                     v1 = v1 + a.beta * bf16_hi(cw.x);
                     v2 = v2 + a.beta * bf16_lo(cw.y);
                     v3 = v3 + a.beta * bf16_hi(cw.y);
                 }
-                const uint32_t h0 = rne_bf16(v0), h1 = rne_bf16(v1), h2 = rne_bf16(v2), h3 = rne_bf16(v3);
-                if constexpr (OUT_D) {
-                    if (m < a.Mv) {
-                        uint16_t *dp = a.D + bz * a.sD + (int64_t)m * a.ldd + n;
-                        if (a.d_vec && n + 3 < a.Nv) {
-                            *reinterpret_cast<uint2 *>(dp) = make_uint2(pack2(h0, h1), pack2(h2, h3));
-                        } else {
-                            if (n < a.Nv) dp[0] = (uint16_t)h0;
-                            if (n + 1 < a.Nv) dp[1] = (uint16_t)h1;
-                            if (n + 2 < a.Nv) dp[2] = (uint16_t)h2;
-                            if (n + 3 < a.Nv) dp[3] = (uint16_t)h3;
-                        }
-                    }
-                    if constexpr (SYM) {
-                        if (ti != tj) {  // mirror of an off-diagonal tile (M == N, no bounds)
-                            uint16_t *dp = a.D + bz * a.sD + (int64_t)n * a.ldd + m;
-                            dp[0] = (uint16_t)h0;
-                            dp[a.ldd] = (uint16_t)h1;
-                            dp[2 * a.ldd] = (uint16_t)h2;
-                            dp[3 * a.ldd] = (uint16_t)h3;
-                        }
-                    }
-                }
-                if constexpr (OUT_DT) {
-                    if (m < a.Mv) {
-                        uint16_t *tp = a.DT + bz * a.sDT + (int64_t)n * a.lddt + m;
-                        if (n < a.Nv) tp[0] = (uint16_t)h0;
-                        if (n + 1 < a.Nv) tp[a.lddt] = (uint16_t)h1;
-                        if (n + 2 < a.Nv) tp[2 * a.lddt] = (uint16_t)h2;
-                        if (n + 3 < a.Nv) tp[3 * a.lddt] = (uint16_t)h3;
-                    }
-                }
+                *sp = make_uint2(pack2(rne_bf16(v0), rne_bf16(v1)), pack2(rne_bf16(v2), rne_bf16(v3)));
+            }
+        }
+    }
+    __syncthreads();
+    if constexpr (OUT_D) {
+        uint16_t *Db = a.D + bz * a.sD;
+#pragma unroll 4
+        for (int it = 0; it < 32; ++it) {
+            const int r = er + 8 * it;
+            const int m = m0 + r, n = n0 + 8 * ec;
+            if (m >= a.Mv) continue;
+            const uint4 w = *reinterpret_cast<const uint4 *>(stg + r * SPITCH + 8 * ec);
+            uint16_t *dp = Db + (int64_t)m * a.ldd + n;
+            if (a.d_vec && n + 8 <= a.Nv) {
+                *reinterpret_cast<uint4 *>(dp) = w;
+            } else {
+                const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (n + j < a.Nv) dp[j] = (uint16_t)(u[j >> 1] >> (16 * (j & 1)));
+            }
+        }
+    }
+    // Transposed copy: T[n][m] = tile[m][n].  Lanes of a wave take 64
+    // consecutive n (a conflict-free LDS row read per element) and each stores
+    // 8 consecutive m (16 bytes) of its row n.
+    bool mirror = false;
+    if constexpr (SYM && OUT_D) mirror = ti != tj;
+    if (OUT_DT || mirror) {
+        uint16_t *Tb;
+        int64_t ldt;
+        int tm0, tn0, tMv, tNv;
+        bool tvec;
+        if (OUT_DT) {
+            Tb = a.DT + bz * a.sDT; ldt = a.lddt; tm0 = m0; tn0 = n0; tMv = a.Mv; tNv = a.Nv; tvec = a.dt_vec;
+        } else {   // mirror of an off-diagonal symmetric tile into D (M == N, no bounds)
+            Tb = a.D + bz * a.sD; ldt = a.ldd; tm0 = m0; tn0 = n0; tMv = a.M; tNv = a.N; tvec = a.d_vec;
+        }
+        const int nl = (tid & 63) + 64 * (tid >> 6 & 3);   // tile column = output row
+        const int n = tn0 + nl;
+#pragma unroll 4
+        for (int c = 0; c < 32; ++c) {            // 8-row chunk of the tile = 8 output columns
+            uint32_t u[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                u[j] = (uint32_t)stg[(8 * c + 2 * j) * SPITCH + nl] | ((uint32_t)stg[(8 * c + 2 * j + 1) * SPITCH + nl] << 16);
+            const int m = tm0 + 8 * c;
+            if (n >= tNv) continue;
+            uint16_t *tp = Tb + (int64_t)n * ldt + m;
+            if (tvec && m + 8 <= tMv) {
+                *reinterpret_cast<uint4 *>(tp) = make_uint4(u[0], u[1], u[2], u[3]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (m + j < tMv) tp[j] = (uint16_t)(u[j >> 1] >> (16 * (j & 1)));
             }
         }
     }
@@ -462,7 +509,8 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
     }
     a.tiles_m = a.M / BM;
     a.tiles_n = a.N / BN;
-    a.d_vec = a.D && aligned(a.D, 8) && (a.ldd % 4) == 0 && (a.sD % 4) == 0;
+    a.d_vec = a.D && aligned(a.D, 16) && (a.ldd % 8) == 0 && (a.sD % 8) == 0;
+    a.dt_vec = a.DT && aligned(a.DT, 16) && (a.lddt % 8) == 0 && (a.sDT % 8) == 0;
     const int64_t tiles = a.symmetric ? (int64_t)a.tiles_m * (a.tiles_m + 1) / 2 : (int64_t)a.tiles_m * a.tiles_n;
     for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
         const int64_t nb = (batch - b0) < 65535 ? (batch - b0) : 65535;
@@ -501,9 +549,9 @@ int msr_gemm_nt(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t 
                   (long long)M, (long long)N, (long long)K);
         return MSR_ERR_ARG;
     }
-    if (!aligned(P, 16) || !aligned(Q, 16) || !aligned(D, 8) || (C && !aligned(C, 8)) || (ldp % 8) || (ldq % 8) ||
-        (ldd % 4) || (C && (ldc % 4)) || (strideP % 8) || (strideQ % 8)) {
-        set_error("msr_gemm_nt: operands must be 16-byte aligned with row strides a multiple of 8 elements");
+    if (!aligned(P, 16) || !aligned(Q, 16) || (ldp % 8) || (ldq % 8) || (strideP % 8) || (strideQ % 8) ||
+        (C && beta != 0.0f && (!aligned(C, 16) || (ldc % 8) || (strideC % 8)))) {
+        set_error("msr_gemm_nt: P, Q and C must be 16-byte aligned with row and batch strides a multiple of 8 elements");
         return MSR_ERR_ALIGN;
     }
     if (batch == 0) return MSR_OK;

@@ -12,15 +12,17 @@
 // preserved exactly by all three products, so only the final store is
 // bounds-checked.
 //
-// Kernel shape: 256 threads (4 wave64s in a 2x2 grid), a 256x256 output tile
-// per work-group, K staged through LDS in 64-wide slabs, double buffered
-// (2 x 64 KiB) and filled by buffer loads that write LDS directly, one slab
-// ahead.  Each wave owns a 128x128 sub-tile = 4x4 tiles of the 32x32x16 bf16
-// MFMA (fp32 accumulators in AGPRs).  LDS rows are 128 B; chunk c of row r is
-// stored at c ^ ((r >> 1) & 7), so the 16 consecutive rows of one 16-lane
-// quarter of a fragment read (256 B) cover all 64 banks once.  Each K substep
-// is one scheduling region in which the 16 MFMAs are interleaved with the
-// next substep's fragment reads and a share of the next slab's loads.
+// Kernel shape: 512 threads (8 wave64s in a 2 x 4 grid, two per SIMD), a
+// 256x256 output tile per work-group, K staged through LDS in 64-wide slabs,
+// double buffered (2 x 64 KiB) and filled by buffer loads that write LDS
+// directly, one slab ahead.  Each wave owns a 128x64 sub-tile = 4x2 tiles of
+// the 32x32x16 bf16 MFMA (fp32 accumulators); with two waves per SIMD, one
+// wave's MFMAs keep the matrix core busy while the other waits at the slab
+// barrier.  LDS rows are 128 B; chunk c of row r is stored at
+// c ^ ((r >> 1) & 7), so the 16 consecutive rows of one 16-lane quarter of a
+// fragment read (256 B) cover all 64 banks once.  Each K substep is one
+// scheduling region in which the MFMAs are interleaved with the next
+// substep's fragment reads and a share of the next slab's loads.
 #include "common.hpp"
 #include "../../include/muon_sr_amd.h"
 
@@ -30,7 +32,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int GEMM_THREADS = 256;
+constexpr int GEMM_THREADS = 512;
 constexpr int CHUNKS = BM * BK / 8;  // 16-byte chunks per operand slab (2048)
 
 struct GemmArgs {
@@ -104,13 +106,13 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave >> 2, wn = wave & 3;   // 2 x 4 waves, 128 x 64 each
     const int r32 = lane & 31;
     const int khalf = lane >> 5;
 
     // Global -> LDS: buffer loads with the lds flag move 64 lanes x 16 B into
     // 1 KiB of consecutive LDS (lane l to byte 16 l, base in M0).  Load i of
-    // wave w fills LDS chunks [(4 i + w) 64, +64) = rows (4 i + w) 8 + l / 8,
+    // wave w fills LDS chunks [(8 i + w) 64, +64) = rows (8 i + w) 8 + l / 8,
     // physical chunk l % 8, i.e. logical chunk (l % 8) ^ ((row >> 1) & 7)
     // = (l % 8) ^ (4 (w & 1) + l / 16).  Per-lane byte offsets are fixed; the
     // row block (i) and the K slab go into the scalar offset.
@@ -120,20 +122,20 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     const __amdgpu_buffer_rsrc_t rQ = __builtin_amdgcn_make_buffer_rsrc((void *)(a.Q + bz * a.sQ), (short)0, 0x7fffffff, 0x00020000);
     const uint32_t voP = (uint32_t)(((int64_t)(m0 + wave * 8 + lrow) * a.ldp + lchunk * 8) * 2);
     const uint32_t voQ = (uint32_t)(((int64_t)(n0 + wave * 8 + lrow) * a.ldq + lchunk * 8) * 2);
-    const uint32_t rowbP = (uint32_t)(32 * a.ldp * 2), rowbQ = (uint32_t)(32 * a.ldq * 2);
-    // Load j (0..15) of a slab: P row block j/2 for even j, Q row block j/2 for odd j.
+    const uint32_t rowbP = (uint32_t)(64 * a.ldp * 2), rowbQ = (uint32_t)(64 * a.ldq * 2);
+    // Load j (0..7) of a slab: P row block j/2 for even j, Q row block j/2 for odd j.
     auto dma_part = [&](int stage, int k0, int j0, int j1) {
 #pragma unroll
         for (int j = j0; j < j1; ++j) {
             const int i = j >> 1;
-            const int dst = (4 * i + wave) * 1024 + stage * 32768;
+            const int dst = (8 * i + wave) * 1024 + stage * 32768;
             if (j & 1)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_void_t *)(g_lds + 65536 + dst), 16, voQ, i * rowbQ + k0 * 2, 0, 0);
             else
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rP, (lds_void_t *)(g_lds + dst), 16, voP, i * rowbP + k0 * 2, 0, 0);
         }
     };
-    auto dma = [&](int stage, int k0) { dma_part(stage, k0, 0, 16); };
+    auto dma = [&](int stage, int k0) { dma_part(stage, k0, 0, 8); };
     // Fragment reads: chunk (2 ks + khalf) ^ ((row >> 1) & 7) of row; bits 1-3 of
     // row come from r32 only, so one byte offset per (operand, ks) serves all
     // four 32-row blocks and both stages through the instruction offset.
@@ -143,66 +145,63 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     for (int ks = 0; ks < 4; ++ks) {
         const int ch = (2 * ks) ^ khalf ^ sw;
         offP[ks] = (uint32_t)((wm * 128 + r32) * 128 + ch * 16);
-        offQ[ks] = (uint32_t)(65536 + (wn * 128 + r32) * 128 + ch * 16);
+        offQ[ks] = (uint32_t)(65536 + (wn * 64 + r32) * 128 + ch * 16);
     }
-    auto frags = [&](int stage, int ks, bf16x8_t (&pa)[4], bf16x8_t (&qb)[4]) {
+    auto frags = [&](int stage, int ks, bf16x8_t (&pa)[4], bf16x8_t (&qb)[2]) {
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi)
             pa[mi] = *reinterpret_cast<const bf16x8_t *>(g_lds + offP[ks] + stage * 32768 + mi * 4096);
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
+        for (int ni = 0; ni < 2; ++ni)
             qb[ni] = *reinterpret_cast<const bf16x8_t *>(g_lds + offQ[ks] + stage * 32768 + ni * 4096);
     };
 
-    f32x16_t acc[4][4];
+    f32x16_t acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    bf16x8_t fa[2][4], fb[2][4];
+    bf16x8_t fa[2][4], fb[2][2];
     auto mm = [&](int b) {
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni)
+            for (int ni = 0; ni < 2; ++ni)
                 acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], fa[b][mi], acc[mi][ni], 0, 0, 0);
     };
-    // One K slab from `stage`; with `next`, the following slab streams into the
-    // other stage, and its first fragments are read after the barrier that ends
-    // this slab, under the last substep's MFMAs.
-    // Each substep is one scheduling region: its 16 MFMAs interleaved with the
-    // 8 fragment reads of the next substep and a share of the next slab's 16
+    // Each substep is one scheduling region: its 8 MFMAs interleaved with the
+    // 6 fragment reads of the next substep and a share of the next slab's 8
     // global->LDS loads (so the load queue drains while the MFMAs run).
     auto pattern = [&](int nvmem) {
 #pragma unroll
-        for (int x = 0; x < 8; ++x) {
+        for (int x = 0; x < 6; ++x) {
             if (x < nvmem) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read (to LDS)
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA (8 per substep)
+            if (x == 0 || x == 2) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
     };
     // One K slab from `stage` while slab `knext` streams into the other stage.
     // The last slab of a tile reloads itself (knext = its own k): the loop
     // then has a single code path, and the extra stage is never read.
     auto slab = [&](int stage, int knext) {
-        dma_part(stage ^ 1, knext, 0, 6);
+        dma_part(stage ^ 1, knext, 0, 3);
         frags(stage, 1, fa[1], fb[1]);
         mm(0);
-        pattern(6);
+        pattern(3);
         __builtin_amdgcn_sched_barrier(0);
-        dma_part(stage ^ 1, knext, 6, 11);
+        dma_part(stage ^ 1, knext, 3, 6);
         frags(stage, 2, fa[0], fb[0]);
         mm(1);
-        pattern(5);
+        pattern(3);
         __builtin_amdgcn_sched_barrier(0);
-        dma_part(stage ^ 1, knext, 11, 16);
+        dma_part(stage ^ 1, knext, 6, 8);
         frags(stage, 3, fa[1], fb[1]);
         mm(0);
-        pattern(5);
+        pattern(2);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(0);   // own loads of the next slab landed, own reads of this stage done
         __syncthreads();                 // everyone's
@@ -217,10 +216,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     frags(0, 0, fa[0], fb[0]);
-    // KT is even (K is a multiple of 128): every iteration runs both stages, so
-    // the MFMA code has a single path; only the loads of the slab after the
-    // last and its barrier are skipped.
-    // KT is even (K is a multiple of 128).
+    // KT is even (K is a multiple of 128): every iteration runs both stages.
     for (int kt = 0; kt < KT; kt += 2) {
         slab(0, (kt + 1) * BK);
         slab(1, (kt + 2 < KT ? kt + 2 : kt + 1) * BK);
@@ -235,12 +231,12 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     uint16_t *stg = reinterpret_cast<uint16_t *>(g_lds);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // every wave is done with the operand slabs
-    const int ec = tid & 31, er = tid >> 5;   // 16-byte chunk in a row, first row
+    const int ec = tid & 31, er = tid >> 5;   // 16-byte chunk in a row, first row (16 rows per pass)
     if constexpr (HAS_C) {
         const uint16_t *Cb = a.C + bz * a.sC + (int64_t)m0 * a.ldc + n0 + 8 * ec;
 #pragma unroll 4
-        for (int it = 0; it < 32; ++it) {
-            const int r = er + 8 * it;
+        for (int it = 0; it < 16; ++it) {
+            const int r = er + 16 * it;
             *reinterpret_cast<uint4 *>(stg + r * SPITCH + 8 * ec) =
                 *reinterpret_cast<const uint4 *>(Cb + (int64_t)r * a.ldc);
         }
@@ -249,11 +245,11 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
+        for (int ni = 0; ni < 2; ++ni) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int ml = wm * 128 + mi * 32 + r32;
-                const int nl = wn * 128 + ni * 32 + 8 * r + 4 * khalf;
+                const int nl = wn * 64 + ni * 32 + 8 * r + 4 * khalf;
                 uint2 *sp = reinterpret_cast<uint2 *>(stg + ml * SPITCH + nl);
                 float v0 = a.alpha * acc[mi][ni][4 * r], v1 = a.alpha * acc[mi][ni][4 * r + 1];
                 float v2 = a.alpha * acc[mi][ni][4 * r + 2], v3 = a.alpha * acc[mi][ni][4 * r + 3];
@@ -272,8 +268,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     if constexpr (OUT_D) {
         uint16_t *Db = a.D + bz * a.sD;
 #pragma unroll 4
-        for (int it = 0; it < 32; ++it) {
-            const int r = er + 8 * it;
+        for (int it = 0; it < 16; ++it) {
+            const int r = er + 16 * it;
             const int m = m0 + r, n = n0 + 8 * ec;
             if (m >= a.Mv) continue;
             const uint4 w = *reinterpret_cast<const uint4 *>(stg + r * SPITCH + 8 * ec);
@@ -303,10 +299,10 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         } else {   // mirror of an off-diagonal symmetric tile into D (M == N, no bounds)
             Tb = a.D + bz * a.sD; ldt = a.ldd; tm0 = m0; tn0 = n0; tMv = a.M; tNv = a.N; tvec = a.d_vec;
         }
-        const int nl = (tid & 63) + 64 * (tid >> 6 & 3);   // tile column = output row
+        const int nl = tid & 255;                 // tile column = output row
         const int n = tn0 + nl;
 #pragma unroll 4
-        for (int c = 0; c < 32; ++c) {            // 8-row chunk of the tile = 8 output columns
+        for (int c = (tid >> 8) * 16; c < (tid >> 8) * 16 + 16; ++c) {   // 8-row chunk of the tile = 8 output columns
             uint32_t u[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j)

@@ -149,6 +149,10 @@ def llama_small_shapes():
 
 
 def bench_sr_accum(micro=16):
+    """Config 3.  The hooks of one micro-batch are queued (as inside a backward
+    pass) and launched together; the timed region is that launch, with the
+    gradients and accumulators resident in HBM.  The one-launch-per-hook path
+    (hooks called outside a backward pass) is timed beside it."""
     import torch
     from muon_sr_amd import TritonSRAccumulator
     dev = "cuda:0"
@@ -167,40 +171,55 @@ def bench_sr_accum(micro=16):
             self.ps = torch.nn.ParameterList(params)
 
     model = Holder()
+    TritonSRAccumulator.max_deferred_bytes = 1 << 40   # one launch per micro-batch
 
-    def run():
-        for mb in range(micro):
-            gs = gsets[mb % 2]
+    def micro_batch(gs, evs=None, deferred=True):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        if deferred:
+            with TritonSRAccumulator.deferred():
+                for p, g in zip(params, gs):
+                    p.grad = g
+                    TritonSRAccumulator._accum_hook(p)
+                s.record()
+            e.record()
+        else:
+            s.record()
             for p, g in zip(params, gs):
                 p.grad = g
                 TritonSRAccumulator._accum_hook(p)
-        TritonSRAccumulator.reassign_grad_buffer(model)
-        for p in params:
-            p.grad = None
+            e.record()
+        if evs is not None:
+            evs.append((s, e))
 
-    run()  # warm-up
+    for mb in range(micro):    # warm-up pass
+        micro_batch(gsets[mb % 2])
+    TritonSRAccumulator.reassign_grad_buffer(model)
+    for p in params:
+        p.grad = None
     sync()
-    # steady-state accumulate kernels (micro-batches 2..16), timed per micro-batch with events
     t0 = time.perf_counter()
     evs = []
     for mb in range(micro):
-        gs = gsets[mb % 2]
-        s = torch.cuda.Event(enable_timing=True)
-        e = torch.cuda.Event(enable_timing=True)
-        s.record()
-        for p, g in zip(params, gs):
-            p.grad = g
-            TritonSRAccumulator._accum_hook(p)
-        e.record()
-        evs.append((s, e))
+        micro_batch(gsets[mb % 2], evs)
     TritonSRAccumulator.reassign_grad_buffer(model)
     sync()
     wall = (time.perf_counter() - t0) * 1e3
     ms = [s.elapsed_time(e) for s, e in evs]
     steady = sum(ms[1:]) / (micro - 1)
+    # one launch per hook, for comparison
+    for p in params:
+        p.grad = None
+    evs1 = []
+    for mb in range(4):
+        micro_batch(gsets[mb % 2], evs1, deferred=False)
+    TritonSRAccumulator.reassign_grad_buffer(model)
+    sync()
+    per_tensor = sum(s.elapsed_time(e) for s, e in evs1[1:]) / 3
     out = dict(tensors=len(params), elements=numel, micro_batches=micro, total_ms=wall,
                first_microbatch_ms=ms[0], accumulate_ms=steady,
-               accumulate_gbps=6.0 * numel / (steady * 1e6), first_gbps=4.0 * numel / (ms[0] * 1e6))
+               accumulate_gbps=6.0 * numel / (steady * 1e6), first_gbps=4.0 * numel / (ms[0] * 1e6),
+               per_tensor_launch_ms=per_tensor, per_tensor_launch_gbps=6.0 * numel / (per_tensor * 1e6))
     del gsets, params, model
     torch.cuda.empty_cache()
     return out

@@ -60,6 +60,23 @@ const char *msr_last_error(void);
 int msr_sr_accum(uint16_t *acc, const void *grad, int32_t grad_is_f32, int64_t n, uint32_t seed,
                  int32_t zero_init, int32_t noise_mode, const uint16_t *inject, msr_stream_t stream);
 
+/* (c) SR gradient accumulation of many tensors in one launch.
+ * Same arithmetic and noise as one msr_sr_accum call per item (noise offsets
+ * restart at 0 in every tensor), for the hooks of one backward pass collected
+ * by TritonSRAccumulator (muon_sr/triton_adamw.py:252-265, one launch per
+ * parameter in the reference).  items: HOST array; any count (split into
+ * launches internally).  noise_mode: MSR_NOISE_TRITON or MSR_NOISE_PHILOX8. */
+typedef struct msr_accum_item {
+    uint16_t *acc;      /* bf16 accumulator [n] */
+    const void *grad;   /* bf16, or fp32 with MSR_ACCUM_GRAD_F32, [n] */
+    int64_t n;
+    uint32_t seed;
+    int32_t flags;      /* MSR_ACCUM_ZERO_INIT | MSR_ACCUM_GRAD_F32 */
+} msr_accum_item;
+#define MSR_ACCUM_ZERO_INIT 1
+#define MSR_ACCUM_GRAD_F32 2
+int msr_sr_accum_multi(const msr_accum_item *items, int32_t count, int32_t noise_mode, msr_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * BF16-moment AdamW step (PyTorch order: decay before the update).
  * Replaces _adamw_kernel / _adamw_step (muon_sr/triton_adamw.py:9-114).

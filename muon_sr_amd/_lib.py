@@ -22,11 +22,22 @@ _P = ctypes.c_void_p
 _I64, _I32, _U32, _F = ctypes.c_int64, ctypes.c_int32, ctypes.c_uint32, ctypes.c_float
 _SIZE_P = ctypes.POINTER(ctypes.c_size_t)
 
+
+class AccumItem(ctypes.Structure):
+    """msr_accum_item (include/muon_sr_amd.h)."""
+    _fields_ = [("acc", ctypes.c_void_p), ("grad", ctypes.c_void_p), ("n", ctypes.c_int64),
+                ("seed", ctypes.c_uint32), ("flags", ctypes.c_int32)]
+
+
+ACCUM_ZERO_INIT = 1
+ACCUM_GRAD_F32 = 2
+
 # name -> (restype, argtypes); mirrors include/muon_sr_amd.h
 SIGNATURES = {
     "msr_version": (ctypes.c_int, []),
     "msr_last_error": (ctypes.c_char_p, []),
     "msr_sr_accum": (ctypes.c_int, [_P, _P, _I32, _I64, _U32, _I32, _I32, _P, _P]),
+    "msr_sr_accum_multi": (ctypes.c_int, [ctypes.POINTER(AccumItem), _I32, _I32, _P]),
     "msr_adamw_bf16_step": (ctypes.c_int, [_P, _P, _P, _P, _I64, _F, _F, _F, _F, _F, _F, _F, _U32, _I32, _P, _P]),
     "msr_adamw8bit_step": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32,
                                           _F, _F, _F, _F, _F, _F, _F, _U32, _I32, _P, _P]),

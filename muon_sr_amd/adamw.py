@@ -6,7 +6,9 @@ kernels are replaced by the gfx950 kernels of libmuon_sr_amd.so.
 """
 from __future__ import annotations
 
+import contextlib
 import random
+import threading
 
 import torch
 from torch.optim import Optimizer
@@ -105,6 +107,39 @@ class TritonAdamW(Optimizer):
         return loss
 
 
+class _AccumQueue:
+    """Accumulations of one device waiting for a multi-tensor launch.  Holds the
+    gradients alive until the launch; items keep their hook order."""
+
+    def __init__(self):
+        self.items = []
+        self.keep = []
+        self.accs = set()
+        self.nbytes = 0
+        self.stream = None
+
+    def flush(self):
+        if not self.items:
+            return
+        arr = (_lib.AccumItem * len(self.items))(*self.items)
+        rc = _lib.lib().msr_sr_accum_multi(arr, len(self.items), _lib.noise_mode(), self.stream)
+        self.items, self.keep, self.accs, self.nbytes, self.stream = [], [], set(), 0, None
+        _lib.check(rc, "msr_sr_accum_multi")
+
+
+_queues = {}
+_queue_lock = threading.Lock()
+_deferred_depth = 0
+_callback_tasks = set()
+
+
+def _flush_all():
+    with _queue_lock:
+        for q in _queues.values():
+            q.flush()
+        _callback_tasks.clear()
+
+
 class TritonSRAccumulator:
     """
     Stochastic-rounding gradient accumulation into a BF16 buffer ``p.acc_grad``.
@@ -124,6 +159,14 @@ class TritonSRAccumulator:
             optimizer.zero_grad()
     """
 
+    # Accumulations are launched many tensors at a time: the hooks of one
+    # backward pass queue their (acc, grad) pairs, and the queue is flushed at
+    # the end of the pass (an autograd final callback), when it holds
+    # `max_deferred_bytes` of gradients, and by reassign_grad_buffer().  The
+    # arithmetic and noise are those of one launch per tensor.  Outside a
+    # backward pass (and outside `deferred()`) each hook launches at once.
+    max_deferred_bytes = 512 << 20
+
     @staticmethod
     def _accum_hook(p):
         grad = p.grad
@@ -137,13 +180,49 @@ class TritonSRAccumulator:
         if first:
             p.acc_grad = torch.empty_like(p.data, dtype=torch.bfloat16, memory_format=torch.contiguous_format)
         acc = p.acc_grad
-        rc = _lib.lib().msr_sr_accum(acc.data_ptr(), grad.data_ptr(), int(grad.dtype == torch.float32), n, seed,
-                                     int(first), _lib.noise_mode(), None, _lib.stream_of(acc))
-        _lib.check(rc, "msr_sr_accum")
+        stream = _lib.stream_of(acc)
+        f32 = grad.dtype == torch.float32
+        task = torch._C._current_graph_task_id()
+        if task == -1 and _deferred_depth == 0:
+            rc = _lib.lib().msr_sr_accum(acc.data_ptr(), grad.data_ptr(), int(f32), n, seed, int(first),
+                                         _lib.noise_mode(), None, stream)
+            _lib.check(rc, "msr_sr_accum")
+        else:
+            flags = (_lib.ACCUM_ZERO_INIT if first else 0) | (_lib.ACCUM_GRAD_F32 if f32 else 0)
+            with _queue_lock:
+                q = _queues.setdefault(acc.device, _AccumQueue())
+                if acc.data_ptr() in q.accs or (q.stream is not None and q.stream != stream):
+                    q.flush()   # keep per-buffer order and one stream per launch
+                q.items.append(_lib.AccumItem(acc.data_ptr(), grad.data_ptr(), n, seed, flags))
+                q.keep.append((acc, grad))
+                q.accs.add(acc.data_ptr())
+                q.nbytes += grad.element_size() * n
+                q.stream = stream
+                if q.nbytes >= TritonSRAccumulator.max_deferred_bytes:
+                    q.flush()
+                if task != -1 and task not in _callback_tasks:
+                    _callback_tasks.add(task)
+                    torch.autograd.Variable._execution_engine.queue_callback(_flush_all)
         del p.grad
 
     @staticmethod
+    @contextlib.contextmanager
+    def deferred():
+        """Queue the accumulations of hooks called directly (outside a backward
+        pass) and launch them together on exit."""
+        global _deferred_depth
+        with _queue_lock:
+            _deferred_depth += 1
+        try:
+            yield
+        finally:
+            with _queue_lock:
+                _deferred_depth -= 1
+            _flush_all()
+
+    @staticmethod
     def reassign_grad_buffer(model):
+        _flush_all()
         for _, p in model.named_parameters():
             if p.requires_grad and hasattr(p, "acc_grad"):
                 p.grad = p.acc_grad

@@ -130,36 +130,92 @@ __device__ __forceinline__ int clamp_valid(int64_t n, int64_t o0) {
 // (c) SR gradient accumulation   (muon_sr/triton_adamw.py:206-229)
 // ---------------------------------------------------------------------------
 
+// One 8-element group of acc <- SR(acc + grad): offsets o0 .. o0+7 of a tensor
+// of n elements (valid = how many exist).
+template <int MODE, bool GF32, bool ZERO, bool VEC>
+__device__ __forceinline__ void accum_group(uint16_t *__restrict__ acc, const void *__restrict__ grad,
+                                            const Noise &ns, int64_t o0, int valid) {
+    float a[8], g[8];
+    if constexpr (ZERO) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = 0.0f;
+    } else {
+        uint32_t w[4];
+        load_bf16x8<VEC>(acc, o0, valid, w);
+        unpack8(w, a);
+    }
+    if constexpr (GF32) {
+        load_f32x8<VEC>(static_cast<const float *>(grad), o0, valid, g);
+    } else {
+        uint32_t w[4];
+        load_bf16x8<VEC>(static_cast<const uint16_t *>(grad), o0, valid, w);
+        unpack8(w, g);
+    }
+    uint32_t r[8];
+    noise8<MODE>(ns, o0, valid, r);
+    uint32_t out[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        out[j] = pack2(sr_bf16(a[2 * j] + g[2 * j], r[2 * j]), sr_bf16(a[2 * j + 1] + g[2 * j + 1], r[2 * j + 1]));
+    store_bf16x8<VEC>(acc, o0, valid, out);
+}
+
 template <int MODE, bool GF32, bool ZERO, bool VEC>
 __global__ __launch_bounds__(THREADS) void sr_accum_kernel(uint16_t *__restrict__ acc, const void *__restrict__ grad,
                                                           int64_t n, Noise ns) {
     const int64_t groups = (n + 7) >> 3;
     for (int64_t t = (int64_t)blockIdx.x * THREADS + threadIdx.x; t < groups; t += (int64_t)gridDim.x * THREADS) {
         const int64_t o0 = t << 3;
-        const int valid = clamp_valid(n, o0);
-        float a[8], g[8];
-        if constexpr (ZERO) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) a[j] = 0.0f;
-        } else {
-            uint32_t w[4];
-            load_bf16x8<VEC>(acc, o0, valid, w);
-            unpack8(w, a);
+        accum_group<MODE, GF32, ZERO, VEC>(acc, grad, ns, o0, clamp_valid(n, o0));
+    }
+}
+
+// Many tensors in one launch (the hooks of a backward pass, deferred).  Tensor
+// t owns groups [gstart[t], gstart[t+1]) of the launch's group space; its
+// offsets, and so its noise counters, start at 0, so the result equals one
+// sr_accum_kernel launch per tensor.
+constexpr int ACC_MAXT = 80;
+constexpr uint32_t ACC_ZERO = 1, ACC_F32 = 2, ACC_VEC = 4;
+struct AccumMultiArgs {
+    int count;
+    int64_t gstart[ACC_MAXT + 1];
+    uint16_t *acc[ACC_MAXT];
+    const void *grad[ACC_MAXT];
+    int64_t n[ACC_MAXT];
+    PhiloxKey key[ACC_MAXT];
+    uint32_t flags[ACC_MAXT];
+};
+
+template <int MODE>
+__global__ __launch_bounds__(THREADS) void sr_accum_multi_kernel(AccumMultiArgs a) {
+    __shared__ int64_t s_start[ACC_MAXT + 1];
+    for (int i = threadIdx.x; i <= a.count; i += THREADS) s_start[i] = a.gstart[i];
+    __syncthreads();
+    const int64_t total = s_start[a.count];
+    for (int64_t gi = (int64_t)blockIdx.x * THREADS + threadIdx.x; gi < total; gi += (int64_t)gridDim.x * THREADS) {
+        int lo = 0, hi = a.count - 1;   // last t with s_start[t] <= gi
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_start[mid] <= gi) lo = mid; else hi = mid - 1;
         }
-        if constexpr (GF32) {
-            load_f32x8<VEC>(static_cast<const float *>(grad), o0, valid, g);
-        } else {
-            uint32_t w[4];
-            load_bf16x8<VEC>(static_cast<const uint16_t *>(grad), o0, valid, w);
-            unpack8(w, g);
+        const int t = lo;
+        const int64_t o0 = (gi - s_start[t]) << 3;
+        const int valid = clamp_valid(a.n[t], o0);
+        Noise ns;
+        ns.key = a.key[t];
+        ns.inject = nullptr;
+        uint16_t *acc = a.acc[t];
+        const void *grad = a.grad[t];
+        switch (a.flags[t]) {
+            case 0: accum_group<MODE, false, false, false>(acc, grad, ns, o0, valid); break;
+            case ACC_ZERO: accum_group<MODE, false, true, false>(acc, grad, ns, o0, valid); break;
+            case ACC_F32: accum_group<MODE, true, false, false>(acc, grad, ns, o0, valid); break;
+            case ACC_F32 | ACC_ZERO: accum_group<MODE, true, true, false>(acc, grad, ns, o0, valid); break;
+            case ACC_VEC: accum_group<MODE, false, false, true>(acc, grad, ns, o0, valid); break;
+            case ACC_VEC | ACC_ZERO: accum_group<MODE, false, true, true>(acc, grad, ns, o0, valid); break;
+            case ACC_VEC | ACC_F32: accum_group<MODE, true, false, true>(acc, grad, ns, o0, valid); break;
+            default: accum_group<MODE, true, true, true>(acc, grad, ns, o0, valid); break;
         }
-        uint32_t r[8];
-        noise8<MODE>(ns, o0, valid, r);
-        uint32_t out[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            out[j] = pack2(sr_bf16(a[2 * j] + g[2 * j], r[2 * j]), sr_bf16(a[2 * j + 1] + g[2 * j + 1], r[2 * j + 1]));
-        store_bf16x8<VEC>(acc, o0, valid, out);
     }
 }
 
@@ -675,6 +731,53 @@ int msr_sr_accum(uint16_t *acc, const void *grad, int32_t grad_is_f32, int64_t n
     }
 #undef LAUNCH_ACC
     return check_launch("msr_sr_accum");
+}
+
+int msr_sr_accum_multi(const msr_accum_item *items, int32_t count, int32_t noise_mode, msr_stream_t stream) {
+    if (count < 0 || (count > 0 && !items)) { set_error("msr_sr_accum_multi: bad arguments"); return MSR_ERR_ARG; }
+    if (noise_mode != NOISE_TRITON && noise_mode != NOISE_PHILOX8) {
+        set_error("msr_sr_accum_multi: noise_mode must be TRITON or PHILOX8 (got %d)", (int)noise_mode);
+        return MSR_ERR_ARG;
+    }
+    for (int32_t i = 0; i < count; ++i) {
+        const msr_accum_item &it = items[i];
+        if (it.n < 0 || (it.n > 0 && (!it.acc || !it.grad)) ||
+            (it.flags & ~(MSR_ACCUM_ZERO_INIT | MSR_ACCUM_GRAD_F32))) {
+            set_error("msr_sr_accum_multi: bad item %d", (int)i);
+            return MSR_ERR_ARG;
+        }
+    }
+    hipStream_t s = (hipStream_t)stream;
+    int32_t i = 0;
+    while (i < count) {
+        AccumMultiArgs a;
+        a.count = 0;
+        int64_t g = 0;
+        for (; i < count && a.count < ACC_MAXT; ++i) {
+            const msr_accum_item &it = items[i];
+            if (it.n == 0) continue;
+            const int t = a.count++;
+            const bool f32 = (it.flags & MSR_ACCUM_GRAD_F32) != 0;
+            a.gstart[t] = g;
+            a.acc[t] = it.acc;
+            a.grad[t] = it.grad;
+            a.n[t] = it.n;
+            a.key[t] = seed_key(it.seed, 0);
+            a.flags[t] = ((it.flags & MSR_ACCUM_ZERO_INIT) ? ACC_ZERO : 0u) | (f32 ? ACC_F32 : 0u) |
+                         ((aligned(it.acc, 16) && aligned(it.grad, 16)) ? ACC_VEC : 0u);
+            g += (it.n + 7) / 8;
+        }
+        if (a.count == 0) break;
+        a.gstart[a.count] = g;
+        const unsigned grid = grid_for(g, THREADS);
+        if (noise_mode == NOISE_TRITON)
+            hipLaunchKernelGGL((sr_accum_multi_kernel<NOISE_TRITON>), dim3(grid), dim3(THREADS), 0, s, a);
+        else
+            hipLaunchKernelGGL((sr_accum_multi_kernel<NOISE_PHILOX8>), dim3(grid), dim3(THREADS), 0, s, a);
+        const int rc = check_launch("msr_sr_accum_multi");
+        if (rc) return rc;
+    }
+    return MSR_OK;
 }
 
 int msr_adamw_bf16_step(uint16_t *p, const uint16_t *g, uint16_t *ema, uint16_t *ema_sq, int64_t n, float lr,

@@ -54,6 +54,11 @@ def test_argument_validation_without_gpu(lib):
     assert lib.msr_sr_accum(None, None, 0, -1, 0, 0, 1, None, None) == 1001
     assert lib.msr_sr_accum(1, 1, 0, 10, 0, 0, 7, None, None) == 1001
     assert lib.msr_sr_accum(1, 1, 0, 10, 0, 0, 2, None, None) == 1001   # INJECT without a buffer
+    from muon_sr_amd import _lib
+    bad = (_lib.AccumItem * 1)(_lib.AccumItem(1, 1, 10, 0, 8))
+    assert lib.msr_sr_accum_multi(bad, 1, 1, None) == 1001          # unknown flag
+    ok = (_lib.AccumItem * 1)(_lib.AccumItem(1, 1, 10, 0, 0))
+    assert lib.msr_sr_accum_multi(ok, 1, 2, None) == 1001           # INJECT is not offered
     size = ctypes.c_size_t(0)
     assert lib.msr_ns_workspace_bytes(2, 100, 60, ctypes.byref(size)) == 0
     # two 256x256-padded X layouts x2 (ping-pong) + A + B, bf16, plus partial sums

@@ -91,6 +91,44 @@ def test_sr_accum_vs_oracle(L, n, mode):
                 assert np.array_equal(dev_to_u16(acc), exp), (gname, zero, misalign)
 
 
+@pytest.mark.parametrize("mode", [O.NOISE_TRITON, O.NOISE_PHILOX8])
+def test_sr_accum_multi_equals_single_launches(L, mode):
+    """One multi-tensor launch (200 items: more than one launch's worth, ragged
+    sizes, unaligned views, fp32 grads, zero-init) equals one msr_sr_accum per
+    item, bit for bit."""
+    from muon_sr_amd import _lib
+    rng = np.random.default_rng(5 + mode)
+    sizes = [0, 1, 7, 8, 9, 1000, 100003, 4096, 333] + list(rng.integers(1, 20000, 191))
+    items, singles, accs_m, accs_s, keep = [], [], [], [], []
+    for i, n in enumerate(sizes):
+        n = int(n)
+        f32 = i % 5 == 3
+        zero = i % 7 == 2
+        acc0 = rng_bf16(rng, n, 1e-3)
+        am, as_ = u16_to_dev(acc0), u16_to_dev(acc0)
+        if i % 4 == 1:   # unaligned accumulators
+            am, as_ = unaligned(am), unaligned(as_)
+        if f32:
+            g = np_to_dev((rng.standard_normal(n) * 1e-3).astype(np.float32))
+        else:
+            g = u16_to_dev(rng_bf16(rng, n, 1e-3))
+            if i % 6 == 5:
+                g = unaligned(g)
+        seed = int(rng.integers(0, 2**32))
+        flags = (_lib.ACCUM_ZERO_INIT if zero else 0) | (_lib.ACCUM_GRAD_F32 if f32 else 0)
+        items.append(_lib.AccumItem(am.data_ptr(), g.data_ptr(), n, seed, flags))
+        singles.append((as_, g, f32, n, seed, zero))
+        accs_m.append(am)
+        accs_s.append(as_)
+        keep.append(g)
+    arr = (_lib.AccumItem * len(items))(*items)
+    check(L, L.msr_sr_accum_multi(arr, len(items), mode, stream()), "multi")
+    for as_, g, f32, n, seed, zero in singles:
+        check(L, L.msr_sr_accum(as_.data_ptr(), g.data_ptr(), int(f32), n, seed, int(zero), mode, None, stream()))
+    for i, (am, as_) in enumerate(zip(accs_m, accs_s)):
+        assert np.array_equal(dev_to_u16(am), dev_to_u16(as_)), (i, sizes[i])
+
+
 # ---------------------------------------------------------------------------
 # BF16-moment AdamW
 # ---------------------------------------------------------------------------

@@ -95,6 +95,11 @@ int msr_adamw_bf16_step(uint16_t *p, const uint16_t *g, uint16_t *ema, uint16_t 
  *   [ceil(n/block)], qmap1 (signed) / qmap2 (unsigned) fp32 [256].
  *   qtable: NULL, or a device copy of msr_quant_table_build(qmap1, qmap2)
  *   (16-byte aligned) -- the same codes from a bucketed threshold table.
+ *   With block 256, a qtable and 16-byte aligned p/g (8-byte aligned codes),
+ *   whole pairs of blocks run through a fast kernel (correctly rounded sqrt and
+ *   quotients from fp32 sequences valid on checked ranges, exact fallback
+ *   per wave outside them) and the rest through the general kernel; both give
+ *   the reference's bits.
  * quantized == 0: state1/state2 are bf16 moments [n]; absmax/qmap unused.
  * block: power of two in [32, 4096].  bc1 = 1-b1^step, bc2 = 1-b2^step.
  * Streams: p uses SEED, bf16 m SEED+1, bf16 v SEED+2 (inject: uint16 [3][n]).
@@ -173,10 +178,21 @@ int msr_quant_table_build(const float *qmap_signed, const float *qmap_unsigned, 
 
 /* Device self-check of a table against the search for every float bit
  * pattern u in [bits_lo, bits_hi] (<= bits(1.0f)): signed map at +x and -x,
- * unsigned map at x.  counts[i] = mismatches found by work-group i. */
+ * unsigned map at x, through both the two-level lookup of the general 8-bit
+ * kernel and the flat table of the fast one.  counts[i] = mismatches found by
+ * work-group i. */
 int msr_quant_table_check(const void *qtable, const float *qmap_signed, const float *qmap_unsigned,
                           uint32_t bits_lo, uint32_t bits_hi, uint32_t *counts, int32_t n_counts,
                           msr_stream_t stream);
+
+/* Device self-check of the fast kernel's correctly rounded building blocks
+ * against the IEEE operations, over the float bit patterns u in
+ * [bits_lo, bits_hi]: kind 0 sqrt (u <= bits(2^62)); kind 1 reciprocal and
+ * kind 2 quotient m/d for 16 hashed m per d (bits(2^-60) <= u < bits(2)).
+ * counts[i] = mismatches found by work-group i.  Test support: no
+ * counterpart in the reference. */
+int msr_fastmath_check(int32_t kind, uint32_t bits_lo, uint32_t bits_hi, uint32_t *counts, int32_t n_counts,
+                       msr_stream_t stream);
 
 /* Batched bf16 GEMM  D[b] = alpha * P[b] Q[b]^T + beta * C[b]  (fp32 accumulate, RNE bf16 out).
  * P: [M][K] (row stride ldp), Q: [N][K] (ldq), C/D: [M][N] (ldc/ldd); C may be NULL when beta == 0.

@@ -50,6 +50,7 @@ SIGNATURES = {
     "msr_quant_table_bytes": (ctypes.c_size_t, []),
     "msr_quant_table_build": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t]),
     "msr_quant_table_check": (ctypes.c_int, [_P, _P, _P, _U32, _U32, _P, _I32, _P]),
+    "msr_fastmath_check": (ctypes.c_int, [_I32, _U32, _U32, _P, _I32, _P]),
     "msr_gemm_nt": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
                                    _I64, _I64, _I64, _I64, _F, _F, _P]),
 }

@@ -1,0 +1,795 @@
+// 8-bit blockwise AdamW for gfx950 (muon_sr/triton_adamw_8bit.py:27-99): the fused
+// quantized step, the bf16-moment step of excluded tensors, the quantizer
+// diagnostics and the quantizer tables.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <algorithm>
+#include <utility>
+#include <vector>
+
+#include "common.hpp"
+#include "vecio.hpp"
+#include "../../include/muon_sr_amd.h"
+
+namespace msr {
+
+// ---------------------------------------------------------------------------
+// 8-bit blockwise AdamW   (muon_sr/triton_adamw_8bit.py:27-99)
+// ---------------------------------------------------------------------------
+
+struct Adam8Args {
+    uint16_t *p;
+    const uint16_t *g;
+    void *s1;
+    void *s2;
+    float *absmax1;
+    float *absmax2;
+    const float *qmap1;
+    const float *qmap2;
+    const QuantTable *qtable;
+    int64_t n;
+    int64_t qb0;   // first quantization block this launch handles (the rest of the tensor is done elsewhere)
+    float lr, b1, b2, eps, wd, bc1, bc2;
+    Noise ns_p, ns_m, ns_v;
+};
+
+struct Adam8Consts {
+    float one_m_b1, one_m_b2, step_c, eps_c, decay;
+};
+
+__device__ __forceinline__ Adam8Consts adam8_consts(const Adam8Args &a) {
+    Adam8Consts c;
+    c.one_m_b1 = 1.0f - a.b1;
+    c.one_m_b2 = 1.0f - a.b2;
+    const float sqrt_bc2 = sqrtf(a.bc2);
+    c.step_c = (a.lr * sqrt_bc2) / a.bc1;     // :74  LR * sqrt(BC2) / BC1
+    c.eps_c = sqrt_bc2 * a.eps;               // :74  sqrt(BC2) * EPS
+    c.decay = 1.0f - a.lr * a.wd;             // :74  (1 - LR * WD)
+    return c;
+}
+
+// Threads per quantization block: BLOCK/8.  Work-group size: max(256, BLOCK/8).
+// QTAB: requantize through the bucketed threshold table (standard codebooks),
+// else through the reference search; both give the search's codes.
+template <int MODE, int BLOCK, bool VEC, bool QTAB>
+__global__ __launch_bounds__((BLOCK / 8 > THREADS) ? BLOCK / 8 : THREADS) void adamw8bit_quant_kernel(Adam8Args a) {
+    constexpr int TPB = BLOCK / 8;
+    constexpr int WG = TPB > THREADS ? TPB : THREADS;
+    constexpr int QB_PER_WG = WG / TPB;
+    constexpr int NWAVES = WG / 64;
+    __shared__ float q1s[256], q2s[256];
+    __shared__ float red_m[NWAVES], red_v[NWAVES];
+    __shared__ uint32_t s_oct[QTAB ? QT_OCT : 1];
+    __shared__ uint2 s_bkt[QTAB ? QT_MAX_BKT : 1];
+    for (int i = threadIdx.x; i < 256; i += WG) {
+        q1s[i] = a.qmap1[i];
+        q2s[i] = a.qmap2[i];
+    }
+    if constexpr (QTAB) {
+        const uint32_t nb = a.qtable->n_bkt;
+        for (int i = threadIdx.x; i < QT_OCT; i += WG) s_oct[i] = a.qtable->oct[i];
+        for (uint32_t i = threadIdx.x; i < nb; i += WG) s_bkt[i] = a.qtable->bkt[i];
+    }
+    __syncthreads();
+    const Adam8Consts c = adam8_consts(a);
+    uint8_t *m8 = static_cast<uint8_t *>(a.s1);
+    uint8_t *v8 = static_cast<uint8_t *>(a.s2);
+    const int64_t nblocks = (a.n + BLOCK - 1) / BLOCK;
+    const int sub = threadIdx.x / TPB;       // quant block within the work-group
+    const int lane_q = threadIdx.x % TPB;    // thread within the quant block
+    const int64_t stride = (int64_t)gridDim.x * QB_PER_WG;
+
+    // raw inputs of one 8-element group; the next group is fetched while the
+    // current one is computed
+    struct Raw {
+        uint32_t wp[4], wg[4];
+        uint2 mc, vc;
+        float ms, vs;
+    };
+    auto fetch = [&](int64_t qb, Raw &r) {
+        const bool ok = qb < nblocks;
+        const int64_t o0 = qb * BLOCK + lane_q * 8;
+        const int valid = ok ? clamp_valid(a.n, o0) : 0;
+        load_bf16x8<VEC>(a.p, o0, valid, r.wp);
+        load_bf16x8<VEC>(a.g, o0, valid, r.wg);
+        if (VEC && valid == 8) {
+            const u32x2_t mc = ld_nt2(m8 + o0), vc = ld_nt2(v8 + o0);
+            r.mc = make_uint2(mc.x, mc.y);
+            r.vc = make_uint2(vc.x, vc.y);
+        } else {
+            uint32_t cm[8], cv[8];
+            load_u8x8<false>(m8, o0, valid, 127u, cm);
+            load_u8x8<false>(v8, o0, valid, 0u, cv);
+            r.mc = make_uint2(cm[0] | cm[1] << 8 | cm[2] << 16 | cm[3] << 24, cm[4] | cm[5] << 8 | cm[6] << 16 | cm[7] << 24);
+            r.vc = make_uint2(cv[0] | cv[1] << 8 | cv[2] << 16 | cv[3] << 24, cv[4] | cv[5] << 8 | cv[6] << 16 | cv[7] << 24);
+        }
+        r.ms = ok ? a.absmax1[qb] : 0.0f;
+        r.vs = ok ? a.absmax2[qb] : 0.0f;
+    };
+
+    int64_t qb = a.qb0 + (int64_t)blockIdx.x * QB_PER_WG + sub;
+    Raw nxt;
+    fetch(qb, nxt);
+    for (int64_t qb0 = a.qb0 + (int64_t)blockIdx.x * QB_PER_WG; qb0 < nblocks; qb0 += stride, qb += stride) {
+        const Raw cur = nxt;
+        if (qb0 + stride < nblocks) fetch(qb + stride, nxt);
+        const bool qb_ok = qb < nblocks;
+        const int64_t o0 = qb * BLOCK + lane_q * 8;
+        const int valid = qb_ok ? clamp_valid(a.n, o0) : 0;
+        float p[8], g[8], m[8], v[8];
+        unpack8(cur.wp, p);
+        unpack8(cur.wg, g);
+        uint32_t rp[8];
+        noise8<MODE>(a.ns_p, o0, valid, rp);
+        float mmax = 0.0f, vmax = 0.0f;
+        uint32_t op[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t mcj = ((j < 4 ? cur.mc.x : cur.mc.y) >> (8 * (j & 3))) & 0xffu;
+            const uint32_t vcj = ((j < 4 ? cur.vc.x : cur.vc.y) >> (8 * (j & 3))) & 0xffu;
+            float mj = q1s[mcj] * cur.ms;                                 // :65
+            float vj = q2s[vcj] * cur.vs;                                 // :66
+            const bool fin = fabsf(g[j]) < __builtin_huge_valf();         // :70
+            mj = fin ? a.b1 * mj + c.one_m_b1 * g[j] : 0.0f;              // :71
+            vj = fin ? a.b2 * vj + (c.one_m_b2 * g[j]) * g[j] : 0.0f;     // :72
+            const float upd = (p[j] - (c.step_c * mj) / (sqrtf(vj) + c.eps_c)) * c.decay;  // :74
+            const uint32_t pin = (j & 1) ? (cur.wp[j >> 1] >> 16) : (cur.wp[j >> 1] & 0xffffu);
+            op[j] = fin ? sr_bf16(upd, rp[j]) : pin;                      // :75-78
+            m[j] = mj;
+            v[j] = vj;
+            if (j < valid) {
+                mmax = fmaxf(mmax, fabsf(mj));
+                vmax = fmaxf(vmax, fabsf(vj));
+            }
+        }
+        uint32_t wo[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wo[j] = pack2(op[2 * j], op[2 * j + 1]);
+        store_bf16x8<VEC>(a.p, o0, valid, wo);
+
+        // block absmax (:80-81): shuffles inside the wave, LDS across waves
+#pragma unroll
+        for (int off = (TPB < 64 ? TPB : 64) / 2; off >= 1; off >>= 1) {
+            mmax = fmaxf(mmax, __shfl_xor(mmax, off, 64));
+            vmax = fmaxf(vmax, __shfl_xor(vmax, off, 64));
+        }
+        if constexpr (TPB > 64) {
+            constexpr int WPQ = TPB / 64;  // waves per quant block
+            const int wave = threadIdx.x / 64;
+            if ((threadIdx.x & 63) == 0) {
+                red_m[wave] = mmax;
+                red_v[wave] = vmax;
+            }
+            __syncthreads();
+            const int w0 = (wave / WPQ) * WPQ;
+            mmax = red_m[w0];
+            vmax = red_v[w0];
+#pragma unroll
+            for (int w = 1; w < WPQ; ++w) {
+                mmax = fmaxf(mmax, red_m[w0 + w]);
+                vmax = fmaxf(vmax, red_v[w0 + w]);
+            }
+            __syncthreads();
+        }
+        const float md = mmax > 0.0f ? mmax : 1.0f;                       // :82
+        const float vd = vmax > 0.0f ? vmax : 1.0f;                       // :83
+        const double rmd = 1.0 / (double)md;
+        const double rvd = 1.0 / (double)vd;
+        const double mlim = fmin((double)md * 0x1p-150, 1.7976931348623157e308);
+        uint32_t mc[8], vc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float xm = quotient_signed(m[j], rmd, mlim);            // m / md, :82
+            const float xv = quotient_unsigned(v[j], rvd);                // v / vd, :83
+            if constexpr (QTAB) {
+                mc[j] = quantize_lookup(xm, s_oct, s_bkt, true);          // :84
+                vc[j] = quantize_lookup(xv, s_oct, s_bkt, false);         // :85
+            } else {
+                mc[j] = quantize_search(xm, q1s, true);
+                vc[j] = quantize_search(xv, q2s, false);
+            }
+        }
+        store_u8x8<VEC>(m8, o0, valid, mc);
+        store_u8x8<VEC>(v8, o0, valid, vc);
+        if (qb_ok && lane_q == 0) {
+            a.absmax1[qb] = mmax;                                         // :86
+            a.absmax2[qb] = vmax;                                         // :87
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fast 8-bit step: block 256, standard codebooks, full 16-byte-aligned blocks.
+//
+// A wave owns two quantization blocks (64 lanes x 8 elements) per iteration
+// and walks the tensor in a grid-stride loop, fetching its next pair while it
+// computes the current one.  Per pair the wave first forms the new moments and
+// the two block maxima, then takes one of two branches, uniformly:
+//  * fast: every gradient finite, max v' < 2^62 and both block divisors in
+//    [2^-60, 2).  The update uses sqrt_rn, the requantization quotients use
+//    rcp_rn/div_rn and the codes come from the flat table; all of these equal
+//    the IEEE operations on these ranges (see common.hpp);
+//  * exact: anything else (non-finite gradients, extreme moments) goes through
+//    the reference arithmetic with IEEE sqrt/division, the double-precision
+//    quotients and the reference search, as in adamw8bit_quant_kernel.
+// Both branches produce the reference's bits; the fast one with about half
+// the VALU work, which bounds this kernel on gfx950.
+// ---------------------------------------------------------------------------
+
+constexpr int F8_THREADS = 256;              // 4 waves
+constexpr int F8_PAIR = 512;                 // elements per wave-iteration (2 blocks of 256)
+
+struct Raw8 {
+    u32x4_t p, g;
+    u32x2_t mc, vc;
+    float ms, vs;
+};
+
+__device__ __forceinline__ uint32_t byte_of(u32x2_t w, int j) { return ((j < 4 ? w.x : w.y) >> (8 * (j & 3))) & 0xffu; }
+__device__ __forceinline__ float bf16_at(u32x4_t w, int j) {
+    const uint32_t x = (j >> 1) == 0 ? w.x : (j >> 1) == 1 ? w.y : (j >> 1) == 2 ? w.z : w.w;
+    return (j & 1) ? bf16_hi(x) : bf16_lo(x);
+}
+
+// Word k (0..3) of a 4-word vector, and the vector with word k replaced, for a
+// loop index k: selects, so the rolled loops below keep everything in registers.
+__device__ __forceinline__ uint32_t word_at(u32x4_t w, int k) { return k == 0 ? w.x : k == 1 ? w.y : k == 2 ? w.z : w.w; }
+__device__ __forceinline__ u32x4_t with_word(u32x4_t w, int k, uint32_t x) {
+    w.x = k == 0 ? x : w.x;
+    w.y = k == 1 ? x : w.y;
+    w.z = k == 2 ? x : w.z;
+    w.w = k == 3 ? x : w.w;
+    return w;
+}
+
+// The reference arithmetic for one full pair: the rare branch of the fast
+// kernel.  Element loops stay rolled and the moments are recomputed for the
+// requantization pass, so this branch needs fewer registers than the fast one
+// and does not lower the kernel's occupancy.
+template <int MODE>
+__device__ __forceinline__ void adam8_pair_exact(const Adam8Args &a, const Raw8 &cur, int64_t o0, int64_t qb,
+                                                 const float *q1s, const float *q2s) {
+    const Adam8Consts c = adam8_consts(a);
+    uint8_t *m8 = static_cast<uint8_t *>(a.s1);
+    uint8_t *v8 = static_cast<uint8_t *>(a.s2);
+    // moments of element j, with non-finite gradients masked (:65-72)
+    auto moments = [&](int j, float &mj, float &vj, float &gj, bool &fin) {
+        const uint32_t gw = word_at(cur.g, j >> 1);
+        gj = (j & 1) ? bf16_hi(gw) : bf16_lo(gw);
+        mj = q1s[byte_of(cur.mc, j)] * cur.ms;                               // :65
+        vj = q2s[byte_of(cur.vc, j)] * cur.vs;                               // :66
+        fin = fabsf(gj) < __builtin_huge_valf();                             // :70
+        mj = fin ? a.b1 * mj + c.one_m_b1 * gj : 0.0f;                       // :71
+        vj = fin ? a.b2 * vj + (c.one_m_b2 * gj) * gj : 0.0f;                // :72
+    };
+    float mmax = 0.0f, vmax = 0.0f;
+    u32x4_t pout = cur.p;
+#pragma unroll 1
+    for (int j = 0; j < 8; ++j) {
+        float mj, vj, gj;
+        bool fin;
+        moments(j, mj, vj, gj, fin);
+        const uint32_t pw = word_at(cur.p, j >> 1);
+        const float pj = (j & 1) ? bf16_hi(pw) : bf16_lo(pw);
+        const float upd = (pj - (c.step_c * mj) / (sqrtf(vj) + c.eps_c)) * c.decay;   // :74
+        const uint32_t op = fin ? sr_bf16(upd, noise1<MODE>(a.ns_p, o0 + j)) : ((pw >> (16 * (j & 1))) & 0xffffu);  // :75-78
+        const uint32_t ow = word_at(pout, j >> 1);
+        pout = with_word(pout, j >> 1, (j & 1) ? ((ow & 0xffffu) | (op << 16)) : ((ow & 0xffff0000u) | op));
+        mmax = fmaxf(mmax, fabsf(mj));
+        vmax = fmaxf(vmax, fabsf(vj));
+    }
+    st_nt4(a.p + o0, pout);
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) {                                // :80-81
+        mmax = fmaxf(mmax, __shfl_xor(mmax, off, 64));
+        vmax = fmaxf(vmax, __shfl_xor(vmax, off, 64));
+    }
+    const float md = mmax > 0.0f ? mmax : 1.0f;                              // :82
+    const float vd = vmax > 0.0f ? vmax : 1.0f;                              // :83
+    const double rmd = 1.0 / (double)md, rvd = 1.0 / (double)vd;
+    const double mlim = fmin((double)md * 0x1p-150, 1.7976931348623157e308);
+    uint32_t mc0 = 0, mc1 = 0, vc0 = 0, vc1 = 0;
+#pragma unroll 1
+    for (int j = 0; j < 8; ++j) {
+        float mj, vj, gj;
+        bool fin;
+        moments(j, mj, vj, gj, fin);
+        const uint32_t mc = quantize_search(quotient_signed(mj, rmd, mlim), q1s, true);     // :82,84
+        const uint32_t vc = quantize_search(quotient_unsigned(vj, rvd), q2s, false);        // :83,85
+        const uint32_t sh = 8u * (uint32_t)(j & 3);
+        if (j < 4) { mc0 |= mc << sh; vc0 |= vc << sh; } else { mc1 |= mc << sh; vc1 |= vc << sh; }
+    }
+    st_nt2(m8 + o0, u32x2_t{mc0, mc1});
+    st_nt2(v8 + o0, u32x2_t{vc0, vc1});
+    if ((threadIdx.x & 31) == 0) {
+        a.absmax1[qb] = mmax;                                                // :86
+        a.absmax2[qb] = vmax;                                                // :87
+    }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(F8_THREADS) void adamw8bit_fast_kernel(Adam8Args a, int64_t npairs) {
+    __shared__ float q1s[256], q2s[256];
+    __shared__ uint32_t s_flat[3 * QF_N];
+    for (int i = threadIdx.x; i < 256; i += F8_THREADS) {
+        q1s[i] = a.qmap1[i];
+        q2s[i] = a.qmap2[i];
+    }
+    for (int i = threadIdx.x; i < 3 * QF_N; i += F8_THREADS) s_flat[i] = a.qtable->flat[i];
+    __syncthreads();
+    const Adam8Consts c = adam8_consts(a);
+    const float b1 = vgpr(a.b1), omb1 = vgpr(c.one_m_b1), b2 = vgpr(a.b2), omb2 = vgpr(c.one_m_b2);
+    const float step_c = vgpr(c.step_c), eps_c = vgpr(c.eps_c), decay = vgpr(c.decay);
+    uint8_t *m8 = static_cast<uint8_t *>(a.s1);
+    uint8_t *v8 = static_cast<uint8_t *>(a.s2);
+    const int lane = threadIdx.x & 63;
+    const int64_t wstride = (int64_t)gridDim.x * (F8_THREADS / 64);
+    auto fetch = [&](int64_t pr, Raw8 &r) {
+        const int64_t o0 = pr * F8_PAIR + lane * 8;
+        const int64_t qb = pr * 2 + (lane >> 5);
+        r.p = ld_nt4(a.p + o0);
+        r.g = ld_nt4(a.g + o0);
+        r.mc = ld_nt2(m8 + o0);
+        r.vc = ld_nt2(v8 + o0);
+        r.ms = a.absmax1[qb];
+        r.vs = a.absmax2[qb];
+    };
+    int64_t pr = (int64_t)blockIdx.x * (F8_THREADS / 64) + (threadIdx.x >> 6);
+    Raw8 nxt;
+    if (pr < npairs) fetch(pr, nxt);
+    for (; pr < npairs; pr += wstride) {
+        const Raw8 cur = nxt;
+        if (pr + wstride < npairs) fetch(pr + wstride, nxt);
+        const int64_t o0 = pr * F8_PAIR + lane * 8;
+        const int64_t qb = pr * 2 + (lane >> 5);
+        float g[8], m[8], v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) g[j] = bf16_at(cur.g, j);
+        // a sum of the 8 gradients is finite iff all of them are (or it overflows: exact branch)
+        const float gsum = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
+        float mx = 0.0f, vx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float mq = q1s[byte_of(cur.mc, j)] * cur.ms;                // :65
+            const float vq = q2s[byte_of(cur.vc, j)] * cur.vs;                // :66
+            m[j] = b1 * mq + omb1 * g[j];                                     // :71
+            v[j] = b2 * vq + (omb2 * g[j]) * g[j];                            // :72
+            mx = fmaxf(mx, fabsf(m[j]));
+            vx = fmaxf(vx, v[j]);
+        }
+        halfwave_max2(mx, vx);                                                // :80-81
+        const float md = mx > 0.0f ? mx : 1.0f;                               // :82
+        const float vd = vx > 0.0f ? vx : 1.0f;                               // :83
+        // Finite gradients and block scales make m' finite or +-inf and v' >= 0 finite or +inf
+        // (never NaN), so the maxima above are exact and the bounds below catch every inf.
+        const bool ok = fabsf(gsum) < __builtin_huge_valf() && fabsf(cur.ms) < __builtin_huge_valf() &&
+                        cur.vs >= 0.0f && cur.vs < __builtin_huge_valf() && vx < 0x1p62f && md >= 0x1p-60f &&
+                        md < 2.0f && vd >= 0x1p-60f && vd < 2.0f;
+        if (__builtin_amdgcn_ballot_w64(!ok) != 0) {
+            adam8_pair_exact<MODE>(a, cur, o0, qb, q1s, q2s);
+            continue;
+        }
+        uint32_t rp[8], w[8];
+        noise8<MODE>(a.ns_p, o0, 8, rp);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float den = sqrt_rn(v[j]) + eps_c;                          // :74
+            const float upd = (bf16_at(cur.p, j) - (step_c * m[j]) / den) * decay;
+            w[j] = __float_as_uint(upd) + rp[j];                              // :75-78 (SR)
+        }
+        st_nt4(a.p + o0, u32x4_t{__builtin_amdgcn_perm(w[1], w[0], 0x07060302u), __builtin_amdgcn_perm(w[3], w[2], 0x07060302u),
+                                 __builtin_amdgcn_perm(w[5], w[4], 0x07060302u), __builtin_amdgcn_perm(w[7], w[6], 0x07060302u)});
+        const float ym = rcp_rn(md), yv = rcp_rn(vd);
+        uint32_t rm[8], rv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            rm[j] = qf_signed(div_rn(m[j], md, ym), s_flat);                  // :82,84
+            rv[j] = qf_unsigned(div_rn(v[j], vd, yv), s_flat + 2 * QF_N);    // :83,85
+        }
+        st_nt2(m8 + o0, u32x2_t{pack_codes(rm[0], rm[1], rm[2], rm[3]), pack_codes(rm[4], rm[5], rm[6], rm[7])});
+        st_nt2(v8 + o0, u32x2_t{pack_codes(rv[0], rv[1], rv[2], rv[3]), pack_codes(rv[4], rv[5], rv[6], rv[7])});
+        if ((lane & 31) == 0) {
+            a.absmax1[qb] = mx;                                               // :86
+            a.absmax2[qb] = vx;                                               // :87
+        }
+    }
+}
+
+// Excluded tensors: bf16 moments with SR on both moment stores (:90-99).
+template <int MODE, bool VEC>
+__global__ __launch_bounds__(THREADS) void adamw8bit_bf16_kernel(Adam8Args a) {
+    const Adam8Consts c = adam8_consts(a);
+    uint16_t *m16 = static_cast<uint16_t *>(a.s1);
+    uint16_t *v16 = static_cast<uint16_t *>(a.s2);
+    const int64_t groups = (a.n + 7) >> 3;
+    for (int64_t t = (int64_t)blockIdx.x * THREADS + threadIdx.x; t < groups; t += (int64_t)gridDim.x * THREADS) {
+        const int64_t o0 = t << 3;
+        const int valid = clamp_valid(a.n, o0);
+        uint32_t wp[4], wg[4], wm[4], wv[4];
+        load_bf16x8<VEC>(a.p, o0, valid, wp);
+        load_bf16x8<VEC>(a.g, o0, valid, wg);
+        load_bf16x8<VEC>(m16, o0, valid, wm);
+        load_bf16x8<VEC>(v16, o0, valid, wv);
+        float p[8], g[8], m[8], v[8];
+        unpack8(wp, p); unpack8(wg, g); unpack8(wm, m); unpack8(wv, v);
+        uint32_t rp[8], rm[8], rv[8];
+        noise8<MODE>(a.ns_p, o0, valid, rp);
+        noise8<MODE>(a.ns_m, o0, valid, rm);
+        noise8<MODE>(a.ns_v, o0, valid, rv);
+        uint32_t op[8], om[8], ov[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bool fin = fabsf(g[j]) < __builtin_huge_valf();
+            const float mj = fin ? a.b1 * m[j] + c.one_m_b1 * g[j] : 0.0f;
+            const float vj = fin ? a.b2 * v[j] + (c.one_m_b2 * g[j]) * g[j] : 0.0f;
+            const float upd = (p[j] - (c.step_c * mj) / (sqrtf(vj) + c.eps_c)) * c.decay;
+            const uint32_t pin = (j & 1) ? (wp[j >> 1] >> 16) : (wp[j >> 1] & 0xffffu);
+            op[j] = fin ? sr_bf16(upd, rp[j]) : pin;
+            om[j] = sr_bf16(mj, rm[j]);
+            ov[j] = sr_bf16(vj, rv[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            wp[j] = pack2(op[2 * j], op[2 * j + 1]);
+            wm[j] = pack2(om[2 * j], om[2 * j + 1]);
+            wv[j] = pack2(ov[2 * j], ov[2 * j + 1]);
+        }
+        store_bf16x8<VEC>(a.p, o0, valid, wp);
+        store_bf16x8<VEC>(m16, o0, valid, wm);
+        store_bf16x8<VEC>(v16, o0, valid, wv);
+    }
+}
+
+
+__global__ __launch_bounds__(THREADS) void quantize_kernel(const float *x, uint8_t *out, int64_t n,
+                                                          const float *qmap, int is_signed, const QuantTable *qt) {
+    __shared__ float q[256];
+    __shared__ uint32_t s_oct[QT_OCT];
+    __shared__ uint2 s_bkt[QT_MAX_BKT];
+    for (int i = threadIdx.x; i < 256; i += THREADS) q[i] = qmap[i];
+    if (qt) {
+        for (int i = threadIdx.x; i < QT_OCT; i += THREADS) s_oct[i] = qt->oct[i];
+        for (uint32_t i = threadIdx.x; i < qt->n_bkt; i += THREADS) s_bkt[i] = qt->bkt[i];
+    }
+    __syncthreads();
+    for (int64_t i = (int64_t)blockIdx.x * THREADS + threadIdx.x; i < n; i += (int64_t)gridDim.x * THREADS)
+        out[i] = (uint8_t)(qt ? quantize_lookup(x[i], s_oct, s_bkt, is_signed != 0)
+                              : quantize_search(x[i], q, is_signed != 0));
+}
+
+// Counts, per work-group, the floats x = bits(u) for u in [lo, hi] where the
+// table disagrees with the search: signed map at x and -x, unsigned map at x.
+__global__ __launch_bounds__(THREADS) void quant_table_check_kernel(const QuantTable *qt, const float *q1,
+                                                                    const float *q2, uint32_t lo, uint32_t hi,
+                                                                    uint32_t *counts) {
+    __shared__ float s1[256], s2[256];
+    __shared__ uint32_t s_oct[QT_OCT];
+    __shared__ uint2 s_bkt[QT_MAX_BKT];
+    __shared__ uint32_t s_flat[3 * QF_N];
+    __shared__ uint32_t red[THREADS];
+    for (int i = threadIdx.x; i < 256; i += THREADS) { s1[i] = q1[i]; s2[i] = q2[i]; }
+    for (int i = threadIdx.x; i < QT_OCT; i += THREADS) s_oct[i] = qt->oct[i];
+    for (uint32_t i = threadIdx.x; i < qt->n_bkt; i += THREADS) s_bkt[i] = qt->bkt[i];
+    for (int i = threadIdx.x; i < 3 * QF_N; i += THREADS) s_flat[i] = qt->flat[i];
+    __syncthreads();
+    uint32_t bad = 0;
+    const uint64_t span = (uint64_t)hi - lo + 1;
+    for (uint64_t i = (uint64_t)blockIdx.x * THREADS + threadIdx.x; i < span; i += (uint64_t)gridDim.x * THREADS) {
+        const float x = __uint_as_float(lo + (uint32_t)i);
+        const uint32_t cp = quantize_search(x, s1, true), cn = quantize_search(-x, s1, true);
+        const uint32_t cu = quantize_search(x, s2, false);
+        bad += quantize_lookup(x, s_oct, s_bkt, true) != cp;
+        bad += quantize_lookup(-x, s_oct, s_bkt, true) != cn;
+        bad += quantize_lookup(x, s_oct, s_bkt, false) != cu;
+        // flat table (fast kernel): every x in [0, 1] and x in [-1, 0) (never -0)
+        bad += ((qf_signed(x, s_flat) >> 16) & 0xffu) != cp;
+        if (x != 0.0f) bad += ((qf_signed(-x, s_flat) >> 16) & 0xffu) != cn;
+        bad += ((qf_unsigned(x, s_flat + 2 * QF_N) >> 16) & 0xffu) != cu;
+    }
+    red[threadIdx.x] = bad;
+    __syncthreads();
+    for (int w = THREADS / 2; w > 0; w >>= 1) {
+        if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) counts[blockIdx.x] = red[0];
+}
+
+// Counts, per work-group, mismatches between a fast building block and the IEEE
+// operation over the float bit patterns u in [lo, hi]:
+//   kind 0: sqrt_rn(x) vs sqrtf(x)            (x in [0, 2^62])
+//   kind 1: rcp_rn(d) vs 1/d                  (d in [2^-60, 2))
+//   kind 2: div_rn(m, d, rcp_rn(d)) vs m/d    (d in [2^-60, 2), 16 hashed m per d with
+//           2^-63 d <= |m| <= d; for |m| < 2^-100 only the sign and zero-ness must agree)
+__device__ __forceinline__ uint32_t mix32(uint32_t x) {
+    x ^= x >> 16; x *= 0x7feb352du; x ^= x >> 15; x *= 0x846ca68bu; x ^= x >> 16;
+    return x;
+}
+
+__global__ __launch_bounds__(THREADS) void fastmath_check_kernel(int kind, uint32_t lo, uint32_t hi, uint32_t *counts) {
+    __shared__ uint32_t red[THREADS];
+    uint32_t bad = 0;
+    const uint64_t span = (uint64_t)hi - lo + 1;
+    for (uint64_t i = (uint64_t)blockIdx.x * THREADS + threadIdx.x; i < span; i += (uint64_t)gridDim.x * THREADS) {
+        const uint32_t u = lo + (uint32_t)i;
+        const float x = __uint_as_float(u);
+        if (kind == 0) {
+            bad += __float_as_uint(sqrt_rn(x)) != __float_as_uint(sqrtf(x));
+        } else if (kind == 1) {
+            bad += __float_as_uint(rcp_rn(x)) != __float_as_uint(1.0f / x);
+        } else {
+            const float y = rcp_rn(x);
+            for (uint32_t k = 0; k < 16; ++k) {
+                const uint32_t h = mix32(u * 16u + k);
+                // |m| = d * 2^-s * (1 + f), s in [0, 63], clamped to d: covers the whole quotient range
+                const uint32_t s = h & 63u;
+                float m = ldexpf(x, -(int)s) * (1.0f + (float)(mix32(h) >> 8) * 0x1p-24f);
+                if (m > x) m = x;
+                if (h & 0x80000000u) m = -m;
+                const float q = div_rn(m, x, y), e = m / x;
+                if (fabsf(m) >= 0x1p-100f) bad += __float_as_uint(q) != __float_as_uint(e);
+                else bad += (signbit(q) != signbit(e)) || ((q == 0.0f) != (m == 0.0f));
+            }
+        }
+    }
+    red[threadIdx.x] = bad;
+    __syncthreads();
+    for (int w = THREADS / 2; w > 0; w >>= 1) {
+        if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) counts[blockIdx.x] = red[0];
+}
+
+}  // namespace msr
+
+using namespace msr;
+
+static inline Noise make_noise(uint32_t seed, uint32_t k, const uint16_t *inject, int64_t stream_stride) {
+    Noise ns;
+    ns.key = seed_key(seed, k);
+    ns.inject = inject ? inject + (int64_t)k * stream_stride : nullptr;
+    return ns;
+}
+
+#define MSR_CHECK_MODE(mode, inject)                                                         \
+    do {                                                                                     \
+        if ((mode) < 0 || (mode) > 2) { set_error("noise_mode %d is not 0, 1 or 2", (int)(mode)); return MSR_ERR_ARG; } \
+        if ((mode) == NOISE_INJECT && !(inject)) { set_error("noise_mode INJECT needs an inject buffer"); return MSR_ERR_ARG; } \
+    } while (0)
+
+template <int MODE, int BLOCK>
+static void launch_quant_mode(bool vec, bool qtab, const Adam8Args &a, hipStream_t s, unsigned grid, int wg) {
+    if (qtab) {
+        if (vec) hipLaunchKernelGGL((adamw8bit_quant_kernel<MODE, BLOCK, true, true>), dim3(grid), dim3(wg), 0, s, a);
+        else hipLaunchKernelGGL((adamw8bit_quant_kernel<MODE, BLOCK, false, true>), dim3(grid), dim3(wg), 0, s, a);
+    } else {
+        if (vec) hipLaunchKernelGGL((adamw8bit_quant_kernel<MODE, BLOCK, true, false>), dim3(grid), dim3(wg), 0, s, a);
+        else hipLaunchKernelGGL((adamw8bit_quant_kernel<MODE, BLOCK, false, false>), dim3(grid), dim3(wg), 0, s, a);
+    }
+}
+
+template <int BLOCK>
+static void launch_quant(int mode, bool vec, const Adam8Args &a, hipStream_t s, int64_t nblocks) {
+    constexpr int TPB = BLOCK / 8;
+    constexpr int WG = TPB > THREADS ? TPB : THREADS;
+    constexpr int QB_PER_WG = WG / TPB;
+    const unsigned grid = grid_for(nblocks - a.qb0, QB_PER_WG, 256 * 8);
+    const bool qtab = a.qtable != nullptr;
+    if (mode == NOISE_TRITON) launch_quant_mode<NOISE_TRITON, BLOCK>(vec, qtab, a, s, grid, WG);
+    else if (mode == NOISE_PHILOX8) launch_quant_mode<NOISE_PHILOX8, BLOCK>(vec, qtab, a, s, grid, WG);
+    else launch_quant_mode<NOISE_INJECT, BLOCK>(vec, qtab, a, s, grid, WG);
+}
+
+#ifndef MSR_F8_GRID_CAP
+#define MSR_F8_GRID_CAP 1024   // 4 work-groups (16 waves) per CU on 256 CUs
+#endif
+
+// Fast kernel over the first 2 * npairs blocks (block 256); returns blocks done.
+static int64_t launch_fast8(int mode, const Adam8Args &a, hipStream_t s, int64_t nfull) {
+    const int64_t npairs = nfull / 2;
+    if (npairs == 0) return 0;
+    const unsigned grid = grid_for(npairs, F8_THREADS / 64, MSR_F8_GRID_CAP);
+    if (mode == NOISE_TRITON) hipLaunchKernelGGL((adamw8bit_fast_kernel<NOISE_TRITON>), dim3(grid), dim3(F8_THREADS), 0, s, a, npairs);
+    else if (mode == NOISE_PHILOX8) hipLaunchKernelGGL((adamw8bit_fast_kernel<NOISE_PHILOX8>), dim3(grid), dim3(F8_THREADS), 0, s, a, npairs);
+    else hipLaunchKernelGGL((adamw8bit_fast_kernel<NOISE_INJECT>), dim3(grid), dim3(F8_THREADS), 0, s, a, npairs);
+    return 2 * npairs;
+}
+
+extern "C" {
+
+int msr_adamw8bit_step(uint16_t *p, const uint16_t *g, void *state1, void *state2, float *absmax1, float *absmax2,
+                       const float *qmap1, const float *qmap2, const void *qtable, int64_t n, int32_t block,
+                       int32_t quantized, float lr,
+                       float beta1, float beta2, float eps, float weight_decay, float bc1, float bc2, uint32_t seed,
+                       int32_t noise_mode, const uint16_t *inject, msr_stream_t stream) {
+    if (n < 0 || (n > 0 && (!p || !g || !state1 || !state2))) { set_error("msr_adamw8bit_step: bad arguments"); return MSR_ERR_ARG; }
+    if (block < 32 || block > 4096 || (block & (block - 1))) {
+        set_error("msr_adamw8bit_step: block %d is not a power of two in [32, 4096]", (int)block);
+        return MSR_ERR_ARG;
+    }
+    if (quantized && (!absmax1 || !absmax2 || !qmap1 || !qmap2)) { set_error("msr_adamw8bit_step: quantized state needs absmax and qmaps"); return MSR_ERR_ARG; }
+    MSR_CHECK_MODE(noise_mode, inject);
+    if (n == 0) return MSR_OK;
+    Adam8Args a;
+    a.p = p; a.g = g; a.s1 = state1; a.s2 = state2; a.absmax1 = absmax1; a.absmax2 = absmax2;
+    a.qmap1 = qmap1; a.qmap2 = qmap2; a.n = n; a.qb0 = 0;
+    a.qtable = static_cast<const QuantTable *>(qtable);
+    if (a.qtable && !aligned(a.qtable, 16)) { set_error("msr_adamw8bit_step: qtable must be 16-byte aligned"); return MSR_ERR_ALIGN; }
+    a.lr = lr; a.b1 = beta1; a.b2 = beta2; a.eps = eps; a.wd = weight_decay; a.bc1 = bc1; a.bc2 = bc2;
+    a.ns_p = make_noise(seed, 0, inject, n);
+    a.ns_m = make_noise(seed, 1, inject, n);
+    a.ns_v = make_noise(seed, 2, inject, n);
+    hipStream_t s = (hipStream_t)stream;
+    if (quantized) {
+        const bool vec = aligned(p, 16) && aligned(g, 16) && aligned(state1, 8) && aligned(state2, 8);
+        const int64_t nblocks = (n + block - 1) / block;
+        // standard codebooks, block 256, aligned: the fast kernel takes the full block pairs
+        if (block == 256 && a.qtable && vec) a.qb0 = launch_fast8(noise_mode, a, s, n / 256);
+        if (a.qb0 == nblocks) return check_launch("msr_adamw8bit_step");
+        switch (block) {
+        case 32: launch_quant<32>(noise_mode, vec, a, s, nblocks); break;
+        case 64: launch_quant<64>(noise_mode, vec, a, s, nblocks); break;
+        case 128: launch_quant<128>(noise_mode, vec, a, s, nblocks); break;
+        case 256: launch_quant<256>(noise_mode, vec, a, s, nblocks); break;
+        case 512: launch_quant<512>(noise_mode, vec, a, s, nblocks); break;
+        case 1024: launch_quant<1024>(noise_mode, vec, a, s, nblocks); break;
+        case 2048: launch_quant<2048>(noise_mode, vec, a, s, nblocks); break;
+        default: launch_quant<4096>(noise_mode, vec, a, s, nblocks); break;
+        }
+    } else {
+        const bool vec = aligned(p, 16) && aligned(g, 16) && aligned(state1, 16) && aligned(state2, 16);
+        const unsigned grid = grid_for((n + 7) / 8, THREADS);
+        if (vec) { MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((adamw8bit_bf16_kernel<M, true>), dim3(grid), dim3(THREADS), 0, s, a)); }
+        else { MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((adamw8bit_bf16_kernel<M, false>), dim3(grid), dim3(THREADS), 0, s, a)); }
+    }
+    return check_launch("msr_adamw8bit_step");
+}
+
+int msr_quantize(const float *x, uint8_t *out, int64_t n, const float *qmap, int32_t is_signed, const void *qtable,
+                 msr_stream_t stream) {
+    if (n < 0 || (n > 0 && (!x || !out || !qmap))) { set_error("msr_quantize: bad arguments"); return MSR_ERR_ARG; }
+    if (n == 0) return MSR_OK;
+    hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(n, THREADS)), dim3(THREADS), 0, (hipStream_t)stream, x, out, n,
+                       qmap, is_signed, static_cast<const QuantTable *>(qtable));
+    return check_launch("msr_quantize");
+}
+
+size_t msr_quant_table_bytes(void) { return sizeof(QuantTable); }
+
+int msr_quant_table_build(const float *qmap_signed, const float *qmap_unsigned, void *table, size_t table_bytes) {
+    if (!qmap_signed || !qmap_unsigned || !table || table_bytes < sizeof(QuantTable)) {
+        set_error("msr_quant_table_build: need host codebooks and a host buffer of %zu bytes", sizeof(QuantTable));
+        return MSR_ERR_ARG;
+    }
+    QuantTable *t = static_cast<QuantTable *>(table);
+    memset(t, 0, sizeof(QuantTable));
+    const uint32_t ONE = 0x3f800000u;
+    uint32_t nb = 0;
+    // three sides: signed map x >= 0, signed map x < 0, unsigned map x >= 0
+    for (int side = 0; side < 3; ++side) {
+        const float *Q = side < 2 ? qmap_signed : qmap_unsigned;
+        const bool sgn = side < 2;
+        const bool neg = side == 1;
+        const uint32_t oct_base = (side == 2 ? 512u : 0u) + (neg ? 256u : 0u);
+        auto f = [&](uint32_t a) {
+            const float x = __builtin_bit_cast(float, a | (neg ? 0x80000000u : 0u));
+            return quantize_search(x, Q, sgn);
+        };
+        // change points of the monotone code over |x| bits a in [0, ONE], by bisection
+        std::vector<uint32_t> tr;
+        std::vector<std::pair<uint32_t, uint32_t>> stack{{0u, ONE}};
+        while (!stack.empty()) {
+            auto [lo, hi] = stack.back();
+            stack.pop_back();
+            if (f(lo) == f(hi)) continue;
+            if (hi == lo + 1) { tr.push_back(hi); continue; }
+            const uint32_t mid = lo + (hi - lo) / 2;
+            stack.push_back({mid, hi});
+            stack.push_back({lo, mid});
+        }
+        std::sort(tr.begin(), tr.end());
+        for (uint32_t e = 0; e < 128; ++e) {
+            const uint32_t base = e << 23;
+            std::vector<uint32_t> te;
+            for (uint32_t x : tr)
+                if ((x >> 23) == e) te.push_back(x);
+            int sh = 23;
+            auto ok = [&](int s) {
+                for (size_t i = 1; i < te.size(); ++i)
+                    if ((te[i] >> s) == (te[i - 1] >> s)) return false;
+                return true;
+            };
+            while (sh > 0 && !ok(sh)) --sh;
+            if (!ok(sh)) { set_error("msr_quant_table_build: two code changes one ulp apart"); return MSR_ERR_ARG; }
+            const uint32_t cnt = 1u << (23 - sh);
+            if (nb + cnt + 1 > (uint32_t)QT_MAX_BKT) { set_error("msr_quant_table_build: more than %d buckets", QT_MAX_BKT); return MSR_ERR_ARG; }
+            t->oct[oct_base + e] = (nb << 8) | (uint32_t)sh;
+            for (uint32_t k = 0; k < cnt; ++k) {
+                const uint32_t a0 = base + (k << sh);
+                const uint32_t a1 = a0 + (1u << sh) - 1;
+                uint32_t thr = 0xffffffffu;
+                for (uint32_t x : te)
+                    if (x > a0 && x <= a1) thr = x;
+                const uint32_t lo_code = a0 <= ONE ? f(a0) : f(ONE);
+                const uint32_t hi_code = thr != 0xffffffffu ? f(thr) : lo_code;
+                t->bkt[nb + k] = make_uint2(thr, lo_code | (hi_code << 8));
+            }
+            nb += cnt;
+        }
+        // exponents 128..255 (|x| > 1 cannot occur; 255 is NaN): the search's NaN code
+        const uint32_t nan_code = quantize_search(__builtin_bit_cast(float, 0x7fc00000u), Q, sgn);
+        t->bkt[nb] = make_uint2(0xffffffffu, nan_code | (nan_code << 8));
+        for (uint32_t e = 128; e < 256; ++e) t->oct[oct_base + e] = (nb << 8) | 23u;
+        nb += 1;
+    }
+    // the unsigned map never sees x < 0 (v >= 0); point that half at its NaN bucket
+    for (uint32_t e = 0; e < 256; ++e) t->oct[512 + 256 + e] = t->oct[512 + 255];
+    t->n_bkt = nb;
+
+    // flat table of the fast kernel: planes signed x >= 0, signed x < 0, unsigned
+    for (int plane = 0; plane < 3; ++plane) {
+        const float *Q = plane < 2 ? qmap_signed : qmap_unsigned;
+        const bool sgn = plane < 2;
+        const uint32_t sign = plane == 1 ? 0x80000000u : 0u;
+        for (int idx = 0; idx < QF_N; ++idx) {
+            const uint32_t key = QF_LO_KEY - 1u + (uint32_t)idx;
+            // code at lookup variable w (low 16 bits, complemented on the negative plane)
+            auto code_at = [&](uint32_t w) {
+                const uint32_t low = sign ? 0xffffu - w : w;
+                return quantize_search(__builtin_bit_cast(float, sign | (key << 16) | low), Q, sgn);
+            };
+            uint32_t entry;
+            if (idx == 0) {
+                // |x| < 2^-23: one code per sign (the fast kernel never forms x = -0)
+                entry = quantize_search(__builtin_bit_cast(float, sign | 1u), Q, sgn) << 16;
+            } else if (key == (127u << 7)) {
+                // [1, 1 + 2^-7): only |x| = 1 occurs
+                entry = quantize_search(__builtin_bit_cast(float, sign | ONE), Q, sgn) << 16;
+            } else {
+                const uint32_t c0 = code_at(0), c1 = code_at(0xffffu);
+                if (c0 == c1) {
+                    entry = c0 << 16;
+                } else {
+                    if (c1 != c0 + 1) { set_error("msr_quant_table_build: codes jump by %d in one bucket", (int)(c1 - c0)); return MSR_ERR_ARG; }
+                    uint32_t lo = 0, hi = 0xffffu;   // code_at(lo) == c0, code_at(hi) == c1
+                    while (hi - lo > 1) {
+                        const uint32_t mid = (lo + hi) / 2;
+                        if (code_at(mid) == c0) lo = mid; else hi = mid;
+                    }
+                    entry = (c0 << 16) | (0x10000u - hi);
+                }
+            }
+            t->flat[plane * QF_N + idx] = entry;
+        }
+    }
+    return MSR_OK;
+}
+
+int msr_quant_table_check(const void *qtable, const float *qmap_signed, const float *qmap_unsigned, uint32_t bits_lo,
+                          uint32_t bits_hi, uint32_t *counts, int32_t n_counts, msr_stream_t stream) {
+    if (!qtable || !qmap_signed || !qmap_unsigned || !counts || n_counts <= 0 || bits_hi < bits_lo ||
+        bits_hi > 0x3f800000u) {
+        set_error("msr_quant_table_check: bad arguments");
+        return MSR_ERR_ARG;
+    }
+    hipLaunchKernelGGL(quant_table_check_kernel, dim3((unsigned)n_counts), dim3(THREADS), 0, (hipStream_t)stream,
+                       static_cast<const QuantTable *>(qtable), qmap_signed, qmap_unsigned, bits_lo, bits_hi, counts);
+    return check_launch("msr_quant_table_check");
+}
+
+int msr_fastmath_check(int32_t kind, uint32_t bits_lo, uint32_t bits_hi, uint32_t *counts, int32_t n_counts,
+                       msr_stream_t stream) {
+    const uint32_t SQRT_HI = 0x5e800000u, RCP_LO = 0x21800000u, RCP_HI = 0x3fffffffu;   // 2^62, 2^-60, 2 - ulp
+    const bool range_ok = kind == 0 ? bits_hi <= SQRT_HI : (kind == 1 || kind == 2) && bits_lo >= RCP_LO && bits_hi <= RCP_HI;
+    if (!counts || n_counts <= 0 || bits_hi < bits_lo || !range_ok) {
+        set_error("msr_fastmath_check: bad arguments (kind %d, range %08x..%08x)", (int)kind, bits_lo, bits_hi);
+        return MSR_ERR_ARG;
+    }
+    hipLaunchKernelGGL(fastmath_check_kernel, dim3((unsigned)n_counts), dim3(THREADS), 0, (hipStream_t)stream, (int)kind,
+                       bits_lo, bits_hi, counts);
+    return check_launch("msr_fastmath_check");
+}
+
+}  // extern "C"

@@ -214,11 +214,26 @@ __host__ __device__ inline uint32_t quantize_search(float x, const float *Q, boo
 constexpr int QT_OCT = 2 * 512;
 constexpr int QT_MAX_BKT = 2048;
 
+// One-level table for the fast kernel (standard codebooks).  A quotient x with
+// bit pattern u, |x| <= 1, falls in bucket key = (u >> 16) & 0x7fff (exponent
+// and 7 mantissa bits); keys up to QF_LO_KEY - 1 (|x| < 2^-23) share entry 0,
+// so entry idx = max(key - (QF_LO_KEY - 1), 0) < QF_N.  Each bucket holds at
+// most one code change (checked when the table is built), so an entry is
+//     bits 0-15: c = 0x10000 - (low 16 bits of the change point), or 0
+//     bits 16-23: code at the bucket's low end
+// and code = ((low16 + entry) >> 16) & 0xff: the carry out of the low half adds
+// the step.  The negative half of the signed map is indexed by |x| with the low
+// 16 bits complemented, so its codes also rise with the lookup variable.
+// Planes: [0] signed x >= 0, [1] signed x < 0, [2] unsigned.
+constexpr uint32_t QF_LO_KEY = 104u << 7;                   // 2^-23
+constexpr int QF_N = (int)((127u << 7) - (QF_LO_KEY - 1u)) + 1;  // 2946
+
 struct QuantTable {
     uint32_t n_bkt;
     uint32_t pad[3];
     uint32_t oct[QT_OCT];
     uint2 bkt[QT_MAX_BKT];
+    uint32_t flat[3 * QF_N];
 };
 
 __host__ __device__ inline uint32_t quantize_lookup(float x, const uint32_t *oct, const uint2 *bkt, bool is_signed) {
@@ -246,6 +261,109 @@ __device__ __forceinline__ float quotient_signed(float m, double rd, double dlim
 // v / d for the unsigned map (v >= 0): below FLT_MIN every value, zero
 // included, codes to 0, so the double product alone decides the code.
 __device__ __forceinline__ float quotient_unsigned(float v, double rd) { return (float)((double)v * rd); }
+
+// ---------------------------------------------------------------------------
+// Correctly rounded fp32 building blocks for a stated input range.
+//
+// Measured on gfx950 (ns per wave64 instruction per SIMD): fp32 add/mul/fma and
+// integer add/and/or/xor/shift-right issue at ~1.05; any instruction with an
+// SGPR operand, max/min, compares, selects, v_perm, SDWA forms and f64 at
+// ~1.8; v_sqrt_f32/v_rcp_f32 at 3.4.  These sequences use the fast class where
+// the IEEE library sequences use compares, selects and range scaling.  Each is
+// checked against the IEEE operation over its whole input range on the GPU
+// (msr_fastmath_check).
+// ---------------------------------------------------------------------------
+
+// Opaque VGPR copy of a wave-uniform value, so arithmetic with it keeps the
+// fast issue rate (the compiler would otherwise read kernel arguments as SGPRs).
+__device__ __forceinline__ float vgpr(float x) {
+    float r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+
+// sqrt(v) correctly rounded, for v == +0 or v in [2^-149, 2^62].  v_sqrt_f32
+// (within 1 ulp) runs on v * 2^64, which is >= 2^-85, where the residuals
+// fma(s -+ 1ulp, s, -v) are exact; the root moves down a step when
+// v <= (s - 1ulp) * s and up a step when v > (s + 1ulp) * s, as in the IEEE
+// sequence, read off the residuals' sign bits.  At v = 0, s - 1ulp saturates to
+// 0 and both residuals are +0.  The result is unscaled by the exact 2^-32.
+__device__ __forceinline__ float sqrt_rn(float v) {
+    const float vs = v * 0x1p64f;
+    const float s = __builtin_amdgcn_sqrtf(vs);
+    const uint32_t sb = __float_as_uint(s);
+    const uint32_t sdn = __builtin_elementwise_sub_sat(sb, 1u);
+    const float rdn = __builtin_fmaf(__uint_as_float(sdn), s, -vs);
+    const float rup = __builtin_fmaf(__uint_as_float(sb + 1u), s, -vs);
+    const uint32_t r = sdn + (__float_as_uint(rdn) >> 31) + (__float_as_uint(rup) >> 31);
+    return __uint_as_float(r) * 0x1p-32f;
+}
+
+// RN(1/d) for d in [2^-60, 2): v_rcp_f32 and one Newton step.
+__device__ __forceinline__ float rcp_rn(float d) {
+    const float r0 = __builtin_amdgcn_rcpf(d);
+    const float e = __builtin_fmaf(-d, r0, 1.0f);
+    return __builtin_fmaf(e, r0, r0);
+}
+
+// RN(m/d) from y = RN(1/d) (Markstein): q0 = RN(m*y) is within an ulp of m/d,
+// the remainder m - d*q0 is exact while it is a normal number, and
+// RN(q0 + r*y) is then the rounded quotient: for d in [2^-60, 2) and
+// |m| in [2^-100, d].  For smaller |m| the quotient keeps m's sign and is +0
+// for m = +-0, which is all the codes need there: with d >= 2^-60 such an
+// |x| = |m/d| is below 2^-23, where every x of one sign codes alike.
+__device__ __forceinline__ float div_rn(float m, float d, float y) {
+    const float q0 = m * y;
+    const float r = __builtin_fmaf(-q0, d, m);
+    return __builtin_fmaf(r, y, q0);
+}
+
+// Signed code of x = RN(m/d) for the fast kernel (x != -0, |x| <= 1), as the
+// entry sum whose bits 16-23 are the code; `tab` is plane 0 of the flat table.
+__device__ __forceinline__ uint32_t qf_signed(float x, const uint32_t *tab) {
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t sm = (uint32_t)((int32_t)u >> 31);
+    const uint32_t idx = __builtin_elementwise_sub_sat((u >> 16) & 0x7fffu, QF_LO_KEY - 1u) + (sm & (uint32_t)QF_N);
+    return ((u ^ sm) & 0xffffu) + tab[idx];
+}
+
+// Unsigned code of x in [0, 1]; `tab` is plane 2 of the flat table.
+__device__ __forceinline__ uint32_t qf_unsigned(float x, const uint32_t *tab) {
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t idx = __builtin_elementwise_sub_sat((u >> 16) & 0x7fffu, QF_LO_KEY - 1u);
+    return (u & 0xffffu) + tab[idx];
+}
+
+// Bytes 2 of four entry sums, packed into one little-endian code word.
+__device__ __forceinline__ uint32_t pack_codes(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3) {
+    const uint32_t lo = __builtin_amdgcn_perm(r1, r0, 0x0c0c0602u);   // [r0.b2, r1.b2, 0, 0]
+    const uint32_t hi = __builtin_amdgcn_perm(r3, r2, 0x06020c0cu);   // [0, 0, r2.b2, r3.b2]
+    return lo | hi;
+}
+
+// Maxima of two non-negative, NaN-free fp32 values over each 32-lane half of a
+// wave64 (integer order equals float order there).  Rows of 16 lanes reduce
+// with DPP (quad_perm [1,0,3,2] and [2,3,0,1], row_ror 4 and 8); then
+// v_permlane16_swap(a, b) returns rows (a0, b0, a2, b2) and (a1, b1, a3, b3), so
+// one swap and a max leave rows (A01, B01, A23, B23), and a swap of that value
+// with itself spreads A and B over both rows of their half.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t x) {
+    return max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, true));
+}
+
+__device__ __forceinline__ void halfwave_max2(float &a, float &b) {
+    uint32_t x = __float_as_uint(a), y = __float_as_uint(b);
+    x = dpp_max_u32<0xB1>(x); y = dpp_max_u32<0xB1>(y);
+    x = dpp_max_u32<0x4E>(x); y = dpp_max_u32<0x4E>(y);
+    x = dpp_max_u32<0x124>(x); y = dpp_max_u32<0x124>(y);
+    x = dpp_max_u32<0x128>(x); y = dpp_max_u32<0x128>(y);
+    const auto s = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+    const uint32_t c = max((uint32_t)s[0], (uint32_t)s[1]);
+    const auto t = __builtin_amdgcn_permlane16_swap(c, c, false, false);
+    a = __uint_as_float(t[0]);
+    b = __uint_as_float(t[1]);
+}
 
 inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 

@@ -1,0 +1,112 @@
+// 8-element vector I/O for the element-wise kernels: every thread owns 8
+// consecutive elements (one 16-byte bf16 vector); the aligned fast path uses
+// vector loads and stores, the masked scalar path handles tails and unaligned views.
+#pragma once
+
+#include "common.hpp"
+
+namespace msr {
+
+constexpr int THREADS = 256;
+
+// ---------------------------------------------------------------------------
+// 8-element vector I/O (aligned fast path, masked scalar path at tails or for
+// unaligned views)
+// ---------------------------------------------------------------------------
+
+// Streaming accesses: every element-wise kernel touches each byte once, so the
+// aligned vector paths use non-temporal loads and stores (measured: the SR
+// accumulate over 7.8 GB goes from 5.2 to 5.6 TB/s).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4_t ld_nt4(const void *p) { return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p)); }
+__device__ __forceinline__ u32x2_t ld_nt2(const void *p) { return __builtin_nontemporal_load(reinterpret_cast<const u32x2_t *>(p)); }
+__device__ __forceinline__ f32x4_t ld_nt4f(const void *p) { return __builtin_nontemporal_load(reinterpret_cast<const f32x4_t *>(p)); }
+__device__ __forceinline__ void st_nt4(void *p, u32x4_t v) { __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t *>(p)); }
+__device__ __forceinline__ void st_nt2(void *p, u32x2_t v) { __builtin_nontemporal_store(v, reinterpret_cast<u32x2_t *>(p)); }
+
+template <bool VEC>
+__device__ __forceinline__ void load_bf16x8(const uint16_t *base, int64_t o0, int valid, uint32_t w[4]) {
+    if (VEC && valid == 8) {
+        const u32x4_t v = ld_nt4(base + o0);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t lo = (2 * j < valid) ? base[o0 + 2 * j] : 0u;
+            uint32_t hi = (2 * j + 1 < valid) ? base[o0 + 2 * j + 1] : 0u;
+            w[j] = lo | (hi << 16);
+        }
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store_bf16x8(uint16_t *base, int64_t o0, int valid, const uint32_t w[4]) {
+    if (VEC && valid == 8) {
+        st_nt4(base + o0, u32x4_t{w[0], w[1], w[2], w[3]});
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (2 * j < valid) base[o0 + 2 * j] = (uint16_t)(w[j] & 0xffffu);
+            if (2 * j + 1 < valid) base[o0 + 2 * j + 1] = (uint16_t)(w[j] >> 16);
+        }
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void load_f32x8(const float *base, int64_t o0, int valid, float f[8]) {
+    if (VEC && valid == 8) {
+        const f32x4_t a = ld_nt4f(base + o0);
+        const f32x4_t b = ld_nt4f(base + o0 + 4);
+        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+        f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = (j < valid) ? base[o0 + j] : 0.0f;
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void load_u8x8(const uint8_t *base, int64_t o0, int valid, uint32_t fill,
+                                          uint32_t c[8]) {
+    if (VEC && valid == 8) {
+        const u32x2_t v = ld_nt2(base + o0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            c[j] = (v.x >> (8 * j)) & 0xffu;
+            c[j + 4] = (v.y >> (8 * j)) & 0xffu;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = (j < valid) ? (uint32_t)base[o0 + j] : fill;
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store_u8x8(uint8_t *base, int64_t o0, int valid, const uint32_t c[8]) {
+    if (VEC && valid == 8) {
+        uint32_t x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+        uint32_t y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+        st_nt2(base + o0, u32x2_t{x, y});
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (j < valid) base[o0 + j] = (uint8_t)c[j];
+    }
+}
+
+__device__ __forceinline__ void unpack8(const uint32_t w[4], float f[8]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[2 * j] = bf16_lo(w[j]);
+        f[2 * j + 1] = bf16_hi(w[j]);
+    }
+}
+
+__device__ __forceinline__ int clamp_valid(int64_t n, int64_t o0) {
+    int64_t r = n - o0;
+    return r <= 0 ? 0 : (r >= 8 ? 8 : (int)r);
+}
+
+}  // namespace msr

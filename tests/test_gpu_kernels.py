@@ -332,6 +332,75 @@ def test_quant_table_exhaustive(L):
     assert int(counts.sum().item()) == 0
 
 
+SQRT_HI = 0x5E800000                     # bits(2^62)
+RCP_LO, RCP_HI = 0x21800000, 0x3FFFFFFF  # bits(2^-60), bits(2) - 1
+
+
+@pytest.mark.parametrize("kind,lo,hi", [
+    (0, 0, SQRT_HI),                       # sqrt: every float in [0, 2^62]
+    (1, RCP_LO, RCP_HI),                   # reciprocal: every float in [2^-60, 2)
+    (2, 0x3F800000, RCP_HI),               # quotient: every d in [1, 2), 16 m each
+    (2, RCP_LO, RCP_LO + (1 << 23) - 1),   # ... every d in [2^-60, 2^-59)
+    (2, 0x30000000, 0x307FFFFF),           # ... every d in [2^-31, 2^-30)
+])
+def test_fastmath_exhaustive(L, kind, lo, hi):
+    """The fast 8-bit kernel's sqrt, reciprocal and quotient equal the IEEE operations
+    on their whole input ranges (the quotient on a hashed sample of numerators)."""
+    nblk = 4096
+    counts = torch.zeros(nblk, dtype=torch.int32, device=DEV)
+    check(L, L.msr_fastmath_check(kind, lo, hi, counts.data_ptr(), nblk, stream()), "fastmath check")
+    assert int(counts.sum().item()) == 0
+
+
+@pytest.mark.parametrize("mode", [O.NOISE_PHILOX8, O.NOISE_TRITON, O.NOISE_INJECT])
+def test_adamw8bit_fast_kernel_vs_oracle(L, mode):
+    """Block 256, standard codebooks, aligned: full block pairs run through the fast kernel,
+    whose waves switch to the exact branch for pairs with non-finite gradients or extreme
+    moments; the odd last full block and the ragged tail run through the general kernel.
+    Bit-exact against the oracle (parameters, codes, block scales) over four steps."""
+    rng = np.random.default_rng(100 + mode)
+    block = 256
+    n = (1 << 19) + 3 * block + 77          # 2051 full blocks (odd) + a ragged tail
+    nb = (n + block - 1) // block
+    Q1, Q2 = O.create_dynamic_map(True), O.create_dynamic_map(False)
+    q1, q2, qt = np_to_dev(Q1), np_to_dev(Q2), qtable_dev(L)
+    p0 = rng_bf16(rng, n, 0.02)
+    s1, s2 = np.full(n, 127, np.uint8), np.zeros(n, np.uint8)
+    a1, a2 = np.zeros(nb, np.float32), np.zeros(nb, np.float32)
+    pd, s1d, s2d, a1d, a2d = u16_to_dev(p0), np_to_dev(s1), np_to_dev(s2), np_to_dev(a1), np_to_dev(a2)
+    pe = p0
+    lr, b1, b2, eps, wd = 3e-4, 0.9, 0.95, 1e-10, 0.01
+    pair = lambda i: slice(512 * i, 512 * (i + 1))  # noqa: E731
+    for step in range(1, 5):
+        g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+        if step == 1:
+            g[pair(3)][100] = np.nan            # non-finite gradient: exact branch
+            g[pair(7)] *= 3e21                  # v' above 2^62: exact branch
+            g[pair(11)] *= 1e-22                # block scales below 2^-60: exact branch
+            g[pair(13)] = 0.0                   # all-zero pair: fast branch, divisor 1
+        if step == 2:
+            g[pair(5)][7] = -np.inf
+            g[pair(17)][:256] *= 1e-30          # one tiny block next to a normal one
+        if step == 3:
+            g[pair(19)] *= 1e4                  # block scales in [2, ...): exact branch
+        g0 = O.f32_to_bf16_rne(g)
+        inj = rng.integers(0, 65536, 3 * n).astype(np.uint16)
+        seed = int(rng.integers(0, 2**32))
+        hyper = (lr, b1, b2, eps, wd, 1 - b1 ** step, 1 - b2 ** step)
+        spec = O.NoiseSpec(mode, seed, 0, inj[:n] if mode == O.NOISE_INJECT else None)
+        pe, s1, s2, a1, a2 = O.adamw8bit(pe, g0, s1, s2, a1, a2, Q1, Q2, block, True, *hyper, spec)
+        inj_d = np_to_dev(inj.view(np.int16)) if mode == O.NOISE_INJECT else None
+        _adam8_call(L, pd, u16_to_dev(g0), s1d, s2d, a1d, a2d, q1, q2, n, block, True, hyper, seed, mode, inj_d,
+                    qt=qt)
+        got = dev_to_u16(pd)
+        same = (got == pe) | (np.isnan(O.bf16_to_f32(got)) & np.isnan(O.bf16_to_f32(pe)))
+        assert same.all(), (step, np.flatnonzero(~same)[:10])
+        assert np.array_equal(s1d.cpu().numpy(), s1), step
+        assert np.array_equal(s2d.cpu().numpy(), s2), step
+        assert np.array_equal(a1d.cpu().numpy().view(np.uint32), a1.view(np.uint32)), step
+        assert np.array_equal(a2d.cpu().numpy().view(np.uint32), a2.view(np.uint32)), step
+
+
 def test_adamw8bit_extreme_moments(L):
     """Huge gradients (v overflows to inf), denormal-scale moments and -0: the
     exact-quotient and table paths against the oracle."""

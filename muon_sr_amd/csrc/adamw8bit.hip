@@ -217,8 +217,12 @@ __global__ __launch_bounds__((BLOCK / 8 > THREADS) ? BLOCK / 8 : THREADS) void a
 // the VALU work, which bounds this kernel on gfx950.
 // ---------------------------------------------------------------------------
 
-constexpr int F8_THREADS = 256;              // 4 waves
+#ifndef MSR_F8_WAVES
+#define MSR_F8_WAVES 4
+#endif
+constexpr int F8_THREADS = 64 * MSR_F8_WAVES;   // each wave owns 2 quant blocks (512 elements) per iteration
 constexpr int F8_PAIR = 512;                 // elements per wave-iteration (2 blocks of 256)
+constexpr int F8_DEFER = 64;                 // pairs a wave defers to its exact pass before flushing
 
 struct Raw8 {
     u32x4_t p, g;
@@ -308,91 +312,129 @@ __device__ __forceinline__ void adam8_pair_exact(const Adam8Args &a, const Raw8 
     }
 }
 
+#ifdef MSR_F8_WPE
+#define MSR_F8_ATTR __attribute__((amdgpu_waves_per_eu(MSR_F8_WPE, MSR_F8_WPE)))
+#else
+#define MSR_F8_ATTR
+#endif
 template <int MODE>
-__global__ __launch_bounds__(F8_THREADS) void adamw8bit_fast_kernel(Adam8Args a, int64_t npairs) {
+__global__ __launch_bounds__(F8_THREADS) MSR_F8_ATTR void adamw8bit_fast_kernel(Adam8Args a, int64_t npairs) {
     __shared__ float q1s[256], q2s[256];
-    __shared__ uint32_t s_flat[3 * QF_N];
+    __shared__ uint32_t s_flat[QF_TOTAL];
+    __shared__ uint32_t s_deferred[F8_THREADS / 64][F8_DEFER];
     for (int i = threadIdx.x; i < 256; i += F8_THREADS) {
         q1s[i] = a.qmap1[i];
         q2s[i] = a.qmap2[i];
     }
-    for (int i = threadIdx.x; i < 3 * QF_N; i += F8_THREADS) s_flat[i] = a.qtable->flat[i];
+    for (int i = threadIdx.x; i < QF_TOTAL; i += F8_THREADS) s_flat[i] = a.qtable->flat[i];
     __syncthreads();
     const Adam8Consts c = adam8_consts(a);
     const float b1 = vgpr(a.b1), omb1 = vgpr(c.one_m_b1), b2 = vgpr(a.b2), omb2 = vgpr(c.one_m_b2);
     const float step_c = vgpr(c.step_c), eps_c = vgpr(c.eps_c), decay = vgpr(c.decay);
-    uint8_t *m8 = static_cast<uint8_t *>(a.s1);
-    uint8_t *v8 = static_cast<uint8_t *>(a.s2);
-    const int lane = threadIdx.x & 63;
+    const uint32_t lo1 = vgpr(QF_LO1), scap = vgpr((uint32_t)QF_SCAP);
+    const char *pb = reinterpret_cast<const char *>(a.p), *gb = reinterpret_cast<const char *>(a.g);
+    const char *mb = static_cast<const char *>(a.s1), *vb = static_cast<const char *>(a.s2);
+    const uint32_t lane = threadIdx.x & 63u;
+    // the pair index is wave-uniform: addresses are a scalar base plus a fixed lane offset
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t wstride = (int64_t)gridDim.x * (F8_THREADS / 64);
     auto fetch = [&](int64_t pr, Raw8 &r) {
-        const int64_t o0 = pr * F8_PAIR + lane * 8;
-        const int64_t qb = pr * 2 + (lane >> 5);
-        r.p = ld_nt4(a.p + o0);
-        r.g = ld_nt4(a.g + o0);
-        r.mc = ld_nt2(m8 + o0);
-        r.vc = ld_nt2(v8 + o0);
-        r.ms = a.absmax1[qb];
-        r.vs = a.absmax2[qb];
+        r.p = ld_nt4(pb + pr * (2 * F8_PAIR) + lane * 16u);
+        r.g = ld_nt4(gb + pr * (2 * F8_PAIR) + lane * 16u);
+        r.mc = ld_nt2(mb + pr * F8_PAIR + lane * 8u);
+        r.vc = ld_nt2(vb + pr * F8_PAIR + lane * 8u);
+        r.ms = a.absmax1[pr * 2 + (lane >> 5)];
+        r.vs = a.absmax2[pr * 2 + (lane >> 5)];
     };
-    int64_t pr = (int64_t)blockIdx.x * (F8_THREADS / 64) + (threadIdx.x >> 6);
-    Raw8 nxt;
-    if (pr < npairs) fetch(pr, nxt);
-    for (; pr < npairs; pr += wstride) {
-        const Raw8 cur = nxt;
-        if (pr + wstride < npairs) fetch(pr + wstride, nxt);
-        const int64_t o0 = pr * F8_PAIR + lane * 8;
-        const int64_t qb = pr * 2 + (lane >> 5);
-        float g[8], m[8], v[8];
+    int64_t pr = (int64_t)blockIdx.x * (F8_THREADS / 64) + wave;
+    // Pairs that need the exact arithmetic are skipped by the streaming loop (nothing is
+    // written for them) and recorded in the wave's LDS list; they are done after the loop,
+    // so the exact code does not add to the loop's registers.
+    uint32_t *deferred = s_deferred[wave];
+    // One pair in flight: the next pair is fetched while the current one is computed.
+    for (;;) {
+        int ndef = 0;
+        Raw8 nxt;
+        if (pr < npairs) fetch(pr, nxt);
+        for (; pr < npairs; pr += wstride) {
+            const Raw8 raw = nxt;
+            if (pr + wstride < npairs) fetch(pr + wstride, nxt);
+            float p[8], g[8], m[8], v[8];
+            const u32x4_t pw = raw.p;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) g[j] = bf16_at(cur.g, j);
-        // a sum of the 8 gradients is finite iff all of them are (or it overflows: exact branch)
-        const float gsum = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
-        float mx = 0.0f, vx = 0.0f;
+            for (int j = 0; j < 8; ++j) {
+                p[j] = bf16_at(pw, j);
+                g[j] = bf16_at(raw.g, j);
+            }
+            // a sum of the 8 gradients is finite iff all of them are (or it overflows: exact)
+            const float gsum = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
+            float mx = 0.0f, vx = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float mq = q1s[byte_of(cur.mc, j)] * cur.ms;                // :65
-            const float vq = q2s[byte_of(cur.vc, j)] * cur.vs;                // :66
-            m[j] = b1 * mq + omb1 * g[j];                                     // :71
-            v[j] = b2 * vq + (omb2 * g[j]) * g[j];                            // :72
-            mx = fmaxf(mx, fabsf(m[j]));
-            vx = fmaxf(vx, v[j]);
-        }
-        halfwave_max2(mx, vx);                                                // :80-81
-        const float md = mx > 0.0f ? mx : 1.0f;                               // :82
-        const float vd = vx > 0.0f ? vx : 1.0f;                               // :83
-        // Finite gradients and block scales make m' finite or +-inf and v' >= 0 finite or +inf
-        // (never NaN), so the maxima above are exact and the bounds below catch every inf.
-        const bool ok = fabsf(gsum) < __builtin_huge_valf() && fabsf(cur.ms) < __builtin_huge_valf() &&
-                        cur.vs >= 0.0f && cur.vs < __builtin_huge_valf() && vx < 0x1p62f && md >= 0x1p-60f &&
-                        md < 2.0f && vd >= 0x1p-60f && vd < 2.0f;
-        if (__builtin_amdgcn_ballot_w64(!ok) != 0) {
-            adam8_pair_exact<MODE>(a, cur, o0, qb, q1s, q2s);
-            continue;
-        }
-        uint32_t rp[8], w[8];
-        noise8<MODE>(a.ns_p, o0, 8, rp);
+            for (int j = 0; j < 8; ++j) {
+                const float mq = q1s[byte_of(raw.mc, j)] * raw.ms;            // :65
+                const float vq = q2s[byte_of(raw.vc, j)] * raw.vs;            // :66
+                m[j] = b1 * mq + omb1 * g[j];                                 // :71
+                v[j] = b2 * vq + (omb2 * g[j]) * g[j];                        // :72
+                mx = fmaxf(mx, fabsf(m[j]));
+                vx = fmaxf(vx, v[j]);
+            }
+            const float ms = raw.ms, vs = raw.vs;
+            halfwave_max2(mx, vx);                                            // :80-81
+            const float md = mx > 0.0f ? mx : 1.0f;                           // :82
+            const float vd = vx > 0.0f ? vx : 1.0f;                           // :83
+            // Fast-branch conditions as sign bits of differences of non-negative bit patterns:
+            // finite gradients and block scales, vs >= +0 (then m' is finite or +-inf and v' >= 0
+            // finite or +inf, never NaN, so the maxima above are exact), max v' < 2^62 and both
+            // divisors in [2^-60, 2).
+            const int32_t FMAX = 0x7f7fffff, DLO = 0x21800000, DHI = 0x3fffffff, VXHI = 0x5e7fffff;
+            const int32_t gsb = (int32_t)(__float_as_uint(gsum) & 0x7fffffffu);
+            const int32_t msb = (int32_t)(__float_as_uint(ms) & 0x7fffffffu);
+            const int32_t vsb = (int32_t)__float_as_uint(vs), vxb = (int32_t)__float_as_uint(vx);
+            const int32_t mdb = (int32_t)__float_as_uint(md), vdb = (int32_t)__float_as_uint(vd);
+            const int32_t neg = (FMAX - gsb) | (FMAX - msb) | vsb | (FMAX - vsb) | (VXHI - vxb) | (mdb - DLO) |
+                                (DHI - mdb) | (vdb - DLO) | (DHI - vdb);
+            if (__builtin_amdgcn_ballot_w64(neg < 0) != 0) {
+                if (lane == 0) deferred[ndef] = (uint32_t)pr;
+                if (++ndef == F8_DEFER) {
+                    pr += wstride;
+                    break;
+                }
+                continue;
+            }
+            const int64_t o0 = pr * F8_PAIR + lane * 8;
+            const int64_t qb = pr * 2 + (lane >> 5);
+            uint32_t rp[8], w[8];
+            noise8<MODE>(a.ns_p, o0, 8, rp);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float den = sqrt_rn(v[j]) + eps_c;                          // :74
-            const float upd = (bf16_at(cur.p, j) - (step_c * m[j]) / den) * decay;
-            w[j] = __float_as_uint(upd) + rp[j];                              // :75-78 (SR)
-        }
-        st_nt4(a.p + o0, u32x4_t{__builtin_amdgcn_perm(w[1], w[0], 0x07060302u), __builtin_amdgcn_perm(w[3], w[2], 0x07060302u),
-                                 __builtin_amdgcn_perm(w[5], w[4], 0x07060302u), __builtin_amdgcn_perm(w[7], w[6], 0x07060302u)});
-        const float ym = rcp_rn(md), yv = rcp_rn(vd);
-        uint32_t rm[8], rv[8];
+            for (int j = 0; j < 8; ++j) {
+                const float den = sqrt_rn(v[j]) + eps_c;                      // :74
+                const float upd = (p[j] - (step_c * m[j]) / den) * decay;
+                w[j] = __float_as_uint(upd) + rp[j];                          // :75-78 (SR)
+            }
+            st_nt4(a.p + o0, u32x4_t{__builtin_amdgcn_perm(w[1], w[0], 0x07060302u), __builtin_amdgcn_perm(w[3], w[2], 0x07060302u),
+                                     __builtin_amdgcn_perm(w[5], w[4], 0x07060302u), __builtin_amdgcn_perm(w[7], w[6], 0x07060302u)});
+            const float ym = rcp_rn(md), yv = rcp_rn(vd);
+            uint32_t rm[8], rv[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            rm[j] = qf_signed(div_rn(m[j], md, ym), s_flat);                  // :82,84
-            rv[j] = qf_unsigned(div_rn(v[j], vd, yv), s_flat + 2 * QF_N);    // :83,85
+            for (int j = 0; j < 8; ++j) {
+                rm[j] = qf_signed(div_rn(m[j], md, ym), s_flat, lo1, scap);               // :82,84
+                rv[j] = qf_unsigned(div_rn(v[j], vd, yv), s_flat + QF_SIGNED, lo1);       // :83,85
+            }
+            st_nt2(static_cast<uint8_t *>(a.s1) + o0, u32x2_t{pack_codes(rm[0], rm[1], rm[2], rm[3]), pack_codes(rm[4], rm[5], rm[6], rm[7])});
+            st_nt2(static_cast<uint8_t *>(a.s2) + o0, u32x2_t{pack_codes(rv[0], rv[1], rv[2], rv[3]), pack_codes(rv[4], rv[5], rv[6], rv[7])});
+            if ((lane & 31) == 0) {
+                a.absmax1[qb] = mx;                                           // :86
+                a.absmax2[qb] = vx;                                           // :87
+            }
         }
-        st_nt2(m8 + o0, u32x2_t{pack_codes(rm[0], rm[1], rm[2], rm[3]), pack_codes(rm[4], rm[5], rm[6], rm[7])});
-        st_nt2(v8 + o0, u32x2_t{pack_codes(rv[0], rv[1], rv[2], rv[3]), pack_codes(rv[4], rv[5], rv[6], rv[7])});
-        if ((lane & 31) == 0) {
-            a.absmax1[qb] = mx;                                               // :86
-            a.absmax2[qb] = vx;                                               // :87
+        __builtin_amdgcn_wave_barrier();   // lane 0's list writes precede the wave's reads
+        for (int i = 0; i < ndef; ++i) {
+            const int64_t pe = (int64_t)__builtin_amdgcn_readfirstlane(deferred[i]);
+            Raw8 r;
+            fetch(pe, r);
+            adam8_pair_exact<MODE>(a, r, pe * F8_PAIR + lane * 8, pe * 2 + (lane >> 5), q1s, q2s);
         }
+        if (pr >= npairs) break;
     }
 }
 
@@ -466,12 +508,12 @@ __global__ __launch_bounds__(THREADS) void quant_table_check_kernel(const QuantT
     __shared__ float s1[256], s2[256];
     __shared__ uint32_t s_oct[QT_OCT];
     __shared__ uint2 s_bkt[QT_MAX_BKT];
-    __shared__ uint32_t s_flat[3 * QF_N];
+    __shared__ uint32_t s_flat[QF_TOTAL];
     __shared__ uint32_t red[THREADS];
     for (int i = threadIdx.x; i < 256; i += THREADS) { s1[i] = q1[i]; s2[i] = q2[i]; }
     for (int i = threadIdx.x; i < QT_OCT; i += THREADS) s_oct[i] = qt->oct[i];
     for (uint32_t i = threadIdx.x; i < qt->n_bkt; i += THREADS) s_bkt[i] = qt->bkt[i];
-    for (int i = threadIdx.x; i < 3 * QF_N; i += THREADS) s_flat[i] = qt->flat[i];
+    for (int i = threadIdx.x; i < QF_TOTAL; i += THREADS) s_flat[i] = qt->flat[i];
     __syncthreads();
     uint32_t bad = 0;
     const uint64_t span = (uint64_t)hi - lo + 1;
@@ -483,9 +525,9 @@ __global__ __launch_bounds__(THREADS) void quant_table_check_kernel(const QuantT
         bad += quantize_lookup(-x, s_oct, s_bkt, true) != cn;
         bad += quantize_lookup(x, s_oct, s_bkt, false) != cu;
         // flat table (fast kernel): every x in [0, 1] and x in [-1, 0) (never -0)
-        bad += ((qf_signed(x, s_flat) >> 16) & 0xffu) != cp;
-        if (x != 0.0f) bad += ((qf_signed(-x, s_flat) >> 16) & 0xffu) != cn;
-        bad += ((qf_unsigned(x, s_flat + 2 * QF_N) >> 16) & 0xffu) != cu;
+        bad += ((qf_signed(x, s_flat, QF_LO1, QF_SCAP) >> 16) & 0xffu) != cp;
+        if (x != 0.0f) bad += ((qf_signed(-x, s_flat, QF_LO1, QF_SCAP) >> 16) & 0xffu) != cn;
+        bad += ((qf_unsigned(x, s_flat + QF_SIGNED, QF_LO1) >> 16) & 0xffu) != cu;
     }
     red[threadIdx.x] = bad;
     __syncthreads();
@@ -583,13 +625,13 @@ static void launch_quant(int mode, bool vec, const Adam8Args &a, hipStream_t s, 
 }
 
 #ifndef MSR_F8_GRID_CAP
-#define MSR_F8_GRID_CAP 1024   // 4 work-groups (16 waves) per CU on 256 CUs
+#define MSR_F8_GRID_CAP 2048   // twice the resident work-groups (4 per CU on 256 CUs): measured best
 #endif
 
 // Fast kernel over the first 2 * npairs blocks (block 256); returns blocks done.
 static int64_t launch_fast8(int mode, const Adam8Args &a, hipStream_t s, int64_t nfull) {
     const int64_t npairs = nfull / 2;
-    if (npairs == 0) return 0;
+    if (npairs == 0 || npairs >= ((int64_t)1 << 31)) return 0;   // deferred pairs are recorded as int32
     const unsigned grid = grid_for(npairs, F8_THREADS / 64, MSR_F8_GRID_CAP);
     if (mode == NOISE_TRITON) hipLaunchKernelGGL((adamw8bit_fast_kernel<NOISE_TRITON>), dim3(grid), dim3(F8_THREADS), 0, s, a, npairs);
     else if (mode == NOISE_PHILOX8) hipLaunchKernelGGL((adamw8bit_fast_kernel<NOISE_PHILOX8>), dim3(grid), dim3(F8_THREADS), 0, s, a, npairs);
@@ -728,21 +770,23 @@ int msr_quant_table_build(const float *qmap_signed, const float *qmap_unsigned, 
     for (uint32_t e = 0; e < 256; ++e) t->oct[512 + 256 + e] = t->oct[512 + 255];
     t->n_bkt = nb;
 
-    // flat table of the fast kernel: planes signed x >= 0, signed x < 0, unsigned
-    for (int plane = 0; plane < 3; ++plane) {
+    // flat table of the fast kernel (layout in common.hpp)
+    for (int i = 0; i < QF_TOTAL; ++i) t->flat[i] = 0;
+    for (int plane = 0; plane < 3; ++plane) {          // signed x >= 0, signed x < 0, unsigned
         const float *Q = plane < 2 ? qmap_signed : qmap_unsigned;
         const bool sgn = plane < 2;
         const uint32_t sign = plane == 1 ? 0x80000000u : 0u;
-        for (int idx = 0; idx < QF_N; ++idx) {
-            const uint32_t key = QF_LO_KEY - 1u + (uint32_t)idx;
+        uint32_t *dst = t->flat + (plane == 2 ? QF_SIGNED : 0);
+        for (int k = 0; k < QF_N; ++k) {
+            const uint32_t key = QF_LO1 + (uint32_t)k;   // k = 0: every |x| < 2^-23
             // code at lookup variable w (low 16 bits, complemented on the negative plane)
             auto code_at = [&](uint32_t w) {
                 const uint32_t low = sign ? 0xffffu - w : w;
                 return quantize_search(__builtin_bit_cast(float, sign | (key << 16) | low), Q, sgn);
             };
             uint32_t entry;
-            if (idx == 0) {
-                // |x| < 2^-23: one code per sign (the fast kernel never forms x = -0)
+            if (k == 0) {
+                // one code per sign (the fast kernel never forms x = -0)
                 entry = quantize_search(__builtin_bit_cast(float, sign | 1u), Q, sgn) << 16;
             } else if (key == (127u << 7)) {
                 // [1, 1 + 2^-7): only |x| = 1 occurs
@@ -761,7 +805,8 @@ int msr_quant_table_build(const float *qmap_signed, const float *qmap_unsigned, 
                     entry = (c0 << 16) | (0x10000u - hi);
                 }
             }
-            t->flat[plane * QF_N + idx] = entry;
+            const int idx = plane == 1 ? (k == 0 ? QF_SCAP : (int)(0x7fffu - key - QF_LO1)) : k;
+            dst[idx] = entry;
         }
     }
     return MSR_OK;

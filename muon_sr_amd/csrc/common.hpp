@@ -53,14 +53,29 @@ __device__ __forceinline__ uint32_t pack2(uint32_t lo16, uint32_t hi16) { return
 constexpr uint32_t PHILOX_KA = 0x9E3779B9u, PHILOX_KB = 0xBB67AE85u;
 constexpr uint32_t PHILOX_RA = 0xD2511F53u, PHILOX_RB = 0xCD9E8D57u;
 
+// a ^ b ^ k.  With a wave-uniform key (UKEY) k is taken from an SGPR into one
+// v_bitop3_b32; the compiler's two v_xor_b32 would read the SGPR at the slow
+// issue rate as well.  A per-lane key (UKEY false) uses plain XORs.
+template <bool UKEY>
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t k) {
+    if constexpr (UKEY) {
+        uint32_t r;
+        asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x96" : "=v"(r) : "v"(a), "v"(b), "s"(k));
+        return r;
+    } else {
+        return a ^ b ^ k;
+    }
+}
+
+template <bool UKEY = true>
 __device__ __forceinline__ void philox10(uint32_t &c0, uint32_t &c1, uint32_t &c2, uint32_t &c3,
                                          uint32_t k0, uint32_t k1) {
 #pragma unroll
     for (int r = 0; r < 10; ++r) {
         uint64_t pa = (uint64_t)PHILOX_RA * c0;
         uint64_t pb = (uint64_t)PHILOX_RB * c2;
-        uint32_t n0 = (uint32_t)(pb >> 32) ^ c1 ^ k0;
-        uint32_t n2 = (uint32_t)(pa >> 32) ^ c3 ^ k1;
+        uint32_t n0 = xor3<UKEY>((uint32_t)(pb >> 32), c1, k0);
+        uint32_t n2 = xor3<UKEY>((uint32_t)(pa >> 32), c3, k1);
         c1 = (uint32_t)pb;
         c3 = (uint32_t)pa;
         c0 = n0;
@@ -72,6 +87,7 @@ __device__ __forceinline__ void philox10(uint32_t &c0, uint32_t &c1, uint32_t &c
 
 // Word 0 of Philox(ctr = (c0, 0, 0, 0), key).  With c1 = c2 = c3 = 0 the first
 // round reduces to c0' = k0, c2' = hi(RA*c0) ^ k1, c1' = 0, c3' = lo(RA*c0).
+template <bool UKEY = true>
 __device__ __forceinline__ uint32_t philox_w0(uint32_t ctr, uint32_t k0, uint32_t k1) {
     uint64_t pa = (uint64_t)PHILOX_RA * ctr;
     uint32_t c0 = k0, c1 = 0u, c2 = (uint32_t)(pa >> 32) ^ k1, c3 = (uint32_t)pa;
@@ -81,8 +97,8 @@ __device__ __forceinline__ uint32_t philox_w0(uint32_t ctr, uint32_t k0, uint32_
     for (int r = 1; r < 9; ++r) {
         uint64_t qa = (uint64_t)PHILOX_RA * c0;
         uint64_t qb = (uint64_t)PHILOX_RB * c2;
-        uint32_t n0 = (uint32_t)(qb >> 32) ^ c1 ^ k0;
-        uint32_t n2 = (uint32_t)(qa >> 32) ^ c3 ^ k1;
+        uint32_t n0 = xor3<UKEY>((uint32_t)(qb >> 32), c1, k0);
+        uint32_t n2 = xor3<UKEY>((uint32_t)(qa >> 32), c3, k1);
         c1 = (uint32_t)qb;
         c3 = (uint32_t)qa;
         c0 = n0;
@@ -91,7 +107,7 @@ __device__ __forceinline__ uint32_t philox_w0(uint32_t ctr, uint32_t k0, uint32_
         k1 += PHILOX_KB;
     }
     // last round: only word 0 is needed
-    return (uint32_t)(((uint64_t)PHILOX_RB * c2) >> 32) ^ c1 ^ k0;
+    return xor3<UKEY>((uint32_t)(((uint64_t)PHILOX_RB * c2) >> 32), c1, k0);
 }
 
 // Philox key of Triton's `SEED + k` stream.  A compiled Triton launch types an
@@ -132,15 +148,16 @@ struct Noise {
 
 // 16 noise bits for each of the 8 offsets o0 .. o0+7 (o0 a multiple of 8 when
 // MODE == NOISE_PHILOX8).  `valid` counts the offsets that exist (<= 8).
-template <int MODE>
+// UKEY: the key is the same in every lane of the wave.
+template <int MODE, bool UKEY = true>
 __device__ __forceinline__ void noise8(const Noise &ns, int64_t o0, int valid, uint32_t out[8]) {
     if constexpr (MODE == NOISE_TRITON) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) out[j] = philox_w0((uint32_t)(o0 + j), ns.key.lo, ns.key.hi) & 0xffffu;
+        for (int j = 0; j < 8; ++j) out[j] = philox_w0<UKEY>((uint32_t)(o0 + j), ns.key.lo, ns.key.hi) & 0xffffu;
     } else if constexpr (MODE == NOISE_PHILOX8) {
         uint64_t o = (uint64_t)o0;
         uint32_t c0 = (uint32_t)(o >> 3), c1 = (uint32_t)(o >> 35), c2 = 0u, c3 = 0u;
-        philox10(c0, c1, c2, c3, ns.key.lo, ns.key.hi);
+        philox10<UKEY>(c0, c1, c2, c3, ns.key.lo, ns.key.hi);
         out[0] = c0 & 0xffffu; out[1] = c0 >> 16;
         out[2] = c1 & 0xffffu; out[3] = c1 >> 16;
         out[4] = c2 & 0xffffu; out[5] = c2 >> 16;
@@ -152,14 +169,14 @@ __device__ __forceinline__ void noise8(const Noise &ns, int64_t o0, int valid, u
 }
 
 // Noise for a single offset (scalar fallback paths).
-template <int MODE>
+template <int MODE, bool UKEY = true>
 __device__ __forceinline__ uint32_t noise1(const Noise &ns, int64_t o) {
     if constexpr (MODE == NOISE_TRITON) {
-        return philox_w0((uint32_t)o, ns.key.lo, ns.key.hi) & 0xffffu;
+        return philox_w0<UKEY>((uint32_t)o, ns.key.lo, ns.key.hi) & 0xffffu;
     } else if constexpr (MODE == NOISE_PHILOX8) {
         uint64_t u = (uint64_t)o;
         uint32_t c0 = (uint32_t)(u >> 3), c1 = (uint32_t)(u >> 35), c2 = 0u, c3 = 0u;
-        philox10(c0, c1, c2, c3, ns.key.lo, ns.key.hi);
+        philox10<UKEY>(c0, c1, c2, c3, ns.key.lo, ns.key.hi);
         uint32_t lane = (uint32_t)(u & 7u);
         uint32_t w = (lane < 2) ? c0 : (lane < 4) ? c1 : (lane < 6) ? c2 : c3;
         return (w >> (16u * (lane & 1u))) & 0xffffu;
@@ -215,25 +232,35 @@ constexpr int QT_OCT = 2 * 512;
 constexpr int QT_MAX_BKT = 2048;
 
 // One-level table for the fast kernel (standard codebooks).  A quotient x with
-// bit pattern u, |x| <= 1, falls in bucket key = (u >> 16) & 0x7fff (exponent
-// and 7 mantissa bits); keys up to QF_LO_KEY - 1 (|x| < 2^-23) share entry 0,
-// so entry idx = max(key - (QF_LO_KEY - 1), 0) < QF_N.  Each bucket holds at
-// most one code change (checked when the table is built), so an entry is
-//     bits 0-15: c = 0x10000 - (low 16 bits of the change point), or 0
+// bit pattern u, |x| <= 1, is looked up through w = (u ^ s) >> 16 and the low
+// half (u ^ s) & 0xffff, where s = 0 for x >= 0 and all ones for x < 0: for
+// x >= 0, w is the bucket key (exponent and 7 mantissa bits); for x < 0 both
+// are complemented, so w = 0x7fff - key and the codes (which fall as |x|
+// grows) rise with w and with the low half.  Entry idx = min(max(w - LO1, 0),
+// QF_SCAP) with LO1 = QF_LO_KEY - 1:
+//   signed plane   [0, QF_N)            x >= 0: key - LO1 (0: x < 2^-23)
+//                  [QF_NEG0, QF_SCAP)   x < 0, |x| >= 2^-23: 0x7fff - key - LO1
+//                  QF_SCAP              x < 0, |x| < 2^-23
+//   unsigned plane [0, QF_N)            key - LO1 (0: x < 2^-23)
+// Each bucket holds at most one code change (checked when the table is
+// built), so an entry is
+//     bits 0-15: c = 0x10000 - (low half at the change point), or 0
 //     bits 16-23: code at the bucket's low end
-// and code = ((low16 + entry) >> 16) & 0xff: the carry out of the low half adds
-// the step.  The negative half of the signed map is indexed by |x| with the low
-// 16 bits complemented, so its codes also rise with the lookup variable.
-// Planes: [0] signed x >= 0, [1] signed x < 0, [2] unsigned.
-constexpr uint32_t QF_LO_KEY = 104u << 7;                   // 2^-23
-constexpr int QF_N = (int)((127u << 7) - (QF_LO_KEY - 1u)) + 1;  // 2946
+// and code = ((low half + entry) >> 16) & 0xff: the carry adds the step.
+constexpr uint32_t QF_LO_KEY = 104u << 7;                         // 2^-23
+constexpr uint32_t QF_LO1 = QF_LO_KEY - 1u;
+constexpr int QF_N = (int)((127u << 7) - QF_LO1) + 1;            // 2946 (1.0 is the last key)
+constexpr int QF_NEG0 = (int)(0x7fffu - (127u << 7) - QF_LO1);   // 3200
+constexpr int QF_SCAP = (int)(0x7fffu - QF_LO_KEY - QF_LO1) + 1; // 6145
+constexpr int QF_SIGNED = QF_SCAP + 1;                           // signed plane entries
+constexpr int QF_TOTAL = QF_SIGNED + QF_N;                       // both planes
 
 struct QuantTable {
     uint32_t n_bkt;
     uint32_t pad[3];
     uint32_t oct[QT_OCT];
     uint2 bkt[QT_MAX_BKT];
-    uint32_t flat[3 * QF_N];
+    uint32_t flat[QF_TOTAL];
 };
 
 __host__ __device__ inline uint32_t quantize_lookup(float x, const uint32_t *oct, const uint2 *bkt, bool is_signed) {
@@ -281,6 +308,11 @@ __device__ __forceinline__ float vgpr(float x) {
     asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(x));
     return r;
 }
+__device__ __forceinline__ uint32_t vgpr(uint32_t x) {
+    uint32_t r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
 
 // sqrt(v) correctly rounded, for v == +0 or v in [2^-149, 2^62].  v_sqrt_f32
 // (within 1 ulp) runs on v * 2^64, which is >= 2^-85, where the residuals
@@ -319,19 +351,20 @@ __device__ __forceinline__ float div_rn(float m, float d, float y) {
 }
 
 // Signed code of x = RN(m/d) for the fast kernel (x != -0, |x| <= 1), as the
-// entry sum whose bits 16-23 are the code; `tab` is plane 0 of the flat table.
-__device__ __forceinline__ uint32_t qf_signed(float x, const uint32_t *tab) {
+// entry sum whose bits 16-23 are the code; `tab` is the signed plane, lo1 and
+// scap are VGPR copies of QF_LO1 and QF_SCAP (an SGPR or literal operand of the
+// saturating subtract would take the slow issue rate).
+__device__ __forceinline__ uint32_t qf_signed(float x, const uint32_t *tab, uint32_t lo1, uint32_t scap) {
     const uint32_t u = __float_as_uint(x);
-    const uint32_t sm = (uint32_t)((int32_t)u >> 31);
-    const uint32_t idx = __builtin_elementwise_sub_sat((u >> 16) & 0x7fffu, QF_LO_KEY - 1u) + (sm & (uint32_t)QF_N);
-    return ((u ^ sm) & 0xffffu) + tab[idx];
+    const uint32_t uc = u ^ (uint32_t)((int32_t)u >> 31);
+    const uint32_t idx = min(__builtin_elementwise_sub_sat(uc >> 16, lo1), scap);
+    return (uc & 0xffffu) + tab[idx];
 }
 
-// Unsigned code of x in [0, 1]; `tab` is plane 2 of the flat table.
-__device__ __forceinline__ uint32_t qf_unsigned(float x, const uint32_t *tab) {
+// Unsigned code of x in [0, 1] (x != -0); `tab` is the unsigned plane.
+__device__ __forceinline__ uint32_t qf_unsigned(float x, const uint32_t *tab, uint32_t lo1) {
     const uint32_t u = __float_as_uint(x);
-    const uint32_t idx = __builtin_elementwise_sub_sat((u >> 16) & 0x7fffu, QF_LO_KEY - 1u);
-    return (u & 0xffffu) + tab[idx];
+    return (u & 0xffffu) + tab[__builtin_elementwise_sub_sat(u >> 16, lo1)];
 }
 
 // Bytes 2 of four entry sums, packed into one little-endian code word.

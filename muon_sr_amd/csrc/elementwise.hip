@@ -44,7 +44,7 @@ int check_launch(const char *what) {
 
 // One 8-element group of acc <- SR(acc + grad): offsets o0 .. o0+7 of a tensor
 // of n elements (valid = how many exist).
-template <int MODE, bool GF32, bool ZERO, bool VEC>
+template <int MODE, bool GF32, bool ZERO, bool VEC, bool UKEY = true>
 __device__ __forceinline__ void accum_group(uint16_t *__restrict__ acc, const void *__restrict__ grad,
                                             const Noise &ns, int64_t o0, int valid) {
     float a[8], g[8];
@@ -64,7 +64,7 @@ __device__ __forceinline__ void accum_group(uint16_t *__restrict__ acc, const vo
         unpack8(w, g);
     }
     uint32_t r[8];
-    noise8<MODE>(ns, o0, valid, r);
+    noise8<MODE, UKEY>(ns, o0, valid, r);
     uint32_t out[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -119,14 +119,14 @@ __global__ __launch_bounds__(THREADS) void sr_accum_multi_kernel(AccumMultiArgs 
         uint16_t *acc = a.acc[t];
         const void *grad = a.grad[t];
         switch (a.flags[t]) {
-            case 0: accum_group<MODE, false, false, false>(acc, grad, ns, o0, valid); break;
-            case ACC_ZERO: accum_group<MODE, false, true, false>(acc, grad, ns, o0, valid); break;
-            case ACC_F32: accum_group<MODE, true, false, false>(acc, grad, ns, o0, valid); break;
-            case ACC_F32 | ACC_ZERO: accum_group<MODE, true, true, false>(acc, grad, ns, o0, valid); break;
-            case ACC_VEC: accum_group<MODE, false, false, true>(acc, grad, ns, o0, valid); break;
-            case ACC_VEC | ACC_ZERO: accum_group<MODE, false, true, true>(acc, grad, ns, o0, valid); break;
-            case ACC_VEC | ACC_F32: accum_group<MODE, true, false, true>(acc, grad, ns, o0, valid); break;
-            default: accum_group<MODE, true, true, true>(acc, grad, ns, o0, valid); break;
+            case 0: accum_group<MODE, false, false, false, false>(acc, grad, ns, o0, valid); break;
+            case ACC_ZERO: accum_group<MODE, false, true, false, false>(acc, grad, ns, o0, valid); break;
+            case ACC_F32: accum_group<MODE, true, false, false, false>(acc, grad, ns, o0, valid); break;
+            case ACC_F32 | ACC_ZERO: accum_group<MODE, true, true, false, false>(acc, grad, ns, o0, valid); break;
+            case ACC_VEC: accum_group<MODE, false, false, true, false>(acc, grad, ns, o0, valid); break;
+            case ACC_VEC | ACC_ZERO: accum_group<MODE, false, true, true, false>(acc, grad, ns, o0, valid); break;
+            case ACC_VEC | ACC_F32: accum_group<MODE, true, false, true, false>(acc, grad, ns, o0, valid); break;
+            default: accum_group<MODE, true, true, true, false>(acc, grad, ns, o0, valid); break;
         }
     }
 }

@@ -42,55 +42,23 @@ int check_launch(const char *what) {
 // (c) SR gradient accumulation   (muon_sr/triton_adamw.py:206-229)
 // ---------------------------------------------------------------------------
 
-// One 8-element group of acc <- SR(acc + grad): offsets o0 .. o0+7 of a tensor
-// of n elements (valid = how many exist).
-template <int MODE, bool GF32, bool ZERO, bool VEC, bool UKEY = true>
-__device__ __forceinline__ void accum_group(uint16_t *__restrict__ acc, const void *__restrict__ grad,
-                                            const Noise &ns, int64_t o0, int valid) {
-    float a[8], g[8];
-    if constexpr (ZERO) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] = 0.0f;
-    } else {
-        uint32_t w[4];
-        load_bf16x8<VEC>(acc, o0, valid, w);
-        unpack8(w, a);
-    }
-    if constexpr (GF32) {
-        load_f32x8<VEC>(static_cast<const float *>(grad), o0, valid, g);
-    } else {
-        uint32_t w[4];
-        load_bf16x8<VEC>(static_cast<const uint16_t *>(grad), o0, valid, w);
-        unpack8(w, g);
-    }
-    uint32_t r[8];
-    noise8<MODE, UKEY>(ns, o0, valid, r);
-    uint32_t out[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        out[j] = pack2(sr_bf16(a[2 * j] + g[2 * j], r[2 * j]), sr_bf16(a[2 * j + 1] + g[2 * j + 1], r[2 * j + 1]));
-    store_bf16x8<VEC>(acc, o0, valid, out);
-}
-
-template <int MODE, bool GF32, bool ZERO, bool VEC>
-__global__ __launch_bounds__(THREADS) void sr_accum_kernel(uint16_t *__restrict__ acc, const void *__restrict__ grad,
-                                                          int64_t n, Noise ns) {
-    const int64_t groups = (n + 7) >> 3;
-    for (int64_t t = (int64_t)blockIdx.x * THREADS + threadIdx.x; t < groups; t += (int64_t)gridDim.x * THREADS) {
-        const int64_t o0 = t << 3;
-        accum_group<MODE, GF32, ZERO, VEC>(acc, grad, ns, o0, clamp_valid(n, o0));
-    }
-}
-
-// Many tensors in one launch (the hooks of a backward pass, deferred).  Tensor
-// t owns groups [gstart[t], gstart[t+1]) of the launch's group space; its
-// offsets, and so its noise counters, start at 0, so the result equals one
-// sr_accum_kernel launch per tensor.
+// Many tensors in one launch (the hooks of a backward pass, deferred).  The
+// launch's 8-element groups are cut into tiles of ACC_TILE groups that never
+// cross a tensor: tensor t owns tiles [tstart[t], tstart[t+1]).  A work-group
+// takes tiles in a grid-stride loop, finds the tile's tensor once (a
+// wave-uniform search, so pointers, key and flags are uniform), and each
+// thread loads ACC_U groups (one per ACC_THREADS-wide slice of the tile)
+// before computing them.  A tensor's offsets, and so its noise counters,
+// start at 0: the result equals one sr_accum_kernel launch per tensor.
 constexpr int ACC_MAXT = 80;
+#ifndef MSR_ACC_U
+#define MSR_ACC_U 4
+#endif
+constexpr int ACC_THREADS = 256, ACC_U = MSR_ACC_U, ACC_TILE = ACC_THREADS * ACC_U;
 constexpr uint32_t ACC_ZERO = 1, ACC_F32 = 2, ACC_VEC = 4;
 struct AccumMultiArgs {
     int count;
-    int64_t gstart[ACC_MAXT + 1];
+    int64_t tstart[ACC_MAXT + 1];
     uint16_t *acc[ACC_MAXT];
     const void *grad[ACC_MAXT];
     int64_t n[ACC_MAXT];
@@ -98,35 +66,84 @@ struct AccumMultiArgs {
     uint32_t flags[ACC_MAXT];
 };
 
+// ACC_U groups of one tile of one tensor: loads first, then SR sums and stores.
+template <int MODE, bool GF32, bool ZERO, bool VEC>
+__device__ __forceinline__ void accum_tile(uint16_t *__restrict__ acc, const void *__restrict__ grad, const Noise &ns,
+                                           int64_t n, int64_t g0) {
+    uint32_t wa[ACC_U][4], wg[ACC_U][4];
+    float gf[ACC_U][8];
+    int valid[ACC_U];
+#pragma unroll
+    for (int u = 0; u < ACC_U; ++u) {
+        const int64_t o0 = (g0 + u * ACC_THREADS + threadIdx.x) * 8;
+        valid[u] = clamp_valid(n, o0);
+        if constexpr (!ZERO) load_bf16x8<VEC>(acc, o0, valid[u], wa[u]);
+        if constexpr (GF32) load_f32x8<VEC>(static_cast<const float *>(grad), o0, valid[u], gf[u]);
+        else load_bf16x8<VEC>(static_cast<const uint16_t *>(grad), o0, valid[u], wg[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < ACC_U; ++u) {
+        if (valid[u] == 0) continue;
+        const int64_t o0 = (g0 + u * ACC_THREADS + threadIdx.x) * 8;
+        float a[8], g[8];
+        if constexpr (ZERO) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a[j] = 0.0f;
+        } else {
+            unpack8(wa[u], a);
+        }
+        if constexpr (GF32) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) g[j] = gf[u][j];
+        } else {
+            unpack8(wg[u], g);
+        }
+        uint32_t r[8];
+        noise8<MODE>(ns, o0, valid[u], r);
+        uint32_t out[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            out[j] = pack2(sr_bf16(a[2 * j] + g[2 * j], r[2 * j]), sr_bf16(a[2 * j + 1] + g[2 * j + 1], r[2 * j + 1]));
+        store_bf16x8<VEC>(acc, o0, valid[u], out);
+    }
+}
+
+// One tensor: tiles of ACC_TILE groups, one work-group per tile (grid-stride
+// beyond the launch's grid).
+template <int MODE, bool GF32, bool ZERO, bool VEC>
+__global__ __launch_bounds__(ACC_THREADS) void sr_accum_kernel(uint16_t *__restrict__ acc, const void *__restrict__ grad,
+                                                              int64_t n, Noise ns) {
+    const int64_t tiles = ((n + 7) / 8 + ACC_TILE - 1) / ACC_TILE;
+    for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x)
+        accum_tile<MODE, GF32, ZERO, VEC>(acc, grad, ns, n, tile * ACC_TILE);
+}
+
 template <int MODE>
-__global__ __launch_bounds__(THREADS) void sr_accum_multi_kernel(AccumMultiArgs a) {
-    __shared__ int64_t s_start[ACC_MAXT + 1];
-    for (int i = threadIdx.x; i <= a.count; i += THREADS) s_start[i] = a.gstart[i];
-    __syncthreads();
-    const int64_t total = s_start[a.count];
-    for (int64_t gi = (int64_t)blockIdx.x * THREADS + threadIdx.x; gi < total; gi += (int64_t)gridDim.x * THREADS) {
-        int lo = 0, hi = a.count - 1;   // last t with s_start[t] <= gi
+__global__ __launch_bounds__(ACC_THREADS) void sr_accum_multi_kernel(AccumMultiArgs a) {
+    const int64_t total = a.tstart[a.count];
+    for (int64_t tile = blockIdx.x; tile < total; tile += gridDim.x) {
+        int lo = 0, hi = a.count - 1;   // last t with tstart[t] <= tile (uniform)
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (s_start[mid] <= gi) lo = mid; else hi = mid - 1;
+            if (a.tstart[mid] <= tile) lo = mid; else hi = mid - 1;
         }
         const int t = lo;
-        const int64_t o0 = (gi - s_start[t]) << 3;
-        const int valid = clamp_valid(a.n[t], o0);
+        const int64_t g0 = (tile - a.tstart[t]) * ACC_TILE;
         Noise ns;
         ns.key = a.key[t];
         ns.inject = nullptr;
         uint16_t *acc = a.acc[t];
         const void *grad = a.grad[t];
+        const int64_t n = a.n[t];
         switch (a.flags[t]) {
-            case 0: accum_group<MODE, false, false, false, false>(acc, grad, ns, o0, valid); break;
-            case ACC_ZERO: accum_group<MODE, false, true, false, false>(acc, grad, ns, o0, valid); break;
-            case ACC_F32: accum_group<MODE, true, false, false, false>(acc, grad, ns, o0, valid); break;
-            case ACC_F32 | ACC_ZERO: accum_group<MODE, true, true, false, false>(acc, grad, ns, o0, valid); break;
-            case ACC_VEC: accum_group<MODE, false, false, true, false>(acc, grad, ns, o0, valid); break;
-            case ACC_VEC | ACC_ZERO: accum_group<MODE, false, true, true, false>(acc, grad, ns, o0, valid); break;
-            case ACC_VEC | ACC_F32: accum_group<MODE, true, false, true, false>(acc, grad, ns, o0, valid); break;
-            default: accum_group<MODE, true, true, true, false>(acc, grad, ns, o0, valid); break;
+            case 0: accum_tile<MODE, false, false, false>(acc, grad, ns, n, g0); break;
+            case ACC_ZERO: accum_tile<MODE, false, true, false>(acc, grad, ns, n, g0); break;
+            case ACC_F32: accum_tile<MODE, true, false, false>(acc, grad, ns, n, g0); break;
+            case ACC_F32 | ACC_ZERO: accum_tile<MODE, true, true, false>(acc, grad, ns, n, g0); break;
+            case ACC_VEC: accum_tile<MODE, false, false, true>(acc, grad, ns, n, g0); break;
+            case ACC_VEC | ACC_ZERO: accum_tile<MODE, false, true, true>(acc, grad, ns, n, g0); break;
+            case ACC_VEC | ACC_F32: accum_tile<MODE, true, false, true>(acc, grad, ns, n, g0); break;
+            default: accum_tile<MODE, true, true, true>(acc, grad, ns, n, g0); break;
         }
     }
 }
@@ -320,6 +337,10 @@ static inline Noise make_noise(uint32_t seed, uint32_t k, const uint16_t *inject
         if ((mode) == NOISE_INJECT && !(inject)) { set_error("noise_mode INJECT needs an inject buffer"); return MSR_ERR_ARG; } \
     } while (0)
 
+#ifndef MSR_ACC_GRID_CAP
+#define MSR_ACC_GRID_CAP (1 << 20)   // one work-group per tile: measured best (6.15 TB/s on 7.8 GB)
+#endif
+
 extern "C" {
 
 int msr_version(void) { return 100; }
@@ -333,10 +354,11 @@ int msr_sr_accum(uint16_t *acc, const void *grad, int32_t grad_is_f32, int64_t n
     if (n == 0) return MSR_OK;
     const Noise ns = make_noise(seed, 0, inject, n);
     const bool vec = aligned(acc, 16) && aligned(grad, 16);
-    const unsigned grid = grid_for((n + 7) / 8, THREADS);
+    const int64_t tiles = ((n + 7) / 8 + ACC_TILE - 1) / ACC_TILE;
+    const unsigned grid = (unsigned)(tiles < MSR_ACC_GRID_CAP ? tiles : MSR_ACC_GRID_CAP);
     hipStream_t s = (hipStream_t)stream;
 #define LAUNCH_ACC(GF, Z, V)                                                                                   \
-    MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((sr_accum_kernel<M, GF, Z, V>), dim3(grid), dim3(THREADS), 0, s, acc, grad, n, ns))
+    MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((sr_accum_kernel<M, GF, Z, V>), dim3(grid), dim3(ACC_THREADS), 0, s, acc, grad, n, ns))
     if (grad_is_f32) {
         if (zero_init) { if (vec) { LAUNCH_ACC(true, true, true); } else { LAUNCH_ACC(true, true, false); } }
         else { if (vec) { LAUNCH_ACC(true, false, true); } else { LAUNCH_ACC(true, false, false); } }
@@ -367,28 +389,28 @@ int msr_sr_accum_multi(const msr_accum_item *items, int32_t count, int32_t noise
     while (i < count) {
         AccumMultiArgs a;
         a.count = 0;
-        int64_t g = 0;
+        int64_t g = 0;   // tiles
         for (; i < count && a.count < ACC_MAXT; ++i) {
             const msr_accum_item &it = items[i];
             if (it.n == 0) continue;
             const int t = a.count++;
             const bool f32 = (it.flags & MSR_ACCUM_GRAD_F32) != 0;
-            a.gstart[t] = g;
+            a.tstart[t] = g;
             a.acc[t] = it.acc;
             a.grad[t] = it.grad;
             a.n[t] = it.n;
             a.key[t] = seed_key(it.seed, 0);
             a.flags[t] = ((it.flags & MSR_ACCUM_ZERO_INIT) ? ACC_ZERO : 0u) | (f32 ? ACC_F32 : 0u) |
                          ((aligned(it.acc, 16) && aligned(it.grad, 16)) ? ACC_VEC : 0u);
-            g += (it.n + 7) / 8;
+            g += ((it.n + 7) / 8 + ACC_TILE - 1) / ACC_TILE;
         }
         if (a.count == 0) break;
-        a.gstart[a.count] = g;
-        const unsigned grid = grid_for(g, THREADS);
+        a.tstart[a.count] = g;
+        const unsigned grid = (unsigned)(g < MSR_ACC_GRID_CAP ? g : MSR_ACC_GRID_CAP);
         if (noise_mode == NOISE_TRITON)
-            hipLaunchKernelGGL((sr_accum_multi_kernel<NOISE_TRITON>), dim3(grid), dim3(THREADS), 0, s, a);
+            hipLaunchKernelGGL((sr_accum_multi_kernel<NOISE_TRITON>), dim3(grid), dim3(ACC_THREADS), 0, s, a);
         else
-            hipLaunchKernelGGL((sr_accum_multi_kernel<NOISE_PHILOX8>), dim3(grid), dim3(THREADS), 0, s, a);
+            hipLaunchKernelGGL((sr_accum_multi_kernel<NOISE_PHILOX8>), dim3(grid), dim3(ACC_THREADS), 0, s, a);
         const int rc = check_launch("msr_sr_accum_multi");
         if (rc) return rc;
     }

@@ -134,11 +134,21 @@ def bench_adamw8bit(steps, warmup, n=N8):
     return out
 
 
-def cpu_baseline_adamw8bit(budget_s=12.0):
-    """The oracle's C restatement (one thread) on a bounded sample of config 2."""
+def host_cpu():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline_adamw8bit(budget_s=8.0):
+    """The oracle's C restatement (OpenMP over blocks) on a bounded sample of config 2."""
     import numpy as np
     import oracle as O
-    n = 1 << 22
+    n = 1 << 24
     rng = np.random.default_rng(0)
     p = O.f32_to_bf16_rne((rng.standard_normal(n) * 0.02).astype(np.float32))
     q1, q2 = O.create_dynamic_map(True), O.create_dynamic_map(False)
@@ -157,9 +167,100 @@ def cpu_baseline_adamw8bit(budget_s=12.0):
         t += time.perf_counter() - t0
         steps += 1
     gbps = B8_PER_ELEM * n * steps / t / 1e9
-    return dict(value=round(gbps, 4), unit="GB/s", cores=1, kind="port",
-                sample=f"{steps} steps of the C oracle on 2^22 of the 2^28 elements (same per-element work), "
-                       f"{t:.1f} s on {platform.processor() or platform.machine()}, 1 thread")
+    threads = int(O.lib().orc_num_threads())
+    return dict(value=round(gbps, 4), unit="GB/s", cores=threads, kind="port",
+                sample=f"{steps} steps of the C oracle (restatement of muon_sr/triton_adamw_8bit.py:56-89, "
+                       f"OpenMP over blocks) on 2^24 of the 2^28 elements (same per-element work), {t:.1f} s, "
+                       f"{threads} threads of {host_cpu()}")
+
+
+def cpu_baselines_torch(budget_s=6.0):
+    """The torch restatement of the reference's pure-PyTorch optimizers
+    (oracle/torch_ref.py) timed on the host cores, per config.  Config 1 runs
+    whole; the others run a bounded sample and are scaled to the config:
+    config 2 by elements (2^22 of 2^28), config 3 by elements (one layer's
+    tensors), configs 4 and 5 by Newton-Schulz flops of one 2048x2048 Muon
+    matrix step plus the 8-bit AdamW group by bytes (extrapolated)."""
+    import numpy as np
+    import torch
+    import oracle as O
+    from oracle import torch_ref as T
+    threads = torch.get_num_threads()
+    out = {"cores": threads, "kind": "port", "host": host_cpu()}
+    gen = torch.Generator().manual_seed(1)
+
+    def bf(shape, std):
+        return (torch.randn(shape, generator=gen) * std).to(torch.bfloat16)
+
+    # config 1: MuonSRWithAuxAdam, 4x256^2 Muon + 2x256 + 512x256 AdamW, 10 steps
+    muon = [torch.nn.Parameter(bf((256, 256), 0.02)) for _ in range(4)]
+    adam = [torch.nn.Parameter(bf((256,), 0.02)) for _ in range(2)] + [torch.nn.Parameter(bf((512, 256), 0.02))]
+    opt = T.TorchMuonSRWithAuxAdam([dict(params=muon, use_muon=True, lr=0.02, momentum=0.95, nesterov=True,
+                                         ns_steps=5, weight_decay=0.01),
+                                    dict(params=adam, use_muon=False, lr=3e-4, betas=(0.9, 0.95), eps=1e-10,
+                                         weight_decay=0.01)], batch_ns=True)
+    t0 = time.perf_counter()
+    for _ in range(10):
+        for p in muon + adam:
+            p.grad = bf(p.shape, 1e-3)
+        opt.step()
+    out["cpu_plumbing_ms_per_step"] = round((time.perf_counter() - t0) * 1e3 / 10, 3)
+
+    # config 2 (torch transcription of the 8-bit math, noise from torch.randint)
+    n = 1 << 22
+    q1, q2 = torch.from_numpy(O.create_dynamic_map(True)), torch.from_numpy(O.create_dynamic_map(False))
+    p, g = bf(n, 0.02), bf(n, 1e-3)
+    s1, s2 = torch.full((n,), 127, dtype=torch.uint8), torch.zeros(n, dtype=torch.uint8)
+    a1, a2 = torch.zeros(n // 256), torch.zeros(n // 256)
+    steps, t = 0, 0.0
+    while t < budget_s / 2 or steps < 2:
+        steps += 1
+        t0 = time.perf_counter()
+        noise = torch.randint(0, 1 << 16, (n,), dtype=torch.int32)
+        T.adamw8bit_step(p, g, s1, s2, a1, a2, q1, q2, 256, 3e-4, 0.9, 0.95, 1e-10, 0.01,
+                         1 - 0.9 ** steps, 1 - 0.95 ** steps, noise)
+        t += time.perf_counter() - t0
+    a8_gbps = B8_PER_ELEM * n * steps / t / 1e9
+    out["adamw8bit_torch_gbps"] = round(a8_gbps, 4)
+
+    # config 3: SR accumulation of one layer's 9 tensors (the second micro-batch onwards)
+    layer = llama_small_shapes()[:9]
+    ps = [torch.nn.Parameter(torch.zeros(s, dtype=torch.bfloat16)) for s in layer]
+    grads = [bf(s, 1e-4) for s in layer]
+    for p_, g_ in zip(ps, grads):
+        p_.grad = g_
+        T.accumulate(p_)
+    el = sum(p_.numel() for p_ in ps)
+    t0 = time.perf_counter()
+    for p_, g_ in zip(ps, grads):
+        p_.grad = g_
+        T.accumulate(p_)
+    acc_s = time.perf_counter() - t0
+    total_el = sum(int(np.prod(s)) for s in llama_small_shapes())
+    out["sr_accum_ms_per_microbatch_extrapolated"] = round(acc_s * total_el / el * 1e3, 1)
+    out["sr_accum_gbps"] = round(6.0 * el / acc_s / 1e9, 4)
+    del ps, grads
+
+    # configs 4 and 5: one 2048x2048 Muon matrix step, scaled by NS flops
+    w = torch.nn.Parameter(bf((2048, 2048), 0.02))
+    buf = torch.zeros(2048, 2048, dtype=torch.bfloat16)
+    w.grad = bf((2048, 2048), 1e-3)
+    T.muon_matrix_step(w, w.grad, buf, 0.95, True, 5, 0.02, 0.01)   # warm-up (library set-up)
+    t0 = time.perf_counter()
+    for _ in range(2):
+        T.muon_matrix_step(w, w.grad, buf, 0.95, True, 5, 0.02, 0.01)
+    mt = (time.perf_counter() - t0) / 2
+    rate = ns_flops([(2048, 2048)]) / mt
+    out["muon_2048_matrix_step_s"] = round(mt, 3)
+    out["ns_gflops"] = round(rate / 1e9, 2)
+    out["muon_ns_16L_d2048_ms_extrapolated"] = round(ns_flops(config4_shapes()) / rate * 1e3, 1)
+    adam_bytes = B8_PER_ELEM * 1050939392
+    out["hybrid_llama3_8b_ms_extrapolated"] = round((ns_flops(llama8b_muon_shapes()) / rate
+                                                     + adam_bytes / (a8_gbps * 1e9)) * 1e3, 1)
+    out["sample"] = ("config 1 whole (10 steps); config 2: 2^22 elements; config 3: one layer (9 tensors) scaled "
+                     "by elements; configs 4/5: one 2048x2048 Muon step scaled by NS flops, plus the 8-bit "
+                     "AdamW group at the torch transcription's GB/s (extrapolated)")
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -299,6 +400,11 @@ def config4_shapes():
 # config 5: full hybrid step on Llama-3-8B shapes (Muon + 8-bit AdamW groups)
 # ---------------------------------------------------------------------------
 
+def llama8b_muon_shapes():
+    d, ffn, kv = 4096, 14336, 1024
+    return [(d, d), (kv, d), (kv, d), (d, d), (ffn, d), (ffn, d), (d, ffn)] * 32
+
+
 def bench_full(steps_timed, warmup):
     import torch
     from muon_sr_amd import TritonMuonSRWithAuxAdam
@@ -409,7 +515,13 @@ def main():
         log(f"full hybrid: {r}")
         configs["hybrid_llama3_8b"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline_adamw8bit()
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_adamw8bit()
+        log(f"cpu baseline (C oracle, 8-bit): {cpu}")
+        tb = cpu_baselines_torch()
+        log(f"cpu baseline (torch restatement): {tb}")
+        configs["cpu_torch_restatement"] = tb
     kernel_gbps = r8["kernel_gbps"]
     line = {
         "metric": "8-bit AdamW step GB/s (% HBM peak); Muon NS bf16 TFLOP/s; full step ms",

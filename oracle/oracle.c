@@ -19,6 +19,19 @@
 #include <math.h>
 #include <stdint.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* Threads the block loop of orc_adamw8bit runs on. */
+int32_t orc_num_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
 
 /* ------------------------------------------------------------------------ */
 /* bf16 helpers                                                              */
@@ -231,8 +244,10 @@ void orc_adamw8bit(uint16_t *p, const uint16_t *g,
     const float eps_c = sqrt_bc2 * EPS;                         /* :81 */
     const float decay = 1.0f - LR * WD;                         /* :81 */
     int64_t nblocks = (n + block - 1) / block;
-    float mnew[4096], vnew[4096];
+    /* blocks are independent (the noise is a function of the element offset) */
+#pragma omp parallel for schedule(static)
     for (int64_t b = 0; b < nblocks; ++b) {
+        float mnew[4096], vnew[4096];
         float m_max = 0.0f, v_max = 0.0f;
         for (int32_t i = 0; i < block; ++i) {
             int64_t o = b * (int64_t)block + i;

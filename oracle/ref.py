@@ -63,6 +63,8 @@ def lib():
                                     F, F, F, F, F, F, F, NP, NP, NP]
         L.orc_muon_prepare.argtypes = [P, P, P, P, I64, F, I32, NP]
         L.orc_muon_apply.argtypes = [P, P, I64, F, F, F, NP]
+        L.orc_num_threads.restype = I32
+        L.orc_num_threads.argtypes = []
         _lib = L
     return _lib
 

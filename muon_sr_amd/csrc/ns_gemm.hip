@@ -22,7 +22,8 @@
 // c ^ ((r >> 1) & 7), so the 16 consecutive rows of one 16-lane quarter of a
 // fragment read (256 B) cover all 64 banks once.  Each K substep is one
 // scheduling region in which the MFMAs are interleaved with the next
-// substep's fragment reads and a share of the next slab's loads.
+// substep's fragment reads; the next slab's loads are all issued at the start
+// of the slab.
 #include "common.hpp"
 #include "../../include/muon_sr_amd.h"
 
@@ -124,9 +125,9 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     const uint32_t voQ = (uint32_t)(((int64_t)(n0 + wave * 8 + lrow) * a.ldq + lchunk * 8) * 2);
     const uint32_t rowbP = (uint32_t)(64 * a.ldp * 2), rowbQ = (uint32_t)(64 * a.ldq * 2);
     // Load j (0..7) of a slab: P row block j/2 for even j, Q row block j/2 for odd j.
-    auto dma_part = [&](int stage, int k0, int j0, int j1) {
+    auto dma = [&](int stage, int k0) {
 #pragma unroll
-        for (int j = j0; j < j1; ++j) {
+        for (int j = 0; j < 8; ++j) {
             const int i = j >> 1;
             const int dst = (8 * i + wave) * 1024 + stage * 32768;
             if (j & 1)
@@ -135,7 +136,6 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rP, (lds_void_t *)(g_lds + dst), 16, voP, i * rowbP + k0 * 2, 0, 0);
         }
     };
-    auto dma = [&](int stage, int k0) { dma_part(stage, k0, 0, 8); };
     // Fragment reads: chunk (2 ks + khalf) ^ ((row >> 1) & 7) of row; bits 1-3 of
     // row come from r32 only, so one byte offset per (operand, ks) serves all
     // four 32-row blocks and both stages through the instruction offset.
@@ -173,41 +173,43 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
                 acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], fa[b][mi], acc[mi][ni], 0, 0, 0);
     };
     // Each substep is one scheduling region: its 8 MFMAs interleaved with the
-    // 6 fragment reads of the next substep and a share of the next slab's 8
-    // global->LDS loads (so the load queue drains while the MFMAs run).
-    auto pattern = [&](int nvmem) {
+    // 6 fragment reads of the next substep.
+    auto pattern = [&]() {
 #pragma unroll
         for (int x = 0; x < 6; ++x) {
-            if (x < nvmem) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read (to LDS)
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA (8 per substep)
             if (x == 0 || x == 2) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
     };
     // One K slab from `stage` while slab `knext` streams into the other stage.
-    // The last slab of a tile reloads itself (knext = its own k): the loop
-    // then has a single code path, and the extra stage is never read.
+    // All 8 global->LDS loads of the next slab are issued before the slab's
+    // first MFMA: the operands arrive through L2 with a latency tail (misses to
+    // the Infinity Cache / HBM), and the wait at the end of the slab then has
+    // the whole slab to cover it (measured +3..19% over spreading the loads
+    // across the substeps).  The last slab of a tile reloads itself (knext =
+    // its own k): the loop then has a single code path, and the extra stage is
+    // never read.
     auto slab = [&](int stage, int knext) {
-        dma_part(stage ^ 1, knext, 0, 3);
+        dma(stage ^ 1, knext);
+        __builtin_amdgcn_sched_barrier(0);
         frags(stage, 1, fa[1], fb[1]);
         mm(0);
-        pattern(3);
+        pattern();
         __builtin_amdgcn_sched_barrier(0);
-        dma_part(stage ^ 1, knext, 3, 6);
         frags(stage, 2, fa[0], fb[0]);
         mm(1);
-        pattern(3);
+        pattern();
         __builtin_amdgcn_sched_barrier(0);
-        dma_part(stage ^ 1, knext, 6, 8);
         frags(stage, 3, fa[1], fb[1]);
         mm(0);
-        pattern(2);
+        pattern();
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(0);   // own loads of the next slab landed, own reads of this stage done
         __syncthreads();                 // everyone's
         frags(stage ^ 1, 0, fa[0], fb[0]);
         mm(1);
-        pattern(0);
+        pattern();
         __builtin_amdgcn_sched_barrier(0);
     };
 

@@ -88,6 +88,19 @@ int msr_adamw_bf16_step(uint16_t *p, const uint16_t *g, uint16_t *ema, uint16_t 
                         int32_t noise_mode, const uint16_t *inject, msr_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Gradient centralization of TritonAdamW, on the device.
+ * Replaces the host-issued torch ops of muon_sr/triton_adamw.py:179-187
+ * (g.to(fp32); g -= g.mean(dims 1..) * c; g.to(bf16)).  g, out: bf16
+ * [rows][cols] (rows = dim 0 of a tensor of 2+ dims, else 1); out[r][j] =
+ * bf16_rne(g[r][j] - (sum_j g[r][j] / cols) * alpha) with fp32 sums in a fixed
+ * order.  workspace: msr_centralize_workspace_bytes(rows, cols) bytes of
+ * device memory (the library does not allocate).  out may equal g.
+ * ------------------------------------------------------------------------- */
+int msr_centralize_workspace_bytes(int64_t rows, int64_t cols, size_t *bytes);
+int msr_centralize_bf16(const uint16_t *g, uint16_t *out, int64_t rows, int64_t cols, float alpha,
+                        void *workspace, size_t workspace_bytes, msr_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * (a) 8-bit blockwise AdamW step (bitsandbytes order: decay after the update).
  * Replaces the _adamw_8bit_kernel launch of TritonAdamW8bit.step
  * (muon_sr/triton_adamw_8bit.py:56-99, launched at :198-204).

@@ -7,6 +7,7 @@ kernels are replaced by the gfx950 kernels of libmuon_sr_amd.so.
 from __future__ import annotations
 
 import contextlib
+import ctypes
 import random
 import threading
 
@@ -40,6 +41,26 @@ def _adamw_step(p: torch.Tensor, g: torch.Tensor, ema: torch.Tensor, ema_sq: tor
                                lr, beta1, beta2, eps, weight_decay, bias_correction, bias_correction_sqrt,
                                _seed(step, param_idx), _lib.noise_mode(), None, _lib.stream_of(p))
     _lib.check(rc, "msr_adamw_bf16_step")
+
+
+def centralize(grad: torch.Tensor, strength: float) -> torch.Tensor:
+    """Gradient centralization (muon_sr/triton_adamw.py:179-187) on the device:
+    bf16(g - mean(g over every dim but the first) * strength), fp32 arithmetic.
+    A tensor of fewer than 2 dims is centred on its overall mean, as torch's
+    ``mean(dim=())`` does there.  Returns a new bf16 tensor."""
+    g = grad.contiguous()
+    if g.dtype != torch.bfloat16:
+        g = g.to(torch.bfloat16)
+    rows = g.shape[0] if g.dim() >= 2 else 1
+    cols = g.numel() // rows if rows > 0 else 0
+    out = torch.empty_like(g)
+    L = _lib.lib()
+    nbytes = ctypes.c_size_t()
+    _lib.check(L.msr_centralize_workspace_bytes(rows, cols, ctypes.byref(nbytes)), "msr_centralize_workspace_bytes")
+    ws = torch.empty(max(1, nbytes.value), dtype=torch.uint8, device=g.device)
+    _lib.check(L.msr_centralize_bf16(g.data_ptr(), out.data_ptr(), rows, cols, strength, ws.data_ptr(), ws.numel(),
+                                     _lib.stream_of(g)), "msr_centralize_bf16")
+    return out
 
 
 class TritonAdamW(Optimizer):
@@ -92,12 +113,11 @@ class TritonAdamW(Optimizer):
 
                 state["step"] += 1
 
-                # gradient centralization: mean over all but the first dim, in fp32
-                # (muon_sr/triton_adamw.py:179-187), on the device
+                # gradient centralization (muon_sr/triton_adamw.py:179-187): one fused
+                # device pass instead of the reference's five torch ops
                 if centralization != 0:
-                    grad = grad.to(torch.float32)
-                    grad.sub_(grad.mean(dim=tuple(range(1, grad.dim())), keepdim=True).mul_(centralization))
-                    grad = grad.to(torch.bfloat16)
+                    _lib.require_gpu(p, "TritonAdamW", RuntimeError)
+                    grad = centralize(grad, centralization)
 
                 with torch.no_grad():
                     _adamw_step(p=p.data, g=grad, ema=state["ema"], ema_sq=state["ema_squared"],

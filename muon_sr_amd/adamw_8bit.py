@@ -115,6 +115,57 @@ def init_8bit_state(p, block_size, optim_bits, min_8bit_size, maps):
     return state
 
 
+_QUANT_KEYS = ("state1", "state2", "qmap1", "qmap2", "absmax1", "absmax2")
+
+
+def split_8bit_state(state_dict, param_groups, is_8bit_group):
+    """Take the 8-bit states of a checkpoint out of torch's Optimizer.load_state_dict,
+    which would cast every floating-point state tensor to the parameter's dtype
+    (fp32 block scales and codebooks to bf16).
+
+    ``is_8bit_group(saved_group)`` selects the groups whose states use the
+    TritonAdamW8bit format.  Their states are checked against format_version 2
+    and the group's block size and bits (the errors of
+    muon_sr/triton_adamw_8bit.py:219-236).  Returns (the state dict without those
+    tensors, restore), where ``restore(optimizer.state)`` puts copies back on each
+    parameter's device after torch has loaded the rest."""
+    groups = state_dict["param_groups"]
+    mapping = dict(zip([i for g in groups for i in g["params"]], [p for g in param_groups for p in g["params"]]))
+    restored = {}
+    for group in groups:
+        if not is_8bit_group(group):
+            continue
+        for ident in group["params"]:
+            state = state_dict["state"].get(ident, {})
+            if not state:
+                continue
+            p = mapping[ident]
+            bits = 16 if p.numel() < group["min_8bit_size"] else group["optim_bits"]
+            if (state.get("format_version") != 2 or state.get("block_size") != group["block_size"]
+                    or state.get("optim_bits") != bits):
+                raise ValueError("Incompatible state format/quantization configuration")
+            specs = {key: (p.shape, torch.uint8 if bits == 8 else torch.bfloat16) for key in ("state1", "state2")}
+            if bits == 8:
+                specs.update({key: ((256,), torch.float32) for key in ("qmap1", "qmap2")})
+                specs.update({key: ((_cdiv(p.numel(), group["block_size"]),), torch.float32)
+                              for key in ("absmax1", "absmax2")})
+            restored[ident] = {}
+            for key, (shape, dtype) in specs.items():
+                value = state[key]
+                if value.dtype != dtype or tuple(value.shape) != tuple(shape):
+                    raise ValueError(f"Invalid checkpoint state: {key}")
+                restored[ident][key] = value.to(device=p.device, dtype=dtype).clone(
+                    memory_format=torch.contiguous_format)
+    stripped = dict(state_dict, state={i: ({k: v for k, v in st.items() if k not in _QUANT_KEYS}
+                                           if i in restored else st)
+                                       for i, st in state_dict["state"].items()})
+
+    def restore(opt_state):
+        for ident, values in restored.items():
+            opt_state[mapping[ident]].update(values)
+    return stripped, restore
+
+
 def step_seed(step: int, param_index: int) -> int:
     """muon_sr/triton_adamw_8bit.py:197."""
     return (step * 2654435761 ^ param_index * 1234567891) & 0xFFFFFFFF
@@ -212,35 +263,8 @@ class TritonAdamW8bit(Optimizer):
         if len(groups) != len(self.param_groups) or any(
                 len(a["params"]) != len(b["params"]) for a, b in zip(groups, self.param_groups)):
             raise ValueError("Checkpoint parameter groups do not match optimizer")
-        mapping = dict(zip([i for g in groups for i in g["params"]],
-                           [p for g in self.param_groups for p in g["params"]]))
-        restored = {}
-        keys = {"state1", "state2", "qmap1", "qmap2", "absmax1", "absmax2"}
         for group in groups:
             self._validate_group(group)
-            for ident in group["params"]:
-                state = state_dict["state"].get(ident, {})
-                if not state:
-                    continue
-                p = mapping[ident]
-                bits = 16 if p.numel() < group["min_8bit_size"] else group["optim_bits"]
-                if (state.get("format_version") != 2 or state.get("block_size") != group["block_size"]
-                        or state.get("optim_bits") != bits):
-                    raise ValueError("Incompatible state format/quantization configuration")
-                specs = {key: (p.shape, torch.uint8 if bits == 8 else torch.bfloat16) for key in ("state1", "state2")}
-                if bits == 8:
-                    specs.update({key: ((256,), torch.float32) for key in ("qmap1", "qmap2")})
-                    specs.update({key: ((_cdiv(p.numel(), group["block_size"]),), torch.float32)
-                                  for key in ("absmax1", "absmax2")})
-                restored[ident] = {}
-                for key, (shape, dtype) in specs.items():
-                    value = state[key]
-                    if value.dtype != dtype or tuple(value.shape) != tuple(shape):
-                        raise ValueError(f"Invalid checkpoint state: {key}")
-                    restored[ident][key] = value.to(device=p.device, dtype=dtype).clone(
-                        memory_format=torch.contiguous_format)
-        stripped = dict(state_dict, state={i: {k: v for k, v in state.items() if k not in keys}
-                                           for i, state in state_dict["state"].items()})
+        stripped, restore = split_8bit_state(state_dict, self.param_groups, lambda group: True)
         super().load_state_dict(stripped)
-        for ident, values in restored.items():
-            self.state[mapping[ident]].update(values)
+        restore(self.state)

@@ -25,7 +25,7 @@ from torch.optim import Optimizer
 
 from . import _lib
 from .adamw import _adamw_step
-from .adamw_8bit import adamw8bit_launch, init_8bit_state, TritonAdamW8bit
+from .adamw_8bit import adamw8bit_launch, init_8bit_state, split_8bit_state, TritonAdamW8bit
 
 NS_COEFFS = (3.4445, -4.7750, 2.0315)
 
@@ -395,6 +395,18 @@ class TritonMuonSRWithAuxAdam(_StackedBufsMixin, Optimizer):
                                 step=state["step"], param_idx=group_offset + i)
 
         return loss
+
+    def load_state_dict(self, state_dict):
+        """As torch's, except that the states of ``optim_bits=8`` AdamW groups keep
+        their uint8 codes and fp32 block scales and codebooks (TritonAdamW8bit's
+        checkpoint format, version 2)."""
+        if len(state_dict["param_groups"]) != len(self.param_groups):
+            raise ValueError("loaded state dict has a different number of parameter groups")
+        stripped, restore = split_8bit_state(
+            state_dict, self.param_groups,
+            lambda group: not group.get("use_muon", False) and group.get("optim_bits", 16) == 8)
+        super().load_state_dict(stripped)
+        restore(self.state)
 
     def _step_8bit(self, p, group, state, lr, beta1, beta2, eps, weight_decay, param_index):
         """8-bit AdamW group step: the TritonAdamW8bit update with seed index group_offset + i."""

@@ -307,6 +307,117 @@ def test_muon_batch_state_dict_round_trip(L):
         assert ob.state[q]["step"] == 3
 
 
+def _resume_matches(make, grads, steps_before=2):
+    """Run `steps_before` steps, save a deep copy of state_dict(), load it into a
+    fresh optimizer over copied parameters, then take one more step with both:
+    parameters and every state entry must be identical (values and dtypes)."""
+    pa, oa = make()
+    for s in range(steps_before):
+        for p, g in zip(pa, grads[s]):
+            p.grad = None if g is None else g.to(DEV)
+        oa.step()
+    sd = copy.deepcopy(oa.state_dict())
+    pb, ob = make()
+    for p, q in zip(pb, pa):
+        p.data.copy_(q.data)
+    ob.load_state_dict(sd)
+    for opt, ps in ((oa, pa), (ob, pb)):
+        for p, g in zip(ps, grads[steps_before]):
+            p.grad = None if g is None else g.to(DEV)
+        opt.step()
+    for p, q in zip(pa, pb):
+        assert torch.equal(p.data, q.data)
+        assert set(oa.state[p]) == set(ob.state[q])
+        for k in oa.state[p]:
+            a, b = oa.state[p][k], ob.state[q][k]
+            if torch.is_tensor(a):
+                assert a.dtype == b.dtype and a.device == b.device and torch.equal(a, b), k
+            else:
+                assert a == b, k
+    return oa, ob, pa, pb
+
+
+def test_hybrid_state_dict_round_trip_with_8bit_group(L):
+    """TritonMuonSRWithAuxAdam with a batch_ns Muon group, a bf16 AdamW group and
+    an optim_bits=8 AdamW group: resume is exact and the 8-bit states keep their
+    uint8 codes and fp32 block scales and codebooks (torch's default load would
+    cast the fp32 tensors to the bf16 parameter dtype)."""
+    from muon_sr_amd import TritonMuonSRWithAuxAdam
+    torch.manual_seed(7)
+    shapes = [(64, 96), (96, 64), (64, 96), (300,), (96, 128), (100,)]
+    base = [(torch.randn(s) * 0.02).to(torch.bfloat16) for s in shapes]
+    grads = [[(torch.randn(s) * 1e-3).to(torch.bfloat16) for s in shapes] for _ in range(3)]
+    grads[1][1] = None   # a missing Muon gradient at step 2
+
+    def make():
+        ps = [torch.nn.Parameter(t.clone().to(DEV)) for t in base]
+        opt = TritonMuonSRWithAuxAdam([
+            dict(params=ps[:3], use_muon=True, lr=0.02, weight_decay=0.01),
+            dict(params=ps[3:4], use_muon=False, lr=3e-4, weight_decay=0.01),
+            dict(params=ps[4:], use_muon=False, lr=3e-4, weight_decay=0.01, optim_bits=8),
+        ], batch_ns=True)
+        return ps, opt
+
+    oa, ob, pa, pb = _resume_matches(make, grads)
+    st8 = ob.state[pb[4]]
+    assert st8["state1"].dtype == torch.uint8 and st8["absmax1"].dtype == torch.float32
+    assert st8["qmap1"].dtype == torch.float32 and st8["format_version"] == 2
+    assert ob.state[pb[5]]["state1"].dtype == torch.bfloat16      # numel < min_8bit_size: 16-bit moments
+    assert ob.state[pb[3]]["ema"].dtype == torch.bfloat16
+    assert ob._global_step == oa._global_step == 3
+
+
+@pytest.mark.parametrize("cls_name", ["TritonAdamW", "TritonMuonSR_per_param"])
+def test_state_dict_round_trip_other_classes(L, cls_name):
+    import muon_sr_amd
+    torch.manual_seed(8)
+    shapes = [(64, 96), (40,)] if cls_name == "TritonAdamW" else [(64, 96), (96, 64)]
+    base = [(torch.randn(s) * 0.02).to(torch.bfloat16) for s in shapes]
+    grads = [[(torch.randn(s) * 1e-3).to(torch.bfloat16) for s in shapes] for _ in range(3)]
+
+    def make():
+        ps = [torch.nn.Parameter(t.clone().to(DEV)) for t in base]
+        if cls_name == "TritonAdamW":
+            return ps, muon_sr_amd.TritonAdamW(ps, lr=1e-3, weight_decay=0.01, centralization=0.2)
+        return ps, muon_sr_amd.TritonMuonSR(ps, lr=0.02, weight_decay=0.01, batch_ns=False)
+
+    _resume_matches(make, grads)
+
+
+def test_adamw8bit_checkpoint_validation(L):
+    """The reference's load-time errors (muon_sr/triton_adamw_8bit.py:212-236)."""
+    from muon_sr_amd import TritonAdamW8bit
+    torch.manual_seed(9)
+    ps = [torch.nn.Parameter((torch.randn(64, 96) * 0.02).to(torch.bfloat16).to(DEV))]
+    opt = TritonAdamW8bit(ps, lr=1e-3)
+    ps[0].grad = (torch.randn(64, 96) * 1e-3).to(torch.bfloat16).to(DEV)
+    opt.step()
+    good = opt.state_dict()
+
+    def fresh():
+        return TritonAdamW8bit([torch.nn.Parameter(ps[0].detach().clone())], lr=1e-3)
+
+    bad = copy.deepcopy(good)
+    bad["state"][0]["format_version"] = 1
+    with pytest.raises(ValueError, match="Incompatible state format"):
+        fresh().load_state_dict(bad)
+    bad = copy.deepcopy(good)
+    bad["state"][0]["absmax1"] = bad["state"][0]["absmax1"].to(torch.bfloat16)
+    with pytest.raises(ValueError, match="Invalid checkpoint state: absmax1"):
+        fresh().load_state_dict(bad)
+    bad = copy.deepcopy(good)
+    bad["param_groups"][0]["block_size"] = 128
+    with pytest.raises(ValueError, match="Incompatible state format"):
+        fresh().load_state_dict(bad)
+    two = TritonAdamW8bit([dict(params=[torch.nn.Parameter(ps[0].detach().clone())]),
+                           dict(params=[torch.nn.Parameter(ps[0].detach().clone())])])
+    with pytest.raises(ValueError, match="groups do not match"):
+        two.load_state_dict(good)
+    o = fresh()
+    o.load_state_dict(good)
+    assert o.state[o.param_groups[0]["params"][0]]["absmax1"].dtype == torch.float32
+
+
 # ---------------------------------------------------------------------------
 # TritonSRAccumulator: hooks through a real backward, against the oracle
 # ---------------------------------------------------------------------------

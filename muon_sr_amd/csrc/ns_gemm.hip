@@ -24,6 +24,8 @@
 // scheduling region in which the MFMAs are interleaved with the next
 // substep's fragment reads; the next slab's loads are all issued at the start
 // of the slab.
+#include <algorithm>
+
 #include "common.hpp"
 #include "../../include/muon_sr_amd.h"
 
@@ -49,15 +51,30 @@ struct GemmArgs {
     int symmetric;     // M == N, P == Q: only tiles ti <= tj, mirrored into D
     int d_vec;         // D rows allow 16-byte stores (set by launch_gemm)
     int dt_vec;        // DT rows allow 16-byte stores (set by launch_gemm)
+    int tiles;         // tiles per matrix
+    int per_xcd;       // 1-D grid over a multiple of 8 matrices, whole matrices per XCD
 };
 
-// Work-group -> tile.  Consecutive work-group ids are dispatched round-robin
-// over the 8 XCDs (each with its own L2), so the id is first mapped to
-// (xcd, slot) and every XCD receives a contiguous range of the tile order;
-// inside a range, tiles go row-group by row-group (GROUP_M rows, then along
-// the columns), so the work-groups resident on one XCD share operand slabs.
+// Work-group -> (matrix, tile).  Consecutive work-group ids are dispatched
+// round-robin over the 8 XCDs (each with its own L2), so tiles that share
+// operand row blocks should run on one XCD at the same time:
+//  * small matrices (at most PER_XCD_TILES tiles) in launches over a multiple
+//    of 8 matrices (1-D grid): whole matrices per XCD.  Work-group L runs on
+//    XCD L % 8 and takes slot L / 8 of that XCD's list, the tiles of matrices
+//    xcd, xcd + 8, xcd + 16, ... in tile order;
+//  * otherwise (2-D grid, blockIdx.y = matrix) each XCD takes a contiguous
+//    range of one matrix's tile order, so the XCDs work on the same matrices
+//    at once and share its operand rows through the Infinity Cache (measured
+//    8 % faster on the 4096 x 14336 products than whole matrices per XCD,
+//    which suits matrices whose tiles/8 would be too few to share operands).
+// Tile order: non-symmetric products go GROUP_M tile-rows at a time, column
+// by column inside a group; symmetric ones walk the upper triangle in bands of
+// GROUP_M tile-rows, column by column, taking the band's rows ti <= tj of each
+// column.  Either way a run of consecutive tiles covers a compact block of
+// tile-rows and tile-columns.
 constexpr int NXCD = 8;
 constexpr int GROUP_M = 4;
+constexpr int PER_XCD_TILES = 64;
 
 __device__ __forceinline__ int xcd_remap(int w, int total) {
     const int per = total / NXCD;          // full rounds
@@ -68,16 +85,27 @@ __device__ __forceinline__ int xcd_remap(int w, int total) {
 __device__ __forceinline__ void decode_tile(const GemmArgs &a, int t, int &ti, int &tj) {
     if (a.symmetric) {
         const int T = a.tiles_m;
-        int row = 0;
-        int start = 0;
-        while (start + (T - row) <= t) {
-            start += T - row;
-            ++row;
+        int g0 = 0, start = 0, rows = min(GROUP_M, T);
+        for (;;) {
+            const int cnt = rows * (rows + 1) / 2 + rows * (T - g0 - rows);
+            if (t < start + cnt) break;
+            start += cnt;
+            g0 += rows;
+            rows = min(GROUP_M, T - g0);
         }
-        ti = row;
-        tj = row + (t - start);
+        int r = t - start;
+        const int tri = rows * (rows + 1) / 2;
+        if (r < tri) {           // columns g0 .. g0+rows-1 hold 1 .. rows tiles
+            int c = 0;
+            while ((c + 1) * (c + 2) / 2 <= r) ++c;
+            tj = g0 + c;
+            ti = g0 + (r - c * (c + 1) / 2);
+        } else {                 // full columns of `rows` tiles
+            r -= tri;
+            tj = g0 + rows + r / rows;
+            ti = g0 + r % rows;
+        }
     } else {
-        // grouped order: GROUP_M tile-rows at a time, column-major inside a group
         const int per_group = GROUP_M * a.tiles_n;
         const int g = t / per_group;
         const int first = g * GROUP_M;
@@ -100,8 +128,15 @@ __shared__ __attribute__((aligned(1024))) char g_lds[256 * SPITCH * 2];
 template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     int ti, tj;
-    decode_tile(a, xcd_remap(blockIdx.x, gridDim.x), ti, tj);
-    const int64_t bz = blockIdx.y;
+    int64_t bz;
+    if (a.per_xcd) {
+        const int slot = (int)(blockIdx.x / NXCD);
+        bz = (int64_t)(blockIdx.x % NXCD) + (int64_t)NXCD * (slot / a.tiles);
+        decode_tile(a, slot % a.tiles, ti, tj);
+    } else {
+        decode_tile(a, xcd_remap(blockIdx.x, gridDim.x), ti, tj);
+        bz = blockIdx.y;
+    }
     const int m0 = ti * BM, n0 = tj * BN;
 
     const int tid = threadIdx.x;
@@ -510,15 +545,9 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
     a.d_vec = a.D && aligned(a.D, 16) && (a.ldd % 8) == 0 && (a.sD % 8) == 0;
     a.dt_vec = a.DT && aligned(a.DT, 16) && (a.lddt % 8) == 0 && (a.sDT % 8) == 0;
     const int64_t tiles = a.symmetric ? (int64_t)a.tiles_m * (a.tiles_m + 1) / 2 : (int64_t)a.tiles_m * a.tiles_n;
-    for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
-        const int64_t nb = (batch - b0) < 65535 ? (batch - b0) : 65535;
-        GemmArgs ab = a;
-        ab.P += b0 * a.sP;
-        ab.Q += b0 * a.sQ;
-        if (ab.C) ab.C += b0 * a.sC;
-        if (ab.D) ab.D += b0 * a.sD;
-        if (ab.DT) ab.DT += b0 * a.sDT;
-        const dim3 grid((unsigned)tiles, (unsigned)nb), block(GEMM_THREADS);
+    a.tiles = (int)tiles;
+    auto launch = [&](const GemmArgs &ab, dim3 grid) {
+        const dim3 block(GEMM_THREADS);
         const bool c = ab.C != nullptr, d = ab.D != nullptr, dt = ab.DT != nullptr;
         if (ab.symmetric && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false>), grid, block, 0, s, ab);
         else if (ab.symmetric && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false>), grid, block, 0, s, ab);
@@ -526,8 +555,35 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
         else if (!ab.symmetric && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false>), grid, block, 0, s, ab);
         else if (!ab.symmetric && c && !d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, false, true>), grid, block, 0, s, ab);
         else if (!ab.symmetric && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false>), grid, block, 0, s, ab);
-        else { set_error("gemm: unsupported epilogue combination"); return MSR_ERR_ARG; }
-        int rc = check_launch("gemm_nt_kernel");
+        else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
+        return check_launch("gemm_nt_kernel");
+    };
+    auto offset = [&](int64_t b0) {
+        GemmArgs ab = a;
+        ab.P += b0 * a.sP;
+        ab.Q += b0 * a.sQ;
+        if (ab.C) ab.C += b0 * a.sC;
+        if (ab.D) ab.D += b0 * a.sD;
+        if (ab.DT) ab.DT += b0 * a.sDT;
+        return ab;
+    };
+    // whole matrices per XCD for the largest multiple of 8 matrices (1-D grids
+    // of at most 2^31 - 1 work-groups), the remainder per matrix (2-D grids)
+    const int64_t per_launch8 = ((int64_t(1) << 31) - 1) / (tiles * NXCD) * NXCD;
+    int64_t b0 = 0;
+    while (tiles <= PER_XCD_TILES && per_launch8 > 0 && batch - b0 >= NXCD) {
+        const int64_t nb = std::min((batch - b0) / NXCD * NXCD, per_launch8);
+        GemmArgs ab = offset(b0);
+        ab.per_xcd = 1;
+        const int rc = launch(ab, dim3((unsigned)(tiles * nb)));
+        if (rc) return rc;
+        b0 += nb;
+    }
+    for (; b0 < batch; b0 += 65535) {
+        const int64_t nb = (batch - b0) < 65535 ? (batch - b0) : 65535;
+        GemmArgs ab = offset(b0);
+        ab.per_xcd = 0;
+        const int rc = launch(ab, dim3((unsigned)tiles, (unsigned)nb));
         if (rc) return rc;
     }
     return MSR_OK;

@@ -1,6 +1,6 @@
 """Benchmark of the muon_sr optimizer-step hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--configs adamw8bit,sr_accum,ns,full] [--noise philox8|triton]
+    python bench.py [--steps K] [--warmup W] [--configs adamw8bit,sr_accum,ns,centralize,full] [--noise philox8|triton]
 
 Prints ONE JSON line.  ``value`` is the headline workload (BASELINE.json
 configs[1]): one fused 8-bit blockwise AdamW step on a flat bf16 parameter of
@@ -443,6 +443,45 @@ def bench_full(steps_timed, warmup):
     return out
 
 
+def bench_centralize(reps=10):
+    """TritonAdamW's gradient centralization on a Llama-3-8B embedding-sized bf16
+    gradient (128256 x 4096): this library's fused kernels against the
+    reference's torch op sequence (muon_sr/triton_adamw.py:180-186) on the same
+    GPU.  Algorithmic traffic 6 B/element (read g twice, write g')."""
+    import torch
+    from muon_sr_amd.adamw import centralize
+    dev = "cuda:0"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    g = (torch.randn(128256, 4096, device=dev, generator=gen) * 1e-3).to(torch.bfloat16)
+
+    def ref_ops():
+        x = g.to(torch.float32)
+        x.sub_(x.mean(dim=tuple(range(1, x.dim())), keepdim=True).mul_(0.5))
+        return x.to(torch.bfloat16)
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        sync()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        sync()
+        return s.elapsed_time(e) / reps
+
+    ms = timed(lambda: centralize(g, 0.5))
+    ref_ms = timed(ref_ops)
+    n = g.numel()
+    out = dict(elements=n, ms=ms, gbps=6.0 * n / (ms * 1e6), reference_torch_ops_ms=ref_ms,
+               speedup_vs_reference_ops=ref_ms / ms)
+    del g
+    torch.cuda.empty_cache()
+    return out
+
+
 def copy_calibration():
     """A plain device copy of known size (2^28 fp32: 1 GiB read + 1 GiB written per
     launch).  Profiled with FETCH_SIZE / WRITE_SIZE, it gives the factor that turns
@@ -478,7 +517,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="adamw8bit,sr_accum,ns,full")
+    ap.add_argument("--configs", default="adamw8bit,sr_accum,ns,centralize,full")
     ap.add_argument("--noise", default="philox8", choices=["philox8", "triton"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -510,6 +549,10 @@ def main():
         r = bench_muon(config4_shapes(), steps_timed=3, warmup=1, label="config4")
         log(f"muon config4: {r}")
         configs["muon_ns_16L_d2048"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+    if "centralize" in todo:
+        r = bench_centralize()
+        log(f"centralize: {r}")
+        configs["centralize_embed_128256x4096"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
     if "full" in todo:
         r = bench_full(steps_timed=2, warmup=1)
         log(f"full hybrid: {r}")

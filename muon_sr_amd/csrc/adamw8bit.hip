@@ -544,6 +544,7 @@ __global__ __launch_bounds__(THREADS) void quant_table_check_kernel(const QuantT
 //   kind 1: rcp_rn(d) vs 1/d                  (d in [2^-60, 2))
 //   kind 2: div_rn(m, d, rcp_rn(d)) vs m/d    (d in [2^-60, 2), 16 hashed m per d with
 //           2^-63 d <= |m| <= d; for |m| < 2^-100 only the sign and zero-ness must agree)
+//   kind 3: rne_bf16x2 (hardware conversion) vs rne_bf16 (any u; both halves)
 __device__ __forceinline__ uint32_t mix32(uint32_t x) {
     x ^= x >> 16; x *= 0x7feb352du; x ^= x >> 15; x *= 0x846ca68bu; x ^= x >> 16;
     return x;
@@ -560,6 +561,9 @@ __global__ __launch_bounds__(THREADS) void fastmath_check_kernel(int kind, uint3
             bad += __float_as_uint(sqrt_rn(x)) != __float_as_uint(sqrtf(x));
         } else if (kind == 1) {
             bad += __float_as_uint(rcp_rn(x)) != __float_as_uint(1.0f / x);
+        } else if (kind == 3) {
+            const float x2 = __uint_as_float(~u);
+            bad += rne_bf16x2(x, x2) != pack2(rne_bf16(x), rne_bf16(x2));
         } else {
             const float y = rcp_rn(x);
             for (uint32_t k = 0; k < 16; ++k) {
@@ -827,7 +831,9 @@ int msr_quant_table_check(const void *qtable, const float *qmap_signed, const fl
 int msr_fastmath_check(int32_t kind, uint32_t bits_lo, uint32_t bits_hi, uint32_t *counts, int32_t n_counts,
                        msr_stream_t stream) {
     const uint32_t SQRT_HI = 0x5e800000u, RCP_LO = 0x21800000u, RCP_HI = 0x3fffffffu;   // 2^62, 2^-60, 2 - ulp
-    const bool range_ok = kind == 0 ? bits_hi <= SQRT_HI : (kind == 1 || kind == 2) && bits_lo >= RCP_LO && bits_hi <= RCP_HI;
+    const bool range_ok = kind == 0 ? bits_hi <= SQRT_HI
+                        : kind == 3 ? true
+                                    : (kind == 1 || kind == 2) && bits_lo >= RCP_LO && bits_hi <= RCP_HI;
     if (!counts || n_counts <= 0 || bits_hi < bits_lo || !range_ok) {
         set_error("msr_fastmath_check: bad arguments (kind %d, range %08x..%08x)", (int)kind, bits_lo, bits_hi);
         return MSR_ERR_ARG;

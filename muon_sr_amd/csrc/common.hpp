@@ -46,6 +46,16 @@ __device__ __forceinline__ uint32_t rne_bf16(float x) {
 
 __device__ __forceinline__ uint32_t pack2(uint32_t lo16, uint32_t hi16) { return (lo16 & 0xffffu) | (hi16 << 16); }
 
+// Two fp32 values rounded to bf16 (nearest even) and packed, lo in bits 0-15:
+// one v_cvt_pk_bf16_f32.  Equal to pack2(rne_bf16(lo), rne_bf16(hi)) for every
+// fp32 bit pattern, NaNs included (msr_fastmath_check kind 3 tests all 2^32).
+typedef __bf16 msr_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float msr_f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t rne_bf16x2(float lo, float hi) {
+    const msr_f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, msr_bf16x2_t));
+}
+
 // ---------------------------------------------------------------------------
 // Philox4x32-10 (Salmon et al., SC'11), the generator Triton's tl.randint uses.
 // ---------------------------------------------------------------------------

@@ -25,6 +25,7 @@
 // substep's fragment reads; the next slab's loads are all issued at the start
 // of the slab.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "../../include/muon_sr_amd.h"
@@ -279,28 +280,40 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         }
         __syncthreads();
     }
+    // alpha * acc (+ beta * C), rounded to bf16 by the hardware conversion; the
+    // multiply is skipped for alpha == 1 (x * 1 == x for every non-NaN x)
+    auto stage_out = [&](auto scaled) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
+        for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
+            for (int ni = 0; ni < 2; ++ni) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int ml = wm * 128 + mi * 32 + r32;
-                const int nl = wn * 64 + ni * 32 + 8 * r + 4 * khalf;
-                uint2 *sp = reinterpret_cast<uint2 *>(stg + ml * SPITCH + nl);
-                float v0 = a.alpha * acc[mi][ni][4 * r], v1 = a.alpha * acc[mi][ni][4 * r + 1];
-                float v2 = a.alpha * acc[mi][ni][4 * r + 2], v3 = a.alpha * acc[mi][ni][4 * r + 3];
-                if constexpr (HAS_C) {
-                    const uint2 cw = *sp;
-                    v0 = v0 + a.beta * bf16_lo(cw.x);
-                    v1 = v1 + a.beta * bf16_hi(cw.x);
-                    v2 = v2 + a.beta * bf16_lo(cw.y);
-                    v3 = v3 + a.beta * bf16_hi(cw.y);
+                for (int r = 0; r < 4; ++r) {
+                    const int ml = wm * 128 + mi * 32 + r32;
+                    const int nl = wn * 64 + ni * 32 + 8 * r + 4 * khalf;
+                    uint2 *sp = reinterpret_cast<uint2 *>(stg + ml * SPITCH + nl);
+                    float v0 = acc[mi][ni][4 * r], v1 = acc[mi][ni][4 * r + 1];
+                    float v2 = acc[mi][ni][4 * r + 2], v3 = acc[mi][ni][4 * r + 3];
+                    if constexpr (decltype(scaled)::value) {
+                        v0 = a.alpha * v0;
+                        v1 = a.alpha * v1;
+                        v2 = a.alpha * v2;
+                        v3 = a.alpha * v3;
+                    }
+                    if constexpr (HAS_C) {
+                        const uint2 cw = *sp;
+                        v0 = v0 + a.beta * bf16_lo(cw.x);
+                        v1 = v1 + a.beta * bf16_hi(cw.x);
+                        v2 = v2 + a.beta * bf16_lo(cw.y);
+                        v3 = v3 + a.beta * bf16_hi(cw.y);
+                    }
+                    *sp = make_uint2(rne_bf16x2(v0, v1), rne_bf16x2(v2, v3));
                 }
-                *sp = make_uint2(pack2(rne_bf16(v0), rne_bf16(v1)), pack2(rne_bf16(v2), rne_bf16(v3)));
             }
         }
-    }
+    };
+    if (a.alpha == 1.0f) stage_out(std::false_type{});
+    else stage_out(std::true_type{});
     __syncthreads();
     if constexpr (OUT_D) {
         uint16_t *Db = a.D + bz * a.sD;
@@ -445,9 +458,7 @@ __global__ __launch_bounds__(256) void normalize_vec_kernel(const uint16_t *in, 
             uint32_t o[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const uint32_t lo = rne_bf16(__uint_as_float(u[k] << 16) / d);
-                const uint32_t hi = rne_bf16(__uint_as_float(u[k] & 0xffff0000u) / d);
-                o[k] = lo | (hi << 16);
+                o[k] = rne_bf16x2(__uint_as_float(u[k] << 16) / d, __uint_as_float(u[k] & 0xffff0000u) / d);
             }
             w = make_uint4(o[0], o[1], o[2], o[3]);
         }

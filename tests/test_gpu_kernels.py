@@ -342,10 +342,13 @@ RCP_LO, RCP_HI = 0x21800000, 0x3FFFFFFF  # bits(2^-60), bits(2) - 1
     (2, 0x3F800000, RCP_HI),               # quotient: every d in [1, 2), 16 m each
     (2, RCP_LO, RCP_LO + (1 << 23) - 1),   # ... every d in [2^-60, 2^-59)
     (2, 0x30000000, 0x307FFFFF),           # ... every d in [2^-31, 2^-30)
+    (3, 0, 0xFFFFFFFF),                    # hardware bf16 rounding: every fp32 bit pattern
 ])
 def test_fastmath_exhaustive(L, kind, lo, hi):
     """The fast 8-bit kernel's sqrt, reciprocal and quotient equal the IEEE operations
-    on their whole input ranges (the quotient on a hashed sample of numerators)."""
+    on their whole input ranges (the quotient on a hashed sample of numerators), and
+    the hardware fp32->bf16 conversion of the GEMM epilogues equals the bit-level
+    round-to-nearest-even on every fp32 bit pattern."""
     nblk = 4096
     counts = torch.zeros(nblk, dtype=torch.int32, device=DEV)
     check(L, L.msr_fastmath_check(kind, lo, hi, counts.data_ptr(), nblk, stream()), "fastmath check")

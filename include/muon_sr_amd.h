@@ -43,6 +43,7 @@ typedef struct ihipStream_t *msr_stream_t; /* == hipStream_t */
 #define MSR_ERR_ALIGN 1002
 #define MSR_ERR_LAUNCH 1003
 #define MSR_ERR_WORKSPACE 1004
+#define MSR_ERR_OVERLAP 1005   /* operands overlap without being the same buffer (a data race) */
 
 /* Library version (major*10000 + minor*100 + patch) and error text. */
 int msr_version(void);

@@ -658,6 +658,17 @@ int msr_adamw8bit_step(uint16_t *p, const uint16_t *g, void *state1, void *state
     if (quantized && (!absmax1 || !absmax2 || !qmap1 || !qmap2)) { set_error("msr_adamw8bit_step: quantized state needs absmax and qmaps"); return MSR_ERR_ARG; }
     MSR_CHECK_MODE(noise_mode, inject);
     if (n == 0) return MSR_OK;
+    {
+        const size_t sb = (quantized ? 1 : 2) * (size_t)n, ab = 4 * (size_t)((n + block - 1) / block);
+        const void *ops[6] = {p, g, state1, state2, quantized ? absmax1 : nullptr, quantized ? absmax2 : nullptr};
+        const size_t len[6] = {2 * (size_t)n, 2 * (size_t)n, sb, sb, ab, ab};
+        for (int i = 0; i < 6; ++i)
+            for (int j = i + 1; j < 6; ++j)
+                if (partial_overlap(ops[i], len[i], ops[j], len[j])) {
+                    set_error("msr_adamw8bit_step: operands %d and %d overlap", i, j);
+                    return MSR_ERR_OVERLAP;
+                }
+    }
     Adam8Args a;
     a.p = p; a.g = g; a.s1 = state1; a.s2 = state2; a.absmax1 = absmax1; a.absmax2 = absmax2;
     a.qmap1 = qmap1; a.qmap2 = qmap2; a.n = n; a.qb0 = 0;

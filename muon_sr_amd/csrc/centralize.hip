@@ -88,7 +88,7 @@ __global__ __launch_bounds__(CENT_THREADS) void centralize_kernel(CentArgs a) {
             const uint32_t u[4] = {w.x, w.y, w.z, w.w};
             uint32_t o[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) o[k] = pack2(rne_bf16(bf16_lo(u[k]) - m), rne_bf16(bf16_hi(u[k]) - m));
+            for (int k = 0; k < 4; ++k) o[k] = rne_bf16x2(bf16_lo(u[k]) - m, bf16_hi(u[k]) - m);
             *reinterpret_cast<uint4 *>(y + i) = make_uint4(o[0], o[1], o[2], o[3]);
         }
     } else {
@@ -125,6 +125,15 @@ int msr_centralize_bf16(const uint16_t *g, uint16_t *out, int64_t rows, int64_t 
     if (!workspace || workspace_bytes < need) {
         set_error("msr_centralize_bf16: workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);
         return MSR_ERR_WORKSPACE;
+    }
+    const size_t gb = 2 * (size_t)rows * (size_t)cols;
+    const bool ws_hit = [&] {
+        const uintptr_t w = (uintptr_t)workspace, g0 = (uintptr_t)g, o0 = (uintptr_t)out;
+        return (w < g0 + gb && g0 < w + need) || (w < o0 + gb && o0 < w + need);
+    }();
+    if (partial_overlap(g, gb, out, gb) || ws_hit) {
+        set_error("msr_centralize_bf16: g, out and the workspace overlap (only out == g is allowed)");
+        return MSR_ERR_OVERLAP;
     }
     CentArgs a;
     a.g = g; a.out = out; a.rows = rows; a.cols = cols; a.chunks = chunks;

@@ -410,6 +410,19 @@ __device__ __forceinline__ void halfwave_max2(float &a, float &b) {
 
 inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// Host-side race check: the byte ranges [a, a + na) and [b, b + nb) overlap
+// without being the same buffer.  Identical ranges are in-place use, which the
+// element-wise kernels allow (each element is read before it is written by the
+// same thread); any other overlap would let one element's write race another's
+// read.
+inline bool partial_overlap(const void *a, size_t na, const void *b, size_t nb) {
+    if (!a || !b || na == 0 || nb == 0) return false;
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    if (x == y && na == nb) return false;
+    return x < y + nb && y < x + na;
+}
+
+
 // Grid size for a grid-stride loop over `work` items with `threads` per block.
 inline unsigned grid_for(int64_t work, int threads, int64_t cap = 256 * 32) {
     int64_t b = (work + threads - 1) / threads;

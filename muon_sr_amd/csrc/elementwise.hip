@@ -351,6 +351,10 @@ int msr_sr_accum(uint16_t *acc, const void *grad, int32_t grad_is_f32, int64_t n
                  int32_t noise_mode, const uint16_t *inject, msr_stream_t stream) {
     if (n < 0 || (n > 0 && (!acc || !grad))) { set_error("msr_sr_accum: bad arguments"); return MSR_ERR_ARG; }
     MSR_CHECK_MODE(noise_mode, inject);
+    if (partial_overlap(acc, 2 * (size_t)n, grad, (grad_is_f32 ? 4 : 2) * (size_t)n)) {
+        set_error("msr_sr_accum: acc and grad overlap");
+        return MSR_ERR_OVERLAP;
+    }
     if (n == 0) return MSR_OK;
     const Noise ns = make_noise(seed, 0, inject, n);
     const bool vec = aligned(acc, 16) && aligned(grad, 16);
@@ -393,8 +397,23 @@ int msr_sr_accum_multi(const msr_accum_item *items, int32_t count, int32_t noise
         for (; i < count && a.count < ACC_MAXT; ++i) {
             const msr_accum_item &it = items[i];
             if (it.n == 0) continue;
-            const int t = a.count++;
             const bool f32 = (it.flags & MSR_ACCUM_GRAD_F32) != 0;
+            // items of one launch run concurrently: an accumulator may share memory
+            // with no other operand of the launch (its own gradient aside, in place)
+            const size_t ab = 2 * (size_t)it.n, gb = (f32 ? 4 : 2) * (size_t)it.n;
+            bool race = partial_overlap(it.acc, ab, it.grad, gb);
+            for (int u = 0; u < a.count && !race; ++u) {
+                const size_t ub = 2 * (size_t)a.n[u];
+                const size_t ug = ((a.flags[u] & ACC_F32) ? 4 : 2) * (size_t)a.n[u];
+                race = (uintptr_t)it.acc < (uintptr_t)a.acc[u] + ub && (uintptr_t)a.acc[u] < (uintptr_t)it.acc + ab;
+                race = race || ((uintptr_t)it.acc < (uintptr_t)a.grad[u] + ug && (uintptr_t)a.grad[u] < (uintptr_t)it.acc + ab);
+                race = race || ((uintptr_t)a.acc[u] < (uintptr_t)it.grad + gb && (uintptr_t)it.grad < (uintptr_t)a.acc[u] + ub);
+            }
+            if (race) {
+                set_error("msr_sr_accum_multi: item %d overlaps another operand of its launch", (int)i);
+                return MSR_ERR_OVERLAP;
+            }
+            const int t = a.count++;
             a.tstart[t] = g;
             a.acc[t] = it.acc;
             a.grad[t] = it.grad;
@@ -423,6 +442,15 @@ int msr_adamw_bf16_step(uint16_t *p, const uint16_t *g, uint16_t *ema, uint16_t 
                         msr_stream_t stream) {
     if (n < 0 || (n > 0 && (!p || !g || !ema || !ema_sq))) { set_error("msr_adamw_bf16_step: bad arguments"); return MSR_ERR_ARG; }
     MSR_CHECK_MODE(noise_mode, inject);
+    {
+        const void *ops[4] = {p, g, ema, ema_sq};
+        for (int i = 0; i < 4; ++i)
+            for (int j = i + 1; j < 4; ++j)
+                if (partial_overlap(ops[i], 2 * (size_t)n, ops[j], 2 * (size_t)n)) {
+                    set_error("msr_adamw_bf16_step: operands %d and %d overlap", i, j);
+                    return MSR_ERR_OVERLAP;
+                }
+    }
     if (n == 0) return MSR_OK;
     AdamWArgs a;
     a.p = p; a.g = g; a.ema = ema; a.ema_sq = ema_sq; a.n = n;
@@ -448,6 +476,13 @@ int msr_muon_prepare(const uint16_t *const *grads, uint16_t *buf, uint16_t *out,
     }
     MSR_CHECK_MODE(noise_mode, inject);
     if (numel_each == 0 || count == 0) return MSR_OK;
+    {
+        const size_t sb = 2 * (size_t)numel_each * (size_t)count, eb = 2 * (size_t)numel_each;
+        bool race = (uintptr_t)buf < (uintptr_t)out + sb && (uintptr_t)out < (uintptr_t)buf + sb;
+        for (int32_t i = 0; i < count && !race; ++i)
+            race = grads[i] && (partial_overlap(grads[i], eb, buf, sb) || partial_overlap(grads[i], eb, out, sb));
+        if (race) { set_error("msr_muon_prepare: gradients, momentum stack and update stack must not overlap"); return MSR_ERR_OVERLAP; }
+    }
     hipStream_t s = (hipStream_t)stream;
     const bool rows_aligned = (numel_each % 8) == 0 && aligned(buf, 16) && aligned(out, 16);
     for (int32_t c0 = 0; c0 < count; c0 += MAX_TABLE) {
@@ -486,6 +521,18 @@ int msr_muon_apply(uint16_t *const *params, const uint16_t *upd, int64_t numel_e
     }
     MSR_CHECK_MODE(noise_mode, inject);
     if (numel_each == 0 || count == 0) return MSR_OK;
+    {
+        // the parameters of one launch are written concurrently: they may share
+        // memory neither with each other nor with the update stack
+        const size_t eb = 2 * (size_t)numel_each, ub = eb * (size_t)count;
+        for (int32_t i = 0; i < count; ++i) {
+            if (!params[i]) { set_error("msr_muon_apply: null parameter pointer %d", (int)i); return MSR_ERR_ARG; }
+            bool race = (uintptr_t)params[i] < (uintptr_t)upd + ub && (uintptr_t)upd < (uintptr_t)params[i] + eb;
+            for (int32_t j = 0; j < i && !race; ++j)
+                race = (uintptr_t)params[i] < (uintptr_t)params[j] + eb && (uintptr_t)params[j] < (uintptr_t)params[i] + eb;
+            if (race) { set_error("msr_muon_apply: parameter %d overlaps another parameter or the update stack", (int)i); return MSR_ERR_OVERLAP; }
+        }
+    }
     hipStream_t s = (hipStream_t)stream;
     const bool rows_aligned = (numel_each % 8) == 0 && aligned(upd, 16);
     for (int32_t c0 = 0; c0 < count; c0 += MAX_TABLE) {

@@ -648,6 +648,16 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
         return MSR_ERR_WORKSPACE;
     }
     if (L.mp > (1 << 30) || L.np > (1 << 30)) { set_error("msr_newton_schulz: matrix too large"); return MSR_ERR_ARG; }
+    {
+        // the input is consumed before the output is written, so in and out may
+        // share memory; neither may share the workspace
+        const uintptr_t w = (uintptr_t)workspace, i0 = (uintptr_t)in, o0 = (uintptr_t)out;
+        const size_t io = 2 * (size_t)batch * (size_t)rows * (size_t)cols;
+        if ((w < i0 + io && i0 < w + L.total) || (w < o0 + io && o0 < w + L.total)) {
+            set_error("msr_newton_schulz: the workspace overlaps the input or the output");
+            return MSR_ERR_OVERLAP;
+        }
+    }
     hipStream_t s = (hipStream_t)stream;
     char *ws = static_cast<char *>(workspace);
     uint16_t *X[2] = {(uint16_t *)(ws + L.off_x[0]), (uint16_t *)(ws + L.off_x[1])};

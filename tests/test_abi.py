@@ -67,3 +67,33 @@ def test_argument_validation_without_gpu(lib):
     assert lib.msr_gemm_nt(1, 64, 0, 1, 64, 0, None, 0, 0, 1, 256, 0, 255, 256, 64, 1, 1.0, 0.0, None) == 1001
     # K must be a multiple of 128 (the K loop runs two 64-wide slabs per iteration)
     assert lib.msr_gemm_nt(1, 64, 0, 1, 64, 0, None, 0, 0, 1, 256, 0, 256, 256, 64, 1, 1.0, 0.0, None) == 1001
+
+
+def test_overlapping_operands_are_rejected(lib):
+    """Operands that share memory without being the same buffer would race; every
+    entry point refuses them (MSR_ERR_OVERLAP) before any HIP call."""
+    from muon_sr_amd import _lib
+    OVERLAP = 1005
+    A, B, C, D = 0x100000, 0x200000, 0x300000, 0x400000
+    # acc and grad: half a buffer apart
+    assert lib.msr_sr_accum(A, A + 64, 0, 100, 0, 0, 1, None, None) == OVERLAP
+    # an fp32 gradient in place of its bf16 accumulator: same start, different extent
+    assert lib.msr_sr_accum(A, A, 1, 100, 0, 0, 1, None, None) == OVERLAP
+    items = (_lib.AccumItem * 2)(_lib.AccumItem(A, B, 100, 0, 0), _lib.AccumItem(A + 100, C, 100, 0, 0))
+    assert lib.msr_sr_accum_multi(items, 2, 1, None) == OVERLAP
+    assert lib.msr_adamw_bf16_step(A, B, C, C + 2, 64, 1e-3, 0.9, 0.99, 1e-8, 0.0, 0.1, 0.1, 0, 1, None, None) == OVERLAP
+    # 8-bit: the code buffer runs into the block scales
+    assert lib.msr_adamw8bit_step(A, B, C, D, C + 32, D + 4096, 1, 1, None, 1024, 256, 1, 1e-3, 0.9, 0.99, 1e-8,
+                                  0.0, 0.1, 0.01, 0, 1, None, None) == OVERLAP
+    grads = _lib.ptr_array([A, A + 128])
+    assert lib.msr_muon_prepare(grads, B, B + 64, 64, 2, 0.95, 1, 0, 1, None, None) == OVERLAP
+    params = _lib.ptr_array([A, A + 64])
+    seeds = _lib.ptr_array([1, 2], ctypes.c_uint32)
+    assert lib.msr_muon_apply(params, B, 64, 2, 0.02, 0.0, 1.0, seeds, 1, None, None) == OVERLAP
+    nb = ctypes.c_size_t()
+    assert lib.msr_centralize_workspace_bytes(4, 100, ctypes.byref(nb)) == 0
+    assert lib.msr_centralize_bf16(A, A + 2, 4, 100, 0.5, C, nb.value, None) == OVERLAP
+    assert lib.msr_centralize_bf16(A, B, 4, 100, 0.5, A + 8, nb.value, None) == OVERLAP
+    assert lib.msr_ns_workspace_bytes(2, 256, 256, ctypes.byref(nb)) == 0
+    assert lib.msr_newton_schulz(A, B, 2, 256, 256, 5, 3.4445, -4.775, 2.0315, A + 1024, nb.value, None) == OVERLAP
+    assert b"overlap" in lib.msr_last_error()

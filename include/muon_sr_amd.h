@@ -201,7 +201,8 @@ int msr_quant_table_check(const void *qtable, const float *qmap_signed, const fl
 
 /* Device self-check of the fast kernel's correctly rounded building blocks
  * against the IEEE operations, over the float bit patterns u in
- * [bits_lo, bits_hi]: kind 0 sqrt (u <= bits(2^62)); kind 1 reciprocal and
+ * [bits_lo, bits_hi]: kind 0 sqrt, alone and fused into the update's
+ * sqrt(v) + eps (u <= bits(2^62)); kind 1 reciprocal and
  * kind 2 quotient m/d for 16 hashed m per d (bits(2^-60) <= u < bits(2));
  * kind 3 the hardware fp32->bf16 round-to-nearest-even of the GEMM epilogues
  * against the bit-level rounding (any u).

@@ -407,7 +407,7 @@ __global__ __launch_bounds__(F8_THREADS) MSR_F8_ATTR void adamw8bit_fast_kernel(
             noise8<MODE>(a.ns_p, o0, 8, rp);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float den = sqrt_rn(v[j]) + eps_c;                      // :74
+                const float den = __builtin_fmaf(sqrt_rn_x2p32(v[j]), 0x1p-32f, eps_c);   // :74 sqrt(v) + eps
                 const float upd = (p[j] - (step_c * m[j]) / den) * decay;
                 w[j] = __float_as_uint(upd) + rp[j];                          // :75-78 (SR)
             }
@@ -540,7 +540,8 @@ __global__ __launch_bounds__(THREADS) void quant_table_check_kernel(const QuantT
 
 // Counts, per work-group, mismatches between a fast building block and the IEEE
 // operation over the float bit patterns u in [lo, hi]:
-//   kind 0: sqrt_rn(x) vs sqrtf(x)            (x in [0, 2^62])
+//   kind 0: sqrt_rn(x) vs sqrtf(x), and fma(sqrt_rn_x2p32(x), 2^-32, e) vs sqrtf(x) + e
+//           for a hashed e in [0, 2)            (x in [0, 2^62])
 //   kind 1: rcp_rn(d) vs 1/d                  (d in [2^-60, 2))
 //   kind 2: div_rn(m, d, rcp_rn(d)) vs m/d    (d in [2^-60, 2), 16 hashed m per d with
 //           2^-63 d <= |m| <= d; for |m| < 2^-100 only the sign and zero-ness must agree)
@@ -558,7 +559,9 @@ __global__ __launch_bounds__(THREADS) void fastmath_check_kernel(int kind, uint3
         const uint32_t u = lo + (uint32_t)i;
         const float x = __uint_as_float(u);
         if (kind == 0) {
-            bad += __float_as_uint(sqrt_rn(x)) != __float_as_uint(sqrtf(x));
+            const float r = sqrtf(x), e = __uint_as_float(mix32(u) & 0x3fffffffu);
+            bad += __float_as_uint(sqrt_rn(x)) != __float_as_uint(r);
+            bad += __float_as_uint(__builtin_fmaf(sqrt_rn_x2p32(x), 0x1p-32f, e)) != __float_as_uint(r + e);
         } else if (kind == 1) {
             bad += __float_as_uint(rcp_rn(x)) != __float_as_uint(1.0f / x);
         } else if (kind == 3) {

@@ -329,17 +329,19 @@ __device__ __forceinline__ uint32_t vgpr(uint32_t x) {
 // fma(s -+ 1ulp, s, -v) are exact; the root moves down a step when
 // v <= (s - 1ulp) * s and up a step when v > (s + 1ulp) * s, as in the IEEE
 // sequence, read off the residuals' sign bits.  At v = 0, s - 1ulp saturates to
-// 0 and both residuals are +0.  The result is unscaled by the exact 2^-32.
-__device__ __forceinline__ float sqrt_rn(float v) {
+// 0 and both residuals are +0.  sqrt_rn_x2p32 returns the root of v * 2^64,
+// i.e. 2^32 * sqrt(v), whose unscaling by 2^-32 is exact (the root of v * 2^64
+// is 0 or >= 2^-42.5): fma(sqrt_rn_x2p32(v), 2^-32, e) == sqrt_rn(v) + e.
+__device__ __forceinline__ float sqrt_rn_x2p32(float v) {
     const float vs = v * 0x1p64f;
     const float s = __builtin_amdgcn_sqrtf(vs);
     const uint32_t sb = __float_as_uint(s);
     const uint32_t sdn = __builtin_elementwise_sub_sat(sb, 1u);
     const float rdn = __builtin_fmaf(__uint_as_float(sdn), s, -vs);
     const float rup = __builtin_fmaf(__uint_as_float(sb + 1u), s, -vs);
-    const uint32_t r = sdn + (__float_as_uint(rdn) >> 31) + (__float_as_uint(rup) >> 31);
-    return __uint_as_float(r) * 0x1p-32f;
+    return __uint_as_float(sdn + (__float_as_uint(rdn) >> 31) + (__float_as_uint(rup) >> 31));
 }
+__device__ __forceinline__ float sqrt_rn(float v) { return sqrt_rn_x2p32(v) * 0x1p-32f; }
 
 // RN(1/d) for d in [2^-60, 2): v_rcp_f32 and one Newton step.
 __device__ __forceinline__ float rcp_rn(float d) {

@@ -219,6 +219,13 @@ int msr_gemm_nt(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t 
                 int64_t strideD, int64_t M, int64_t N, int64_t K, int64_t batch, float alpha, float beta,
                 msr_stream_t stream);
 
+/* The same with a K-major Q:  D[b] = alpha * P[b] Q[b] + beta * C[b],  Q: [K][N] (row stride ldq).
+ * This is the kernel of Newton-Schulz's X' = B X + a X.  Test support: no counterpart in the reference. */
+int msr_gemm_nn(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q, int64_t ldq,
+                int64_t strideQ, const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D, int64_t ldd,
+                int64_t strideD, int64_t M, int64_t N, int64_t K, int64_t batch, float alpha, float beta,
+                msr_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,13 +1,15 @@
 // Batched Newton-Schulz orthogonalisation on gfx950 bf16 MFMA.
 //
-// Every product of the iteration is written as an "NT" GEMM,
-//     D[m][n] = alpha * sum_k P[m][k] * Q[n][k] + beta * C[m][n],
-// with both operands K-contiguous, so each MFMA operand fragment is one
-// 16-byte LDS read.  The iterate X (m x n, m <= n) is kept in two layouts,
-// X (row-major m x n) and XT (row-major n x m):
-//     A  = X X^T          P = X,  Q = X      (symmetric: upper tiles + mirror)
-//     B  = c A A + b A    P = A,  Q = A      (A symmetric, so A A = A A^T)
-//     X' = B X + a X      P = B,  Q = XT     (writes X' and X'^T)
+// Every product of the iteration is one GEMM kernel,
+//     D[m][n] = alpha * sum_k P[m][k] * Q[n][k] + beta * C[m][n]      ("NT")
+//     D[m][n] = alpha * sum_k P[m][k] * Q[k][n] + beta * C[m][n]      ("NN", QK)
+// with P K-contiguous, so each MFMA P fragment is one 16-byte LDS read; a
+// K-contiguous Q fragment is one 16-byte read too, a K-major one (QK) two
+// 8-byte transposing reads (ds_read_b64_tr_b16).  The iterate X (m x n,
+// m <= n) is kept row-major:
+//     A  = X X^T          NT, P = X,  Q = X      (symmetric: upper tiles + mirror)
+//     B  = c A A + b A    NT, P = A,  Q = A      (A symmetric, so A A = A A^T)
+//     X' = B X + a X      NN, P = B,  Q = X
 // Workspace matrices are zero-padded to multiples of 256; zero padding is
 // preserved exactly by all three products, so only the final store is
 // bounds-checked.
@@ -34,6 +36,8 @@ namespace msr {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int GEMM_THREADS = 512;
@@ -54,6 +58,7 @@ struct GemmArgs {
     int dt_vec;        // DT rows allow 16-byte stores (set by launch_gemm)
     int tiles;         // tiles per matrix
     int per_xcd;       // 1-D grid over a multiple of 8 matrices, whole matrices per XCD
+    int qk;            // Q is K-major: Q[k][n] at Q + k * ldq + n (the NN product)
 };
 
 // Work-group -> (matrix, tile).  Consecutive work-group ids are dispatched
@@ -119,14 +124,30 @@ __device__ __forceinline__ void decode_tile(const GemmArgs &a, int t, int &ti, i
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// LDS: four 32 KiB slabs, P stage 0/1 at 0/32K, Q stage 0/1 at 64K/96K; after
-// the K loop the same memory stages the 256 x 256 bf16 output tile with a row
-// pitch of SPITCH elements (528 B: 16-byte aligned rows; the 8-byte writes of
-// 32 consecutive rows hit each bank at most twice).
+// LDS: four variables of 33 KiB, one per slab: P stage 0, P stage 1, Q stage
+// 0, Q stage 1 (32 KiB used each).  Separate variables tell the compiler that
+// the fragment reads of one stage do not alias the direct-to-LDS loads into
+// the other stage (it would otherwise wait for those loads before the reads).
+// After the K loop the same memory stages the 256 x 256 bf16 output tile with
+// a row pitch of SPITCH elements (528 B: 16-byte aligned rows; the 8-byte
+// writes of 32 consecutive rows hit each bank at most twice), rows 64 v ..
+// 64 v + 63 in variable v.
 constexpr int SPITCH = 264;
-__shared__ __attribute__((aligned(1024))) char g_lds[256 * SPITCH * 2];
+constexpr int SLAB_BYTES = 64 * SPITCH * 2;
+__shared__ __attribute__((aligned(1024))) char lds_p0[SLAB_BYTES];
+__shared__ __attribute__((aligned(1024))) char lds_p1[SLAB_BYTES];
+__shared__ __attribute__((aligned(1024))) char lds_q0[SLAB_BYTES];
+__shared__ __attribute__((aligned(1024))) char lds_q1[SLAB_BYTES];
 
-template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT>
+__device__ __forceinline__ char *lds_p(int stage) { return stage ? lds_p1 : lds_p0; }
+__device__ __forceinline__ char *lds_q(int stage) { return stage ? lds_q1 : lds_q0; }
+__device__ __forceinline__ uint16_t *stg_row(int r) {
+    const int v = r >> 6, o = (r & 63) * (SPITCH * 2);
+    char *b = v == 0 ? lds_p0 : v == 1 ? lds_p1 : v == 2 ? lds_q0 : lds_q1;
+    return reinterpret_cast<uint16_t *>(b + o);
+}
+
+template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, bool QK>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     int ti, tj;
     int64_t bz;
@@ -158,18 +179,33 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     const __amdgpu_buffer_rsrc_t rP = __builtin_amdgcn_make_buffer_rsrc((void *)(a.P + bz * a.sP), (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rQ = __builtin_amdgcn_make_buffer_rsrc((void *)(a.Q + bz * a.sQ), (short)0, 0x7fffffff, 0x00020000);
     const uint32_t voP = (uint32_t)(((int64_t)(m0 + wave * 8 + lrow) * a.ldp + lchunk * 8) * 2);
-    const uint32_t voQ = (uint32_t)(((int64_t)(n0 + wave * 8 + lrow) * a.ldq + lchunk * 8) * 2);
-    const uint32_t rowbP = (uint32_t)(64 * a.ldp * 2), rowbQ = (uint32_t)(64 * a.ldq * 2);
+    const uint32_t rowbP = (uint32_t)(64 * a.ldp * 2);
+    // A K-major Q slab is 64 rows (k) of the tile's 256 columns, 512 B per row;
+    // chunk c of row k is stored at c ^ 4 (k & 3), so the four rows of one
+    // transposing read fall in different banks.  Load i of wave w fills LDS block
+    // 8 i + w = rows 16 i + 2 w + lane / 32, physical chunk lane % 32.
+    uint32_t voQ, rowbQ, kbQ;
+    if constexpr (QK) {
+        const int qr = 2 * wave + (lane >> 5);
+        const int qc = (lane & 31) ^ (4 * (qr & 3));
+        voQ = (uint32_t)(((int64_t)qr * a.ldq + n0 + 8 * qc) * 2);
+        rowbQ = (uint32_t)(16 * a.ldq * 2);
+        kbQ = (uint32_t)(a.ldq * 2);
+    } else {
+        voQ = (uint32_t)(((int64_t)(n0 + wave * 8 + lrow) * a.ldq + lchunk * 8) * 2);
+        rowbQ = (uint32_t)(64 * a.ldq * 2);
+        kbQ = 2;
+    }
     // Load j (0..7) of a slab: P row block j/2 for even j, Q row block j/2 for odd j.
     auto dma = [&](int stage, int k0) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int i = j >> 1;
-            const int dst = (8 * i + wave) * 1024 + stage * 32768;
+            const int dst = (8 * i + wave) * 1024;
             if (j & 1)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_void_t *)(g_lds + 65536 + dst), 16, voQ, i * rowbQ + k0 * 2, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_void_t *)(lds_q(stage) + dst), 16, voQ, i * rowbQ + k0 * kbQ, 0, 0);
             else
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rP, (lds_void_t *)(g_lds + dst), 16, voP, i * rowbP + k0 * 2, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rP, (lds_void_t *)(lds_p(stage) + dst), 16, voP, i * rowbP + k0 * 2, 0, 0);
         }
     };
     // Fragment reads: chunk (2 ks + khalf) ^ ((row >> 1) & 7) of row; bits 1-3 of
@@ -181,15 +217,37 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     for (int ks = 0; ks < 4; ++ks) {
         const int ch = (2 * ks) ^ khalf ^ sw;
         offP[ks] = (uint32_t)((wm * 128 + r32) * 128 + ch * 16);
-        offQ[ks] = (uint32_t)(65536 + (wn * 64 + r32) * 128 + ch * 16);
+        offQ[ks] = (uint32_t)((wn * 64 + r32) * 128 + ch * 16);
+    }
+    // K-major Q: the fragment of lane l (column l % 32, k = 8 (l / 32) + 0..7 of
+    // the substep) is two transposing reads of 4 k each.  In a read, lane i of a
+    // 16-lane group returns element i % 4 of the 8-byte rows fetched by lanes
+    // i / 4 + 4 j (j = 0..3), so lane i fetches row k = i / 4 (+4 for the second
+    // read), columns 4 (i % 4) .. +3 of its group's 16.
+    uint32_t offQK[2];
+    {
+        const int G = lane >> 4, i = lane & 15;
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+            const int c = wn * 8 + ni * 4 + 2 * (G & 1) + ((i >> 1) & 1);
+            offQK[ni] = (uint32_t)((8 * (G >> 1) + (i >> 2)) * 512 + (c ^ (4 * (i >> 2))) * 16 + (i & 1) * 8);
+        }
     }
     auto frags = [&](int stage, int ks, bf16x8_t (&pa)[4], bf16x8_t (&qb)[2]) {
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi)
-            pa[mi] = *reinterpret_cast<const bf16x8_t *>(g_lds + offP[ks] + stage * 32768 + mi * 4096);
+            pa[mi] = *reinterpret_cast<const bf16x8_t *>(lds_p(stage) + offP[ks] + mi * 4096);
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-            qb[ni] = *reinterpret_cast<const bf16x8_t *>(g_lds + offQ[ks] + stage * 32768 + ni * 4096);
+        for (int ni = 0; ni < 2; ++ni) {
+            if constexpr (QK) {
+                const char *q = lds_q(stage) + offQK[ni] + ks * 8192;
+                const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(q));
+                const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(q + 2048));
+                qb[ni] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            } else {
+                qb[ni] = *reinterpret_cast<const bf16x8_t *>(lds_q(stage) + offQ[ks] + ni * 4096);
+            }
+        }
     };
 
     f32x16_t acc[4][2];
@@ -209,13 +267,13 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
                 acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], fa[b][mi], acc[mi][ni], 0, 0, 0);
     };
     // Each substep is one scheduling region: its 8 MFMAs interleaved with the
-    // 6 fragment reads of the next substep.
+    // fragment reads of the next substep (6, or 8 with a K-major Q).
     auto pattern = [&]() {
 #pragma unroll
-        for (int x = 0; x < 6; ++x) {
+        for (int x = 0; x < (QK ? 8 : 6); ++x) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA (8 per substep)
-            if (x == 0 || x == 2) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (!QK && (x == 0 || x == 2)) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
     };
     // One K slab from `stage` while slab `knext` streams into the other stage.
@@ -266,7 +324,6 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     // that way, and the transposed copies (DT, or the mirror of an off-diagonal
     // symmetric tile) are gathered column-wise from LDS.
     // Lane l holds D[m = l % 32][n = 8r + 4(l / 32) + q] of each 32x32 MFMA tile.
-    uint16_t *stg = reinterpret_cast<uint16_t *>(g_lds);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // every wave is done with the operand slabs
     const int ec = tid & 31, er = tid >> 5;   // 16-byte chunk in a row, first row (16 rows per pass)
@@ -275,7 +332,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
 #pragma unroll 4
         for (int it = 0; it < 16; ++it) {
             const int r = er + 16 * it;
-            *reinterpret_cast<uint4 *>(stg + r * SPITCH + 8 * ec) =
+            *reinterpret_cast<uint4 *>(stg_row(r) + 8 * ec) =
                 *reinterpret_cast<const uint4 *>(Cb + (int64_t)r * a.ldc);
         }
         __syncthreads();
@@ -291,7 +348,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
                 for (int r = 0; r < 4; ++r) {
                     const int ml = wm * 128 + mi * 32 + r32;
                     const int nl = wn * 64 + ni * 32 + 8 * r + 4 * khalf;
-                    uint2 *sp = reinterpret_cast<uint2 *>(stg + ml * SPITCH + nl);
+                    uint2 *sp = reinterpret_cast<uint2 *>(stg_row(ml) + nl);
                     float v0 = acc[mi][ni][4 * r], v1 = acc[mi][ni][4 * r + 1];
                     float v2 = acc[mi][ni][4 * r + 2], v3 = acc[mi][ni][4 * r + 3];
                     if constexpr (decltype(scaled)::value) {
@@ -322,7 +379,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
             const int r = er + 16 * it;
             const int m = m0 + r, n = n0 + 8 * ec;
             if (m >= a.Mv) continue;
-            const uint4 w = *reinterpret_cast<const uint4 *>(stg + r * SPITCH + 8 * ec);
+            const uint4 w = *reinterpret_cast<const uint4 *>(stg_row(r) + 8 * ec);
             uint16_t *dp = Db + (int64_t)m * a.ldd + n;
             if (a.d_vec && n + 8 <= a.Nv) {
                 *reinterpret_cast<uint4 *>(dp) = w;
@@ -356,7 +413,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
             uint32_t u[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                u[j] = (uint32_t)stg[(8 * c + 2 * j) * SPITCH + nl] | ((uint32_t)stg[(8 * c + 2 * j + 1) * SPITCH + nl] << 16);
+                u[j] = (uint32_t)stg_row(8 * c + 2 * j)[nl] | ((uint32_t)stg_row(8 * c + 2 * j + 1)[nl] << 16);
             const int m = tm0 + 8 * c;
             if (n >= tNv) continue;
             uint16_t *tp = Tb + (int64_t)n * ldt + m;
@@ -518,7 +575,7 @@ static inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * 
 struct NSLayout {
     int64_t m, n, mp, np;
     bool transposed;
-    size_t off_x[2], off_xt[2], off_a, off_b, off_part, total;
+    size_t off_x[2], off_a, off_b, off_part, total;
 };
 
 static NSLayout ns_layout(int64_t batch, int64_t rows, int64_t cols) {
@@ -533,9 +590,7 @@ static NSLayout ns_layout(int64_t batch, int64_t rows, int64_t cols) {
     size_t o = 0;
     auto take = [&](size_t s) { size_t r = o; o += (s + 255) & ~(size_t)255; return r; };
     L.off_x[0] = take(xs);
-    L.off_xt[0] = take(xs);
     L.off_x[1] = take(xs);
-    L.off_xt[1] = take(xs);
     L.off_a = take(as);
     L.off_b = take(as);
     L.off_part = take((size_t)batch * NPART * 4);
@@ -546,8 +601,8 @@ static NSLayout ns_layout(int64_t batch, int64_t rows, int64_t cols) {
 static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
     GemmArgs a = a0;
     // operand loads address one matrix with 32-bit byte offsets
-    if (((int64_t)(a.M - 1) * a.ldp + a.K) * 2 >= (int64_t(1) << 31) ||
-        ((int64_t)(a.N - 1) * a.ldq + a.K) * 2 >= (int64_t(1) << 31)) {
+    const int64_t qspan = a.qk ? (int64_t)(a.K - 1) * a.ldq + a.N : (int64_t)(a.N - 1) * a.ldq + a.K;
+    if (((int64_t)(a.M - 1) * a.ldp + a.K) * 2 >= (int64_t(1) << 31) || qspan * 2 >= (int64_t(1) << 31)) {
         set_error("msr_gemm_nt: an operand matrix spans 2 GiB or more");
         return MSR_ERR_ARG;
     }
@@ -560,12 +615,16 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
     auto launch = [&](const GemmArgs &ab, dim3 grid) {
         const dim3 block(GEMM_THREADS);
         const bool c = ab.C != nullptr, d = ab.D != nullptr, dt = ab.DT != nullptr;
-        if (ab.symmetric && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false>), grid, block, 0, s, ab);
-        else if (ab.symmetric && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false>), grid, block, 0, s, ab);
-        else if (!ab.symmetric && c && d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, true>), grid, block, 0, s, ab);
-        else if (!ab.symmetric && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false>), grid, block, 0, s, ab);
-        else if (!ab.symmetric && c && !d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, false, true>), grid, block, 0, s, ab);
-        else if (!ab.symmetric && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false>), grid, block, 0, s, ab);
+        if (ab.qk) {   // NN: X' = B X + a X (D = X', or DT = X'^T for the tall output), diagnostics
+            if (ab.symmetric) { set_error("gemm: a K-major Q cannot be symmetric"); return (int)MSR_ERR_ARG; }
+            if (c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false, true>), grid, block, 0, s, ab);
+            else if (c && !d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, false, true, true>), grid, block, 0, s, ab);
+            else if (!c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, true>), grid, block, 0, s, ab);
+            else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
+        } else if (ab.symmetric && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false, false>), grid, block, 0, s, ab);
+        else if (ab.symmetric && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false, false>), grid, block, 0, s, ab);
+        else if (!ab.symmetric && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false, false>), grid, block, 0, s, ab);
+        else if (!ab.symmetric && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, false>), grid, block, 0, s, ab);
         else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
         return check_launch("gemm_nt_kernel");
     };
@@ -604,19 +663,18 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
 
 using namespace msr;
 
-extern "C" {
-
-int msr_gemm_nt(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q, int64_t ldq, int64_t strideQ,
-                const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D, int64_t ldd, int64_t strideD, int64_t M,
-                int64_t N, int64_t K, int64_t batch, float alpha, float beta, msr_stream_t stream) {
+static int gemm_entry(const char *name, int qk, const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q,
+                      int64_t ldq, int64_t strideQ, const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D,
+                      int64_t ldd, int64_t strideD, int64_t M, int64_t N, int64_t K, int64_t batch, float alpha,
+                      float beta, msr_stream_t stream) {
     if (!P || !Q || !D || batch < 0 || M <= 0 || N <= 0 || K <= 0 || (M % BM) || (N % BN) || (K % (2 * BK))) {
-        set_error("msr_gemm_nt: need M, N multiples of 256 and K a multiple of 128 (got %lld, %lld, %lld)",
+        set_error("%s: need M, N multiples of 256 and K a multiple of 128 (got %lld, %lld, %lld)", name,
                   (long long)M, (long long)N, (long long)K);
         return MSR_ERR_ARG;
     }
     if (!aligned(P, 16) || !aligned(Q, 16) || (ldp % 8) || (ldq % 8) || (strideP % 8) || (strideQ % 8) ||
         (C && beta != 0.0f && (!aligned(C, 16) || (ldc % 8) || (strideC % 8)))) {
-        set_error("msr_gemm_nt: P, Q and C must be 16-byte aligned with row and batch strides a multiple of 8 elements");
+        set_error("%s: P, Q and C must be 16-byte aligned with row and batch strides a multiple of 8 elements", name);
         return MSR_ERR_ALIGN;
     }
     if (batch == 0) return MSR_OK;
@@ -627,8 +685,24 @@ int msr_gemm_nt(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t 
     a.D = D; a.ldd = ldd; a.sD = strideD;
     a.DT = nullptr;
     a.M = (int)M; a.N = (int)N; a.K = (int)K; a.Mv = (int)M; a.Nv = (int)N;
-    a.alpha = alpha; a.beta = beta; a.symmetric = 0;
+    a.alpha = alpha; a.beta = beta; a.symmetric = 0; a.qk = qk;
     return launch_gemm(a, batch, (hipStream_t)stream);
+}
+
+extern "C" {
+
+int msr_gemm_nt(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q, int64_t ldq, int64_t strideQ,
+                const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D, int64_t ldd, int64_t strideD, int64_t M,
+                int64_t N, int64_t K, int64_t batch, float alpha, float beta, msr_stream_t stream) {
+    return gemm_entry("msr_gemm_nt", 0, P, ldp, strideP, Q, ldq, strideQ, C, ldc, strideC, D, ldd, strideD, M, N, K,
+                      batch, alpha, beta, stream);
+}
+
+int msr_gemm_nn(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q, int64_t ldq, int64_t strideQ,
+                const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D, int64_t ldd, int64_t strideD, int64_t M,
+                int64_t N, int64_t K, int64_t batch, float alpha, float beta, msr_stream_t stream) {
+    return gemm_entry("msr_gemm_nn", 1, P, ldp, strideP, Q, ldq, strideQ, C, ldc, strideC, D, ldd, strideD, M, N, K,
+                      batch, alpha, beta, stream);
 }
 
 int msr_ns_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, size_t *bytes) {
@@ -661,7 +735,6 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
     hipStream_t s = (hipStream_t)stream;
     char *ws = static_cast<char *>(workspace);
     uint16_t *X[2] = {(uint16_t *)(ws + L.off_x[0]), (uint16_t *)(ws + L.off_x[1])};
-    uint16_t *XT[2] = {(uint16_t *)(ws + L.off_xt[0]), (uint16_t *)(ws + L.off_xt[1])};
     uint16_t *A = (uint16_t *)(ws + L.off_a);
     uint16_t *B = (uint16_t *)(ws + L.off_b);
     float *part = (float *)(ws + L.off_part);
@@ -689,17 +762,16 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
         return check_launch("normalize_kernel");
     };
 
-    // Padded extents of the input layout: wide -> X is (mp x np); tall -> XT is (np x mp).
+    // Padded extents of the input layout: wide -> X = x0 (mp x np); tall -> X = x0^T, x0 is (np x mp).
     const int64_t Rp = L.transposed ? L.np : L.mp;
     const int64_t Cp = L.transposed ? L.mp : L.np;
     if (steps == 0) {
         return normalize(dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch), out, cols,
                          numel, nullptr, 0, 0, rows, cols);
     }
-    uint16_t *Sx = L.transposed ? XT[0] : X[0];
-    uint16_t *Tx = L.transposed ? X[0] : XT[0];
-    const int64_t ldS = Cp, ldT = Rp;
-    if ((rc = normalize(dim3((unsigned)(Cp / 64), (unsigned)(Rp / 64), (unsigned)batch), Sx, ldS, xs, Tx, ldT, xs, Rp,
+    uint16_t *Sx = L.transposed ? nullptr : X[0];
+    uint16_t *Tx = L.transposed ? X[0] : nullptr;
+    if ((rc = normalize(dim3((unsigned)(Cp / 64), (unsigned)(Rp / 64), (unsigned)batch), Sx, Cp, xs, Tx, Rp, xs, Rp,
                         Cp)))
         return rc;
 
@@ -726,16 +798,16 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
         g.M = mp; g.N = mp; g.K = mp; g.Mv = mp; g.Nv = mp;
         g.alpha = c_coef; g.beta = b_coef; g.symmetric = 1;
         if ((rc = launch_gemm(g, batch, s))) return rc;
-        // X' = (B X) + a X
+        // X' = (B X) + a X, X read K-major
         g = GemmArgs{};
         g.P = B; g.ldp = mp; g.sP = as;
-        g.Q = XT[cur]; g.ldq = mp; g.sQ = xs;
+        g.Q = X[cur]; g.ldq = np; g.sQ = xs;
         g.C = X[cur]; g.ldc = np; g.sC = xs;
         g.M = mp; g.N = np; g.K = mp;
-        g.alpha = 1.0f; g.beta = a_coef; g.symmetric = 0;
+        g.alpha = 1.0f; g.beta = a_coef; g.symmetric = 0; g.qk = 1;
         if (!last) {
             g.D = X[cur ^ 1]; g.ldd = np; g.sD = xs;
-            g.DT = XT[cur ^ 1]; g.lddt = mp; g.sDT = xs;
+            g.DT = nullptr;
             g.Mv = mp; g.Nv = np;
         } else if (!L.transposed) {
             g.D = out; g.ldd = cols; g.sD = numel;  // out[m][n], m = rows, n = cols

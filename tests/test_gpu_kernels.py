@@ -525,6 +525,42 @@ def test_gemm_nt_vs_torch_fp32(L, M, N, K, batch, alpha, beta):
     assert bool((err <= tol).all()), float((err - tol).max())
 
 
+@pytest.mark.parametrize("M,N,K,batch,alpha,beta,pad", [(256, 256, 128, 1, 1.0, 0.0, 0), (512, 768, 384, 2, 0.5, -1.25, 8),
+                                                        (256, 512, 1024, 3, 1.0, 3.4445, 0), (768, 256, 256, 9, 1.0, 0.0, 16)])
+def test_gemm_nn_vs_torch_fp32(L, M, N, K, batch, alpha, beta, pad):
+    """K-major Q (the X' = B X + a X product of Newton-Schulz): transposing LDS reads."""
+    torch.manual_seed(M + 3 * N + K)
+    ldq = N + pad
+    P = torch.randn(batch, M, K, device=DEV).to(torch.bfloat16)
+    Qs = torch.randn(batch, K, ldq, device=DEV).to(torch.bfloat16)
+    C = torch.randn(batch, M, N, device=DEV).to(torch.bfloat16)
+    D = torch.empty(batch, M, N, device=DEV, dtype=torch.bfloat16)
+    check(L, L.msr_gemm_nn(P.data_ptr(), K, M * K, Qs.data_ptr(), ldq, K * ldq, C.data_ptr(), N, M * N, D.data_ptr(),
+                           N, M * N, M, N, K, batch, alpha, beta, stream()), "gemm nn")
+    ref = alpha * torch.matmul(P.float(), Qs[:, :, :N].float().contiguous()) + beta * C.float()
+    err = (D.float() - ref).abs()
+    tol = 2.0 ** -8 * ref.abs() + 1e-5 * ref.abs().max()
+    assert bool((err <= tol).all()), float((err - tol).max())
+
+
+def test_gemm_nn_equals_nt_on_transposed_operand(L):
+    """The NN product with Q equals the NT product with Q^T bit for bit: same fp32
+    accumulation order and the same MFMA operand layout, only the LDS path differs."""
+    torch.manual_seed(11)
+    M, N, K, batch = 512, 768, 512, 2
+    P = torch.randn(batch, M, K, device=DEV).to(torch.bfloat16)
+    Q = torch.randn(batch, K, N, device=DEV).to(torch.bfloat16)
+    QT = Q.transpose(1, 2).contiguous()
+    C = torch.randn(batch, M, N, device=DEV).to(torch.bfloat16)
+    D1 = torch.empty(batch, M, N, device=DEV, dtype=torch.bfloat16)
+    D2 = torch.empty_like(D1)
+    check(L, L.msr_gemm_nn(P.data_ptr(), K, M * K, Q.data_ptr(), N, K * N, C.data_ptr(), N, M * N, D1.data_ptr(), N,
+                           M * N, M, N, K, batch, 1.0, 3.4445, stream()), "gemm nn")
+    check(L, L.msr_gemm_nt(P.data_ptr(), K, M * K, QT.data_ptr(), K, N * K, C.data_ptr(), N, M * N, D2.data_ptr(), N,
+                           M * N, M, N, K, batch, 1.0, 3.4445, stream()), "gemm nt")
+    assert torch.equal(D1, D2)
+
+
 def ns_same_op_fp32(G):
     """fp32 emulation of the library's NS: bf16 storage of X, A, B between
     products, fp32 accumulation, fused fp32 epilogues."""

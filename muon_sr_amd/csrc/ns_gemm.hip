@@ -7,7 +7,7 @@
 // K-contiguous Q fragment is one 16-byte read too, a K-major one (QK) two
 // 8-byte transposing reads (ds_read_b64_tr_b16).  The iterate X (m x n,
 // m <= n) is kept row-major:
-//     A  = X X^T          NT, P = X,  Q = X      (symmetric: upper tiles + mirror)
+//     A  = X X^T          NT, P = X,  Q = X      (symmetric: upper tiles only)
 //     B  = c A A + b A    NT, P = A,  Q = A      (A symmetric, so A A = A A^T)
 //     X' = B X + a X      NN, P = B,  Q = X
 // Workspace matrices are zero-padded to multiples of 256; zero padding is
@@ -53,12 +53,12 @@ struct GemmArgs {
     int Mv, Nv;        // stores are limited to m < Mv, n < Nv
     float alpha, beta;
     int tiles_m, tiles_n;
-    int symmetric;     // M == N, P == Q: only tiles ti <= tj, mirrored into D
+    int symmetric;     // M == N, P == Q: only tiles ti <= tj are computed and stored
     int d_vec;         // D rows allow 16-byte stores (set by launch_gemm)
     int dt_vec;        // DT rows allow 16-byte stores (set by launch_gemm)
     int tiles;         // tiles per matrix
     int per_xcd;       // 1-D grid over a multiple of 8 matrices, whole matrices per XCD
-    int qk;            // Q is K-major: Q[k][n] at Q + k * ldq + n (the NN product)
+    int gm;            // operand layouts by K range (GM_*)
 };
 
 // Work-group -> (matrix, tile).  Consecutive work-group ids are dispatched
@@ -147,7 +147,19 @@ __device__ __forceinline__ uint16_t *stg_row(int r) {
     return reinterpret_cast<uint16_t *>(b + o);
 }
 
-template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, bool QK>
+// Operand layouts of a product, by K range.  A slab of an operand is read
+// either row-major (its rows are the tile's 256 rows, K-contiguous: "R") or
+// K-major (64 rows of k, each the tile's 256 columns: "K").  P is K-major for
+// k < kP and Q for k < kQ, with kP <= kQ, so a K range is KK, RK or RR:
+//   GM_RR      P, Q row-major everywhere            (A = X X^T, msr_gemm_nt)
+//   GM_RK      Q K-major everywhere                  (msr_gemm_nn)
+//   GM_TRI_P   Q K-major; P is a symmetric matrix stored as its upper
+//              256-tiles only, so its row block ti is read K-major (as the
+//              stored block (kb, ti)) for kb < ti         (X' = B X + a X)
+//   GM_TRI_PQ  P and Q the same upper-stored symmetric matrix (B = c A A + b A)
+enum : int { GM_RR = 0, GM_RK = 1, GM_TRI_P = 2, GM_TRI_PQ = 3 };
+
+template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, int GM>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     int ti, tj;
     int64_t bz;
@@ -160,6 +172,11 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         bz = blockIdx.y;
     }
     const int m0 = ti * BM, n0 = tj * BN;
+    constexpr bool HAS_KK = GM == GM_TRI_P || GM == GM_TRI_PQ;
+    constexpr bool HAS_RK = GM != GM_RR;
+    constexpr bool HAS_RR = GM == GM_RR || GM == GM_TRI_PQ;
+    const int kP = HAS_KK ? m0 : 0;
+    const int kQ = GM == GM_RR ? 0 : GM == GM_TRI_PQ ? n0 : a.K;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -169,48 +186,46 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     const int khalf = lane >> 5;
 
     // Global -> LDS: buffer loads with the lds flag move 64 lanes x 16 B into
-    // 1 KiB of consecutive LDS (lane l to byte 16 l, base in M0).  Load i of
-    // wave w fills LDS chunks [(8 i + w) 64, +64) = rows (8 i + w) 8 + l / 8,
-    // physical chunk l % 8, i.e. logical chunk (l % 8) ^ ((row >> 1) & 7)
-    // = (l % 8) ^ (4 (w & 1) + l / 16).  Per-lane byte offsets are fixed; the
-    // row block (i) and the K slab go into the scalar offset.
+    // 1 KiB of consecutive LDS (lane l to byte 16 l, base in M0); load i
+    // (0..3) of wave w fills LDS block 8 i + w of the operand's slab.
+    //  * row-major slab (256 rows x 128 B): block 8 i + w = rows (8 i + w) 8 +
+    //    l / 8, physical chunk l % 8, i.e. logical chunk (l % 8) ^ ((row >> 1)
+    //    & 7) = (l % 8) ^ (4 (w & 1) + l / 16);
+    //  * K-major slab (64 rows x 512 B): chunk c of row k is stored at c ^ 4
+    //    (k & 3), so the four rows of one transposing read fall in different
+    //    banks; block 8 i + w = rows 16 i + 2 w + l / 32, physical chunk l % 32.
+    // Per-lane byte offsets are fixed; the row block (i) and the K slab go into
+    // the scalar offset.
     const int lrow = lane >> 3;
     const int lchunk = (lane & 7) ^ (4 * (wave & 1) + (lane >> 4));
+    const int kr = 2 * wave + (lane >> 5);
+    const int kc = (lane & 31) ^ (4 * (kr & 3));
     const __amdgpu_buffer_rsrc_t rP = __builtin_amdgcn_make_buffer_rsrc((void *)(a.P + bz * a.sP), (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rQ = __builtin_amdgcn_make_buffer_rsrc((void *)(a.Q + bz * a.sQ), (short)0, 0x7fffffff, 0x00020000);
-    const uint32_t voP = (uint32_t)(((int64_t)(m0 + wave * 8 + lrow) * a.ldp + lchunk * 8) * 2);
-    const uint32_t rowbP = (uint32_t)(64 * a.ldp * 2);
-    // A K-major Q slab is 64 rows (k) of the tile's 256 columns, 512 B per row;
-    // chunk c of row k is stored at c ^ 4 (k & 3), so the four rows of one
-    // transposing read fall in different banks.  Load i of wave w fills LDS block
-    // 8 i + w = rows 16 i + 2 w + lane / 32, physical chunk lane % 32.
-    uint32_t voQ, rowbQ, kbQ;
-    if constexpr (QK) {
-        const int qr = 2 * wave + (lane >> 5);
-        const int qc = (lane & 31) ^ (4 * (qr & 3));
-        voQ = (uint32_t)(((int64_t)qr * a.ldq + n0 + 8 * qc) * 2);
-        rowbQ = (uint32_t)(16 * a.ldq * 2);
-        kbQ = (uint32_t)(a.ldq * 2);
-    } else {
-        voQ = (uint32_t)(((int64_t)(n0 + wave * 8 + lrow) * a.ldq + lchunk * 8) * 2);
-        rowbQ = (uint32_t)(64 * a.ldq * 2);
-        kbQ = 2;
-    }
-    // Load j (0..7) of a slab: P row block j/2 for even j, Q row block j/2 for odd j.
-    auto dma = [&](int stage, int k0) {
+    const uint32_t voP_r = (uint32_t)(((int64_t)(m0 + wave * 8 + lrow) * a.ldp + lchunk * 8) * 2);
+    const uint32_t voQ_r = (uint32_t)(((int64_t)(n0 + wave * 8 + lrow) * a.ldq + lchunk * 8) * 2);
+    const uint32_t voP_k = (uint32_t)(((int64_t)kr * a.ldp + m0 + 8 * kc) * 2);
+    const uint32_t voQ_k = (uint32_t)(((int64_t)kr * a.ldq + n0 + 8 * kc) * 2);
+    const uint32_t ldbP = (uint32_t)(a.ldp * 2), ldbQ = (uint32_t)(a.ldq * 2);
+    // Load j (0..7) of a slab: P block j/2 for even j, Q block j/2 for odd j,
+    // each in the layout of the slab's K range (pk, qk: wave-uniform).
+    auto dma = [&](bool pk, bool qk, int stage, int k0) {
+        const uint32_t vp = pk ? voP_k : voP_r, vq = qk ? voQ_k : voQ_r;
+        const uint32_t ip = pk ? 16 * ldbP : 64 * ldbP, iq = qk ? 16 * ldbQ : 64 * ldbQ;
+        const uint32_t kp = pk ? k0 * ldbP : k0 * 2, kq = qk ? k0 * ldbQ : k0 * 2;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int i = j >> 1;
             const int dst = (8 * i + wave) * 1024;
             if (j & 1)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_void_t *)(lds_q(stage) + dst), 16, voQ, i * rowbQ + k0 * kbQ, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_void_t *)(lds_q(stage) + dst), 16, vq, i * iq + kq, 0, 0);
             else
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rP, (lds_void_t *)(lds_p(stage) + dst), 16, voP, i * rowbP + k0 * 2, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rP, (lds_void_t *)(lds_p(stage) + dst), 16, vp, i * ip + kp, 0, 0);
         }
     };
-    // Fragment reads: chunk (2 ks + khalf) ^ ((row >> 1) & 7) of row; bits 1-3 of
-    // row come from r32 only, so one byte offset per (operand, ks) serves all
-    // four 32-row blocks and both stages through the instruction offset.
+    // Row-major fragment reads: chunk (2 ks + khalf) ^ ((row >> 1) & 7) of row;
+    // bits 1-3 of row come from r32 only, so one byte offset per (operand, ks)
+    // serves all 32-row blocks through the instruction offset.
     const int sw = (r32 >> 1) & 7;
     uint32_t offP[4], offQ[4];
 #pragma unroll
@@ -219,34 +234,36 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         offP[ks] = (uint32_t)((wm * 128 + r32) * 128 + ch * 16);
         offQ[ks] = (uint32_t)((wn * 64 + r32) * 128 + ch * 16);
     }
-    // K-major Q: the fragment of lane l (column l % 32, k = 8 (l / 32) + 0..7 of
-    // the substep) is two transposing reads of 4 k each.  In a read, lane i of a
-    // 16-lane group returns element i % 4 of the 8-byte rows fetched by lanes
-    // i / 4 + 4 j (j = 0..3), so lane i fetches row k = i / 4 (+4 for the second
-    // read), columns 4 (i % 4) .. +3 of its group's 16.
-    uint32_t offQK[2];
+    // K-major fragment reads: the fragment of lane l (column l % 32, k = 8 (l /
+    // 32) + 0..7 of the substep) is two transposing reads of 4 k each.  In a
+    // read, lane i of a 16-lane group returns element i % 4 of the 8-byte rows
+    // fetched by lanes i / 4 + 4 j (j = 0..3), so lane i fetches row k = i / 4
+    // (+4 for the second read), columns 4 (i % 4) .. +3 of its group's 16.
+    uint32_t offPK[4], offQK[2];
     {
         const int G = lane >> 4, i = lane & 15;
+        const uint32_t rowb = (uint32_t)((8 * (G >> 1) + (i >> 2)) * 512 + (i & 1) * 8);
+        const int c0 = 2 * (G & 1) + ((i >> 1) & 1);
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-            const int c = wn * 8 + ni * 4 + 2 * (G & 1) + ((i >> 1) & 1);
-            offQK[ni] = (uint32_t)((8 * (G >> 1) + (i >> 2)) * 512 + (c ^ (4 * (i >> 2))) * 16 + (i & 1) * 8);
-        }
+        for (int mi = 0; mi < 4; ++mi) offPK[mi] = rowb + (uint32_t)(((wm * 16 + mi * 4 + c0) ^ (4 * (i >> 2))) * 16);
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) offQK[ni] = rowb + (uint32_t)(((wn * 8 + ni * 4 + c0) ^ (4 * (i >> 2))) * 16);
     }
-    auto frags = [&](int stage, int ks, bf16x8_t (&pa)[4], bf16x8_t (&qb)[2]) {
+    auto trfrag = [](const char *p) {
+        const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(p));
+        const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(p + 2048));
+        return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    auto frags = [&](auto PK, auto QK, int stage, int ks, bf16x8_t (&pa)[4], bf16x8_t (&qb)[2]) {
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
-            pa[mi] = *reinterpret_cast<const bf16x8_t *>(lds_p(stage) + offP[ks] + mi * 4096);
+        for (int mi = 0; mi < 4; ++mi) {
+            if constexpr (decltype(PK)::value) pa[mi] = trfrag(lds_p(stage) + offPK[mi] + ks * 8192);
+            else pa[mi] = *reinterpret_cast<const bf16x8_t *>(lds_p(stage) + offP[ks] + mi * 4096);
+        }
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) {
-            if constexpr (QK) {
-                const char *q = lds_q(stage) + offQK[ni] + ks * 8192;
-                const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(q));
-                const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(q + 2048));
-                qb[ni] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-            } else {
-                qb[ni] = *reinterpret_cast<const bf16x8_t *>(lds_q(stage) + offQ[ks] + ni * 4096);
-            }
+            if constexpr (decltype(QK)::value) qb[ni] = trfrag(lds_q(stage) + offQK[ni] + ks * 8192);
+            else qb[ni] = *reinterpret_cast<const bf16x8_t *>(lds_q(stage) + offQ[ks] + ni * 4096);
         }
     };
 
@@ -267,62 +284,98 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
                 acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], fa[b][mi], acc[mi][ni], 0, 0, 0);
     };
     // Each substep is one scheduling region: its 8 MFMAs interleaved with the
-    // fragment reads of the next substep (6, or 8 with a K-major Q).
-    auto pattern = [&]() {
+    // fragment reads of the next substep (6 row-major, 8 or 12 with K-major
+    // operands: 4 reads per row-major P, 8 per K-major P, 2 or 4 for Q).
+    auto pattern = [&](auto PK, auto QK) {
+        constexpr int NDS = (decltype(PK)::value ? 8 : 4) + (decltype(QK)::value ? 4 : 2);
+        if constexpr (NDS == 6) {
 #pragma unroll
-        for (int x = 0; x < (QK ? 8 : 6); ++x) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA (8 per substep)
-            if (!QK && (x == 0 || x == 2)) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            for (int x = 0; x < 6; ++x) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                if (x == 0 || x == 2) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+        } else {
+#pragma unroll
+            for (int x = 0; x < 8; ++x) {
+                if (NDS == 12 && (x & 1) == 0) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
         }
     };
-    // One K slab from `stage` while slab `knext` streams into the other stage.
-    // All 8 global->LDS loads of the next slab are issued before the slab's
-    // first MFMA: the operands arrive through L2 with a latency tail (misses to
-    // the Infinity Cache / HBM), and the wait at the end of the slab then has
-    // the whole slab to cover it (measured +3..19% over spreading the loads
-    // across the substeps).  The last slab of a tile reloads itself (knext =
-    // its own k): the loop then has a single code path, and the extra stage is
-    // never read.
-    auto slab = [&](int stage, int knext) {
-        dma(stage ^ 1, knext);
+    // One K slab from `stage` (layouts PK, QK) while slab `knext` (layouts
+    // pkn, qkn) streams into the other stage.  All 8 global->LDS loads of the
+    // next slab are issued before the slab's first MFMA: the operands arrive
+    // through L2 with a latency tail (misses to the Infinity Cache / HBM), and
+    // the wait at the end of the slab then has the whole slab to cover it
+    // (measured +3..19% over spreading the loads across the substeps).  The
+    // last substep's MFMAs overlap the next slab's first fragment reads, in
+    // this slab's layouts; after the last slab of a K range these are unused.
+    auto slab = [&](auto PK, auto QK, int stage, int knext, bool pkn, bool qkn) {
+        dma(pkn, qkn, stage ^ 1, knext);
         __builtin_amdgcn_sched_barrier(0);
-        frags(stage, 1, fa[1], fb[1]);
+        frags(PK, QK, stage, 1, fa[1], fb[1]);
         mm(0);
-        pattern();
+        pattern(PK, QK);
         __builtin_amdgcn_sched_barrier(0);
-        frags(stage, 2, fa[0], fb[0]);
+        frags(PK, QK, stage, 2, fa[0], fb[0]);
         mm(1);
-        pattern();
+        pattern(PK, QK);
         __builtin_amdgcn_sched_barrier(0);
-        frags(stage, 3, fa[1], fb[1]);
+        frags(PK, QK, stage, 3, fa[1], fb[1]);
         mm(0);
-        pattern();
+        pattern(PK, QK);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(0);   // own loads of the next slab landed, own reads of this stage done
         __syncthreads();                 // everyone's
-        frags(stage ^ 1, 0, fa[0], fb[0]);
+        frags(PK, QK, stage ^ 1, 0, fa[0], fb[0]);
         mm(1);
-        pattern();
+        pattern(PK, QK);
         __builtin_amdgcn_sched_barrier(0);
     };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
 
-    const int KT = a.K / BK;
-    dma(0, 0);
+    // The K ranges [0, kP) (KK), [kP, kQ) (RK) and [kQ, K) (RR) run as
+    // separate loops with uniform bodies, one after the other.  Each range
+    // starts in stage 0 with its first slab landed (ranges are multiples of 4
+    // slabs) and reads its own first fragments, so no fragment registers live
+    // across ranges and the accumulators keep their registers.  The last slab
+    // of a range loads the first slab of the next one (selected, not
+    // branched), or itself again at the end of K.
+    const int KT = a.K / BK, ktP = kP / BK, ktQ = kQ / BK;
+    auto range = [&](auto PK, auto QK, int kt0, int kt1) {
+        const bool end = kt1 >= KT;
+        const int kafter = end ? (kt1 - 1) * BK : kt1 * BK;
+        const bool pka = end ? decltype(PK)::value : kt1 < ktP, qka = end ? decltype(QK)::value : kt1 < ktQ;
+        frags(PK, QK, 0, 0, fa[0], fb[0]);
+#pragma clang loop unroll(disable)
+        for (int kt = kt0; kt < kt1; kt += 2) {
+            const bool more = kt + 2 < kt1;
+            slab(PK, QK, 0, (kt + 1) * BK, PK, QK);
+            slab(PK, QK, 1, more ? (kt + 2) * BK : kafter, more ? decltype(PK)::value : pka,
+                 more ? decltype(QK)::value : qka);
+        }
+    };
+    dma(0 < ktP, 0 < ktQ, 0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    frags(0, 0, fa[0], fb[0]);
-    // KT is even (K is a multiple of 128): every iteration runs both stages.
-    for (int kt = 0; kt < KT; kt += 2) {
-        slab(0, (kt + 1) * BK);
-        slab(1, (kt + 2 < KT ? kt + 2 : kt + 1) * BK);
+    if constexpr (HAS_KK) {
+        if (0 < ktP) range(T_{}, T_{}, 0, ktP);
+    }
+    if constexpr (HAS_RK) {
+        if (ktP < ktQ) range(F_{}, T_{}, ktP, ktQ);
+    }
+    if constexpr (HAS_RR) {
+        if (ktQ < KT) range(F_{}, F_{}, ktQ, KT);
     }
 
     // ---------------- epilogue ----------------
     // The output tile is staged through LDS as bf16 (row pitch SPITCH) so that
     // global traffic is 16-byte row chunks: C is loaded that way, D is stored
-    // that way, and the transposed copies (DT, or the mirror of an off-diagonal
-    // symmetric tile) are gathered column-wise from LDS.
+    // that way, and the transposed copy (DT) is gathered column-wise from LDS.
+    // A symmetric product stores its upper tiles only.
     // Lane l holds D[m = l % 32][n = 8r + 4(l / 32) + q] of each 32x32 MFMA tile.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // every wave is done with the operand slabs
@@ -394,18 +447,11 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     // Transposed copy: T[n][m] = tile[m][n].  Lanes of a wave take 64
     // consecutive n (a conflict-free LDS row read per element) and each stores
     // 8 consecutive m (16 bytes) of its row n.
-    bool mirror = false;
-    if constexpr (SYM && OUT_D) mirror = ti != tj;
-    if (OUT_DT || mirror) {
-        uint16_t *Tb;
-        int64_t ldt;
-        int tm0, tn0, tMv, tNv;
-        bool tvec;
-        if (OUT_DT) {
-            Tb = a.DT + bz * a.sDT; ldt = a.lddt; tm0 = m0; tn0 = n0; tMv = a.Mv; tNv = a.Nv; tvec = a.dt_vec;
-        } else {   // mirror of an off-diagonal symmetric tile into D (M == N, no bounds)
-            Tb = a.D + bz * a.sD; ldt = a.ldd; tm0 = m0; tn0 = n0; tMv = a.M; tNv = a.N; tvec = a.d_vec;
-        }
+    if constexpr (OUT_DT) {
+        uint16_t *Tb = a.DT + bz * a.sDT;
+        const int64_t ldt = a.lddt;
+        const int tm0 = m0, tn0 = n0, tMv = a.Mv, tNv = a.Nv;
+        const bool tvec = a.dt_vec;
         const int nl = tid & 255;                 // tile column = output row
         const int n = tn0 + nl;
 #pragma unroll 4
@@ -600,10 +646,22 @@ static NSLayout ns_layout(int64_t batch, int64_t rows, int64_t cols) {
 
 static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
     GemmArgs a = a0;
+    // an operand read from upper-stored symmetric tiles is square
+    if ((a.gm == GM_TRI_P && a.M != a.K) || (a.gm == GM_TRI_PQ && (a.M != a.K || a.N != a.K || !a.symmetric)) ||
+        (a.symmetric && a.gm != GM_RR && a.gm != GM_TRI_PQ)) {
+        set_error("gemm: operand layout %d does not fit a %d x %d x %d product", a.gm, a.M, a.N, a.K);
+        return MSR_ERR_ARG;
+    }
     // operand loads address one matrix with 32-bit byte offsets
-    const int64_t qspan = a.qk ? (int64_t)(a.K - 1) * a.ldq + a.N : (int64_t)(a.N - 1) * a.ldq + a.K;
-    if (((int64_t)(a.M - 1) * a.ldp + a.K) * 2 >= (int64_t(1) << 31) || qspan * 2 >= (int64_t(1) << 31)) {
-        set_error("msr_gemm_nt: an operand matrix spans 2 GiB or more");
+    const bool pk = a.gm == GM_TRI_P || a.gm == GM_TRI_PQ, prow = true;
+    const bool qk = a.gm != GM_RR, qrow = a.gm == GM_RR || a.gm == GM_TRI_PQ;
+    int64_t span = 0;
+    if (prow) span = std::max(span, (int64_t)(a.M - 1) * a.ldp + a.K);
+    if (pk) span = std::max(span, (int64_t)(a.K - 1) * a.ldp + a.M);
+    if (qrow) span = std::max(span, (int64_t)(a.N - 1) * a.ldq + a.K);
+    if (qk) span = std::max(span, (int64_t)(a.K - 1) * a.ldq + a.N);
+    if (span * 2 >= (int64_t(1) << 31)) {
+        set_error("gemm: an operand matrix spans 2 GiB or more");
         return MSR_ERR_ARG;
     }
     a.tiles_m = a.M / BM;
@@ -615,17 +673,27 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
     auto launch = [&](const GemmArgs &ab, dim3 grid) {
         const dim3 block(GEMM_THREADS);
         const bool c = ab.C != nullptr, d = ab.D != nullptr, dt = ab.DT != nullptr;
-        if (ab.qk) {   // NN: X' = B X + a X (D = X', or DT = X'^T for the tall output), diagnostics
-            if (ab.symmetric) { set_error("gemm: a K-major Q cannot be symmetric"); return (int)MSR_ERR_ARG; }
-            if (c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false, true>), grid, block, 0, s, ab);
-            else if (c && !d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, false, true, true>), grid, block, 0, s, ab);
-            else if (!c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, true>), grid, block, 0, s, ab);
+        const int gm = ab.gm;
+        if (ab.symmetric) {   // A = X X^T (RR), B = c A A + b A (TRI_PQ)
+            if (gm == GM_RR && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false, GM_RR>), grid, block, 0, s, ab);
+            else if (gm == GM_TRI_PQ && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false, GM_TRI_PQ>), grid, block, 0, s, ab);
+            else { set_error("gemm: unsupported symmetric product"); return (int)MSR_ERR_ARG; }
+        } else if (gm == GM_TRI_P) {   // X' = B X + a X: D = X', or DT = X'^T for the tall output
+            if (c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false, GM_TRI_P>), grid, block, 0, s, ab);
+            else if (c && !d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, false, true, GM_TRI_P>), grid, block, 0, s, ab);
             else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
-        } else if (ab.symmetric && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false, false>), grid, block, 0, s, ab);
-        else if (ab.symmetric && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false, false>), grid, block, 0, s, ab);
-        else if (!ab.symmetric && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false, false>), grid, block, 0, s, ab);
-        else if (!ab.symmetric && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, false>), grid, block, 0, s, ab);
-        else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
+        } else if (gm == GM_RK) {   // msr_gemm_nn
+            if (c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false, GM_RK>), grid, block, 0, s, ab);
+            else if (!c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_RK>), grid, block, 0, s, ab);
+            else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
+        } else if (gm == GM_RR) {   // msr_gemm_nt
+            if (c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false, GM_RR>), grid, block, 0, s, ab);
+            else if (!c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_RR>), grid, block, 0, s, ab);
+            else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
+        } else {
+            set_error("gemm: unknown operand layout %d", gm);
+            return (int)MSR_ERR_ARG;
+        }
         return check_launch("gemm_nt_kernel");
     };
     auto offset = [&](int64_t b0) {
@@ -685,7 +753,7 @@ static int gemm_entry(const char *name, int qk, const uint16_t *P, int64_t ldp, 
     a.D = D; a.ldd = ldd; a.sD = strideD;
     a.DT = nullptr;
     a.M = (int)M; a.N = (int)N; a.K = (int)K; a.Mv = (int)M; a.Nv = (int)N;
-    a.alpha = alpha; a.beta = beta; a.symmetric = 0; a.qk = qk;
+    a.alpha = alpha; a.beta = beta; a.symmetric = 0; a.gm = qk ? GM_RK : GM_RR;
     return launch_gemm(a, batch, (hipStream_t)stream);
 }
 
@@ -780,31 +848,31 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
     for (int it = 0; it < steps; ++it) {
         const bool last = it == steps - 1;
         GemmArgs g = {};
-        // A = X X^T
+        // A = X X^T, upper tiles stored
         g.P = X[cur]; g.ldp = np; g.sP = xs;
         g.Q = X[cur]; g.ldq = np; g.sQ = xs;
         g.C = nullptr;
         g.D = A; g.ldd = mp; g.sD = as;
         g.DT = nullptr;
         g.M = mp; g.N = mp; g.K = np; g.Mv = mp; g.Nv = mp;
-        g.alpha = 1.0f; g.beta = 0.0f; g.symmetric = 1;
+        g.alpha = 1.0f; g.beta = 0.0f; g.symmetric = 1; g.gm = GM_RR;
         if ((rc = launch_gemm(g, batch, s))) return rc;
-        // B = c (A A) + b A
+        // B = c (A A) + b A, reading A's lower tiles as the transposed upper ones; upper tiles stored
         g = GemmArgs{};
         g.P = A; g.ldp = mp; g.sP = as;
         g.Q = A; g.ldq = mp; g.sQ = as;
         g.C = A; g.ldc = mp; g.sC = as;
         g.D = B; g.ldd = mp; g.sD = as;
         g.M = mp; g.N = mp; g.K = mp; g.Mv = mp; g.Nv = mp;
-        g.alpha = c_coef; g.beta = b_coef; g.symmetric = 1;
+        g.alpha = c_coef; g.beta = b_coef; g.symmetric = 1; g.gm = GM_TRI_PQ;
         if ((rc = launch_gemm(g, batch, s))) return rc;
-        // X' = (B X) + a X, X read K-major
+        // X' = (B X) + a X, X read K-major, B's lower tiles as the transposed upper ones
         g = GemmArgs{};
         g.P = B; g.ldp = mp; g.sP = as;
         g.Q = X[cur]; g.ldq = np; g.sQ = xs;
         g.C = X[cur]; g.ldc = np; g.sC = xs;
         g.M = mp; g.N = np; g.K = mp;
-        g.alpha = 1.0f; g.beta = a_coef; g.symmetric = 0; g.qk = 1;
+        g.alpha = 1.0f; g.beta = a_coef; g.symmetric = 0; g.gm = GM_TRI_P;
         if (!last) {
             g.D = X[cur ^ 1]; g.ldd = np; g.sD = xs;
             g.DT = nullptr;

@@ -561,6 +561,38 @@ def test_gemm_nn_equals_nt_on_transposed_operand(L):
     assert torch.equal(D1, D2)
 
 
+def test_newton_schulz_equals_composed_products(L):
+    """msr_newton_schulz equals its iteration composed from the diagnostic GEMMs bit for
+    bit.  The symmetric A and B are stored as their upper 256-tiles and read back as the
+    transposed upper tiles; here the full products are computed and their lower tiles
+    replaced by the transposed upper ones, which is what those reads see.  4 x 4 tiles
+    per A exercise every K range (both operands transposed, one, none)."""
+    from muon_sr_amd.muon import newton_schulz, NS_COEFFS
+    a, b, c = NS_COEFFS
+    torch.manual_seed(5)
+    batch, m, n = 2, 1024, 1536
+    G = (torch.randn(batch, m, n, device=DEV) * 1e-3).to(torch.bfloat16)
+    X = newton_schulz(G, steps=0)
+    T = m // 256
+    upper = torch.tensor([[ti <= tj for tj in range(T)] for ti in range(T)], device=DEV)
+    upper = upper.repeat_interleave(256, 0).repeat_interleave(256, 1)
+
+    def tile_sym(S):
+        return torch.where(upper, S, S.transpose(1, 2))
+
+    def gemm(f, P, Q, C, M, N, K, ldq, alpha, beta):
+        D = torch.empty(batch, M, N, device=DEV, dtype=torch.bfloat16)
+        check(L, f(P.data_ptr(), K, M * K, Q.data_ptr(), ldq, Q[0].numel(), C.data_ptr() if C is not None else None,
+                   N, M * N, D.data_ptr(), N, M * N, M, N, K, batch, alpha, beta, stream()), "gemm")
+        return D
+
+    for _ in range(5):
+        A = tile_sym(gemm(L.msr_gemm_nt, X, X, None, m, m, n, n, 1.0, 0.0))
+        B = tile_sym(gemm(L.msr_gemm_nt, A, A, A, m, m, m, m, c, b))
+        X = gemm(L.msr_gemm_nn, B, X, X, m, n, m, n, 1.0, a)
+    assert torch.equal(newton_schulz(G), X)
+
+
 def ns_same_op_fp32(G):
     """fp32 emulation of the library's NS: bf16 storage of X, A, B between
     products, fp32 accumulation, fused fp32 epilogues."""

@@ -160,8 +160,9 @@ int msr_muon_apply(uint16_t *const *params, const uint16_t *upd, int64_t numel_e
  * Replaces _newton_schulz(G, steps, out_dtype=None) (muon_sr/muon_sr.py:82-98)
  * for a contiguous bf16 stack G [batch][rows][cols]; out has the same shape.
  * The iteration runs on the wide orientation (transposed when rows > cols):
- *   X = G/(||G||_F + 1e-7);  repeat: A = X X^T; B = b A + c A A; X = a X + B X.
- * Products accumulate in fp32; A, B and X are stored in bf16 between GEMMs.
+ *   X = G/(||G||_F + 1e-7);  repeat: A = X X^T; B = b A + c A A; X = a X + B X,
+ * evaluated as B' = c A A + b A + a I, X = B' X: products accumulate in fp32,
+ * A, B' and X are stored in bf16 between GEMMs.
  * Results do not depend on `batch` (each matrix is computed independently).
  * ------------------------------------------------------------------------- */
 int msr_ns_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, size_t *bytes);
@@ -211,20 +212,22 @@ int msr_quant_table_check(const void *qtable, const float *qmap_signed, const fl
 int msr_fastmath_check(int32_t kind, uint32_t bits_lo, uint32_t bits_hi, uint32_t *counts, int32_t n_counts,
                        msr_stream_t stream);
 
-/* Batched bf16 GEMM  D[b] = alpha * P[b] Q[b]^T + beta * C[b]  (fp32 accumulate, RNE bf16 out).
+/* Batched bf16 GEMM  D[b] = alpha * P[b] Q[b]^T + beta * C[b] + diag * I  (fp32 accumulate, RNE
+ * bf16 out; the diag term is added where m == n).
  * P: [M][K] (row stride ldp), Q: [N][K] (ldq), C/D: [M][N] (ldc/ldd); C may be NULL when beta == 0.
  * M, N multiples of 256 and K a multiple of 128 (the NS workspace is padded to these). */
 int msr_gemm_nt(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q, int64_t ldq,
                 int64_t strideQ, const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D, int64_t ldd,
                 int64_t strideD, int64_t M, int64_t N, int64_t K, int64_t batch, float alpha, float beta,
-                msr_stream_t stream);
+                float diag, msr_stream_t stream);
 
-/* The same with a K-major Q:  D[b] = alpha * P[b] Q[b] + beta * C[b],  Q: [K][N] (row stride ldq).
- * This is the kernel of Newton-Schulz's X' = B X + a X.  Test support: no counterpart in the reference. */
+/* The same with a K-major Q:  D[b] = alpha * P[b] Q[b] + beta * C[b] + diag * I,  Q: [K][N] (row
+ * stride ldq).  This is the kernel of Newton-Schulz's X' = B' X.  Test support: no counterpart in
+ * the reference. */
 int msr_gemm_nn(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q, int64_t ldq,
                 int64_t strideQ, const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D, int64_t ldd,
                 int64_t strideD, int64_t M, int64_t N, int64_t K, int64_t batch, float alpha, float beta,
-                msr_stream_t stream);
+                float diag, msr_stream_t stream);
 
 #ifdef __cplusplus
 }

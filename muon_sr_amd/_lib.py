@@ -54,9 +54,9 @@ SIGNATURES = {
     "msr_quant_table_check": (ctypes.c_int, [_P, _P, _P, _U32, _U32, _P, _I32, _P]),
     "msr_fastmath_check": (ctypes.c_int, [_I32, _U32, _U32, _P, _I32, _P]),
     "msr_gemm_nt": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
-                                   _I64, _I64, _I64, _I64, _F, _F, _P]),
+                                   _I64, _I64, _I64, _I64, _F, _F, _F, _P]),
     "msr_gemm_nn": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
-                                   _I64, _I64, _I64, _I64, _F, _F, _P]),
+                                   _I64, _I64, _I64, _I64, _F, _F, _F, _P]),
 }
 
 _lib = None

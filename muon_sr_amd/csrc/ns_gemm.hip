@@ -7,11 +7,12 @@
 // K-contiguous Q fragment is one 16-byte read too, a K-major one (QK) two
 // 8-byte transposing reads (ds_read_b64_tr_b16).  The iterate X (m x n,
 // m <= n) is kept row-major:
-//     A  = X X^T          NT, P = X,  Q = X      (symmetric: upper tiles only)
-//     B  = c A A + b A    NT, P = A,  Q = A      (A symmetric, so A A = A A^T)
-//     X' = B X + a X      NN, P = B,  Q = X
-// Workspace matrices are zero-padded to multiples of 256; zero padding is
-// preserved exactly by all three products, so only the final store is
+//     A  = X X^T              NT, P = X,  Q = X   (symmetric: upper tiles only)
+//     B' = c A A + b A + a I  NT, P = A,  Q = A   (A symmetric, so A A = A A^T)
+//     X' = B' X               NN, P = B', Q = X   (= B X + a X)
+// Workspace matrices are zero-padded to multiples of 256.  The padding of X
+// and A stays zero through every product (B' carries a on its padded
+// diagonal, which meets only zero rows of X), so only the final store is
 // bounds-checked.
 //
 // Kernel shape: 512 threads (8 wave64s in a 2 x 4 grid, two per SIMD), a
@@ -52,6 +53,7 @@ struct GemmArgs {
     int M, N, K;       // padded extents (multiples of 256, 256, 128)
     int Mv, Nv;        // stores are limited to m < Mv, n < Nv
     float alpha, beta;
+    float diag;        // added to the elements with m == n
     int tiles_m, tiles_n;
     int symmetric;     // M == N, P == Q: only tiles ti <= tj are computed and stored
     int d_vec;         // D rows allow 16-byte stores (set by launch_gemm)
@@ -390,9 +392,10 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         }
         __syncthreads();
     }
-    // alpha * acc (+ beta * C), rounded to bf16 by the hardware conversion; the
-    // multiply is skipped for alpha == 1 (x * 1 == x for every non-NaN x)
-    auto stage_out = [&](auto scaled) {
+    // (alpha * acc (+ beta * C)) (+ diag where m == n), rounded to bf16 by the
+    // hardware conversion; the multiply is skipped for alpha == 1 (x * 1 == x
+    // for every non-NaN x) and the diagonal term outside diagonal tiles.
+    auto stage_out = [&](auto scaled, auto dg) {
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
@@ -417,13 +420,24 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
                         v2 = v2 + a.beta * bf16_lo(cw.y);
                         v3 = v3 + a.beta * bf16_hi(cw.y);
                     }
+                    if constexpr (decltype(dg)::value) {   // m0 == n0 here
+                        v0 = ml == nl ? v0 + a.diag : v0;
+                        v1 = ml == nl + 1 ? v1 + a.diag : v1;
+                        v2 = ml == nl + 2 ? v2 + a.diag : v2;
+                        v3 = ml == nl + 3 ? v3 + a.diag : v3;
+                    }
                     *sp = make_uint2(rne_bf16x2(v0, v1), rne_bf16x2(v2, v3));
                 }
             }
         }
     };
-    if (a.alpha == 1.0f) stage_out(std::false_type{});
-    else stage_out(std::true_type{});
+    if (ti == tj && a.diag != 0.0f) {
+        if (a.alpha == 1.0f) stage_out(std::false_type{}, std::true_type{});
+        else stage_out(std::true_type{}, std::true_type{});
+    } else {
+        if (a.alpha == 1.0f) stage_out(std::false_type{}, std::false_type{});
+        else stage_out(std::true_type{}, std::false_type{});
+    }
     __syncthreads();
     if constexpr (OUT_D) {
         uint16_t *Db = a.D + bz * a.sD;
@@ -678,9 +692,9 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
             if (gm == GM_RR && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false, GM_RR>), grid, block, 0, s, ab);
             else if (gm == GM_TRI_PQ && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false, GM_TRI_PQ>), grid, block, 0, s, ab);
             else { set_error("gemm: unsupported symmetric product"); return (int)MSR_ERR_ARG; }
-        } else if (gm == GM_TRI_P) {   // X' = B X + a X: D = X', or DT = X'^T for the tall output
-            if (c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false, GM_TRI_P>), grid, block, 0, s, ab);
-            else if (c && !d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, false, true, GM_TRI_P>), grid, block, 0, s, ab);
+        } else if (gm == GM_TRI_P) {   // X' = B' X: D = X', or DT = X'^T for the tall output
+            if (!c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P>), grid, block, 0, s, ab);
+            else if (!c && !d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, false, true, GM_TRI_P>), grid, block, 0, s, ab);
             else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
         } else if (gm == GM_RK) {   // msr_gemm_nn
             if (c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false, GM_RK>), grid, block, 0, s, ab);
@@ -734,7 +748,7 @@ using namespace msr;
 static int gemm_entry(const char *name, int qk, const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q,
                       int64_t ldq, int64_t strideQ, const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D,
                       int64_t ldd, int64_t strideD, int64_t M, int64_t N, int64_t K, int64_t batch, float alpha,
-                      float beta, msr_stream_t stream) {
+                      float beta, float diag, msr_stream_t stream) {
     if (!P || !Q || !D || batch < 0 || M <= 0 || N <= 0 || K <= 0 || (M % BM) || (N % BN) || (K % (2 * BK))) {
         set_error("%s: need M, N multiples of 256 and K a multiple of 128 (got %lld, %lld, %lld)", name,
                   (long long)M, (long long)N, (long long)K);
@@ -753,7 +767,7 @@ static int gemm_entry(const char *name, int qk, const uint16_t *P, int64_t ldp, 
     a.D = D; a.ldd = ldd; a.sD = strideD;
     a.DT = nullptr;
     a.M = (int)M; a.N = (int)N; a.K = (int)K; a.Mv = (int)M; a.Nv = (int)N;
-    a.alpha = alpha; a.beta = beta; a.symmetric = 0; a.gm = qk ? GM_RK : GM_RR;
+    a.alpha = alpha; a.beta = beta; a.diag = diag; a.symmetric = 0; a.gm = qk ? GM_RK : GM_RR;
     return launch_gemm(a, batch, (hipStream_t)stream);
 }
 
@@ -761,16 +775,16 @@ extern "C" {
 
 int msr_gemm_nt(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q, int64_t ldq, int64_t strideQ,
                 const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D, int64_t ldd, int64_t strideD, int64_t M,
-                int64_t N, int64_t K, int64_t batch, float alpha, float beta, msr_stream_t stream) {
+                int64_t N, int64_t K, int64_t batch, float alpha, float beta, float diag, msr_stream_t stream) {
     return gemm_entry("msr_gemm_nt", 0, P, ldp, strideP, Q, ldq, strideQ, C, ldc, strideC, D, ldd, strideD, M, N, K,
-                      batch, alpha, beta, stream);
+                      batch, alpha, beta, diag, stream);
 }
 
 int msr_gemm_nn(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t *Q, int64_t ldq, int64_t strideQ,
                 const uint16_t *C, int64_t ldc, int64_t strideC, uint16_t *D, int64_t ldd, int64_t strideD, int64_t M,
-                int64_t N, int64_t K, int64_t batch, float alpha, float beta, msr_stream_t stream) {
+                int64_t N, int64_t K, int64_t batch, float alpha, float beta, float diag, msr_stream_t stream) {
     return gemm_entry("msr_gemm_nn", 1, P, ldp, strideP, Q, ldq, strideQ, C, ldc, strideC, D, ldd, strideD, M, N, K,
-                      batch, alpha, beta, stream);
+                      batch, alpha, beta, diag, stream);
 }
 
 int msr_ns_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, size_t *bytes) {
@@ -857,22 +871,22 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
         g.M = mp; g.N = mp; g.K = np; g.Mv = mp; g.Nv = mp;
         g.alpha = 1.0f; g.beta = 0.0f; g.symmetric = 1; g.gm = GM_RR;
         if ((rc = launch_gemm(g, batch, s))) return rc;
-        // B = c (A A) + b A, reading A's lower tiles as the transposed upper ones; upper tiles stored
+        // B' = c (A A) + b A + a I, reading A's lower tiles as the transposed upper ones; upper tiles stored
         g = GemmArgs{};
         g.P = A; g.ldp = mp; g.sP = as;
         g.Q = A; g.ldq = mp; g.sQ = as;
         g.C = A; g.ldc = mp; g.sC = as;
         g.D = B; g.ldd = mp; g.sD = as;
         g.M = mp; g.N = mp; g.K = mp; g.Mv = mp; g.Nv = mp;
-        g.alpha = c_coef; g.beta = b_coef; g.symmetric = 1; g.gm = GM_TRI_PQ;
+        g.alpha = c_coef; g.beta = b_coef; g.diag = a_coef; g.symmetric = 1; g.gm = GM_TRI_PQ;
         if ((rc = launch_gemm(g, batch, s))) return rc;
-        // X' = (B X) + a X, X read K-major, B's lower tiles as the transposed upper ones
+        // X' = B' X (= B X + a X), X read K-major, B' lower tiles as the transposed upper ones
         g = GemmArgs{};
         g.P = B; g.ldp = mp; g.sP = as;
         g.Q = X[cur]; g.ldq = np; g.sQ = xs;
-        g.C = X[cur]; g.ldc = np; g.sC = xs;
+        g.C = nullptr;
         g.M = mp; g.N = np; g.K = mp;
-        g.alpha = 1.0f; g.beta = a_coef; g.symmetric = 0; g.gm = GM_TRI_P;
+        g.alpha = 1.0f; g.beta = 0.0f; g.symmetric = 0; g.gm = GM_TRI_P;
         if (!last) {
             g.D = X[cur ^ 1]; g.ldd = np; g.sD = xs;
             g.DT = nullptr;

@@ -64,10 +64,10 @@ def test_argument_validation_without_gpu(lib):
     # two 256x256-padded iterates (ping-pong) + A + B, bf16, plus partial sums, per matrix
     assert size.value >= 2 * (2 * 256 * 256 * 2 + 2 * 256 * 256 * 2)
     assert lib.msr_newton_schulz(1, 1, 1, 300, 300, 5, 1.0, 1.0, 1.0, 1, 16, None) == 1004
-    assert lib.msr_gemm_nt(1, 64, 0, 1, 64, 0, None, 0, 0, 1, 256, 0, 255, 256, 64, 1, 1.0, 0.0, None) == 1001
+    assert lib.msr_gemm_nt(1, 64, 0, 1, 64, 0, None, 0, 0, 1, 256, 0, 255, 256, 64, 1, 1.0, 0.0, 0.0, None) == 1001
     # K must be a multiple of 128 (the K loop runs two 64-wide slabs per iteration)
-    assert lib.msr_gemm_nt(1, 64, 0, 1, 64, 0, None, 0, 0, 1, 256, 0, 256, 256, 64, 1, 1.0, 0.0, None) == 1001
-    assert lib.msr_gemm_nn(1, 64, 0, 1, 64, 0, None, 0, 0, 1, 256, 0, 256, 256, 64, 1, 1.0, 0.0, None) == 1001
+    assert lib.msr_gemm_nt(1, 64, 0, 1, 64, 0, None, 0, 0, 1, 256, 0, 256, 256, 64, 1, 1.0, 0.0, 0.0, None) == 1001
+    assert lib.msr_gemm_nn(1, 64, 0, 1, 64, 0, None, 0, 0, 1, 256, 0, 256, 256, 64, 1, 1.0, 0.0, 0.0, None) == 1001
 
 
 def test_overlapping_operands_are_rejected(lib):

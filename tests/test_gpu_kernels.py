@@ -509,17 +509,19 @@ def test_muon_apply_multi_vs_oracle(L, mode):
 # (b) MFMA GEMM and Newton-Schulz
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("M,N,K,batch,alpha,beta", [(256, 256, 128, 1, 1.0, 0.0), (512, 768, 384, 2, 0.5, -1.25),
-                                                    (256, 512, 1024, 3, 2.0315, -4.775)])
-def test_gemm_nt_vs_torch_fp32(L, M, N, K, batch, alpha, beta):
+@pytest.mark.parametrize("M,N,K,batch,alpha,beta,diag", [(256, 256, 128, 1, 1.0, 0.0, 0.0),
+                                                         (512, 768, 384, 2, 0.5, -1.25, 3.4445),
+                                                         (256, 512, 1024, 3, 2.0315, -4.775, 0.0)])
+def test_gemm_nt_vs_torch_fp32(L, M, N, K, batch, alpha, beta, diag):
     torch.manual_seed(M + N + K)
     P = torch.randn(batch, M, K, device=DEV).to(torch.bfloat16)
     Q = torch.randn(batch, N, K, device=DEV).to(torch.bfloat16)
     C = torch.randn(batch, M, N, device=DEV).to(torch.bfloat16)
     D = torch.empty(batch, M, N, device=DEV, dtype=torch.bfloat16)
     check(L, L.msr_gemm_nt(P.data_ptr(), K, M * K, Q.data_ptr(), K, N * K, C.data_ptr(), N, M * N, D.data_ptr(), N,
-                           M * N, M, N, K, batch, alpha, beta, stream()), "gemm")
+                           M * N, M, N, K, batch, alpha, beta, diag, stream()), "gemm")
     ref = alpha * torch.matmul(P.float(), Q.float().transpose(1, 2).contiguous()) + beta * C.float()
+    ref = ref + diag * torch.eye(M, N, device=DEV)
     err = (D.float() - ref).abs()
     tol = 2.0 ** -8 * ref.abs() + 1e-5 * ref.abs().max()
     assert bool((err <= tol).all()), float((err - tol).max())
@@ -536,7 +538,7 @@ def test_gemm_nn_vs_torch_fp32(L, M, N, K, batch, alpha, beta, pad):
     C = torch.randn(batch, M, N, device=DEV).to(torch.bfloat16)
     D = torch.empty(batch, M, N, device=DEV, dtype=torch.bfloat16)
     check(L, L.msr_gemm_nn(P.data_ptr(), K, M * K, Qs.data_ptr(), ldq, K * ldq, C.data_ptr(), N, M * N, D.data_ptr(),
-                           N, M * N, M, N, K, batch, alpha, beta, stream()), "gemm nn")
+                           N, M * N, M, N, K, batch, alpha, beta, 0.0, stream()), "gemm nn")
     ref = alpha * torch.matmul(P.float(), Qs[:, :, :N].float().contiguous()) + beta * C.float()
     err = (D.float() - ref).abs()
     tol = 2.0 ** -8 * ref.abs() + 1e-5 * ref.abs().max()
@@ -555,9 +557,9 @@ def test_gemm_nn_equals_nt_on_transposed_operand(L):
     D1 = torch.empty(batch, M, N, device=DEV, dtype=torch.bfloat16)
     D2 = torch.empty_like(D1)
     check(L, L.msr_gemm_nn(P.data_ptr(), K, M * K, Q.data_ptr(), N, K * N, C.data_ptr(), N, M * N, D1.data_ptr(), N,
-                           M * N, M, N, K, batch, 1.0, 3.4445, stream()), "gemm nn")
+                           M * N, M, N, K, batch, 1.0, 3.4445, 0.0, stream()), "gemm nn")
     check(L, L.msr_gemm_nt(P.data_ptr(), K, M * K, QT.data_ptr(), K, N * K, C.data_ptr(), N, M * N, D2.data_ptr(), N,
-                           M * N, M, N, K, batch, 1.0, 3.4445, stream()), "gemm nt")
+                           M * N, M, N, K, batch, 1.0, 3.4445, 0.0, stream()), "gemm nt")
     assert torch.equal(D1, D2)
 
 
@@ -580,22 +582,22 @@ def test_newton_schulz_equals_composed_products(L):
     def tile_sym(S):
         return torch.where(upper, S, S.transpose(1, 2))
 
-    def gemm(f, P, Q, C, M, N, K, ldq, alpha, beta):
+    def gemm(f, P, Q, C, M, N, K, ldq, alpha, beta, diag):
         D = torch.empty(batch, M, N, device=DEV, dtype=torch.bfloat16)
         check(L, f(P.data_ptr(), K, M * K, Q.data_ptr(), ldq, Q[0].numel(), C.data_ptr() if C is not None else None,
-                   N, M * N, D.data_ptr(), N, M * N, M, N, K, batch, alpha, beta, stream()), "gemm")
+                   N, M * N, D.data_ptr(), N, M * N, M, N, K, batch, alpha, beta, diag, stream()), "gemm")
         return D
 
     for _ in range(5):
-        A = tile_sym(gemm(L.msr_gemm_nt, X, X, None, m, m, n, n, 1.0, 0.0))
-        B = tile_sym(gemm(L.msr_gemm_nt, A, A, A, m, m, m, m, c, b))
-        X = gemm(L.msr_gemm_nn, B, X, X, m, n, m, n, 1.0, a)
+        A = tile_sym(gemm(L.msr_gemm_nt, X, X, None, m, m, n, n, 1.0, 0.0, 0.0))
+        B = tile_sym(gemm(L.msr_gemm_nt, A, A, A, m, m, m, m, c, b, a))   # B' = c A A + b A + a I
+        X = gemm(L.msr_gemm_nn, B, X, None, m, n, m, n, 1.0, 0.0, 0.0)
     assert torch.equal(newton_schulz(G), X)
 
 
 def ns_same_op_fp32(G):
-    """fp32 emulation of the library's NS: bf16 storage of X, A, B between
-    products, fp32 accumulation, fused fp32 epilogues."""
+    """fp32 emulation of the library's NS: bf16 storage of X, A, B' = c A A + b A + a I
+    between products, fp32 accumulation, fused fp32 epilogues."""
     a, b, c = O.NS_COEFFS
     rb = lambda x: x.to(torch.bfloat16).float()  # noqa: E731
     X = G.float()
@@ -604,10 +606,11 @@ def ns_same_op_fp32(G):
         X = X.mT
     nrm = rb(X.norm(dim=(-2, -1), keepdim=True))
     X = rb(X / rb(nrm + 1e-7))
+    eye = torch.eye(X.size(-2))
     for _ in range(5):
         A = rb(X @ X.mT)
-        B = rb(c * (A @ A) + b * A)
-        X = rb((B @ X) + a * X)
+        B = rb(c * (A @ A) + b * A + a * eye)
+        X = rb(B @ X)
     if tr:
         X = X.mT
     return X

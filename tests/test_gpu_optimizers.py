@@ -526,7 +526,7 @@ def test_sr_unbiased(L, mode):
 
 def _ns_same_op_fp32_gpu(G):
     """fp32 products on the GPU with bf16 storage between them, as the kernel
-    stores X, A and B; TF32 disabled."""
+    stores X, A and B' = c A A + b A + a I; TF32 disabled."""
     a, b, c = O.NS_COEFFS
     rb = lambda x: x.to(torch.bfloat16).float()  # noqa: E731
     X = G.float()
@@ -535,10 +535,11 @@ def _ns_same_op_fp32_gpu(G):
         X = X.mT.contiguous()
     nrm = rb(X.norm(dim=(-2, -1), keepdim=True))
     X = rb(X / rb(nrm + 1e-7))
+    eye = torch.eye(X.size(-2), device=X.device)
     for _ in range(5):
         A = rb(X @ X.mT.contiguous())
-        B = rb(c * (A @ A) + b * A)
-        X = rb((B @ X) + a * X)
+        B = rb(c * (A @ A) + b * A + a * eye)
+        X = rb(B @ X)
     return X.mT if tr else X
 
 

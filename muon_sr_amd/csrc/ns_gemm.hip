@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "vecio.hpp"
 #include "../../include/muon_sr_amd.h"
 
 namespace msr {
@@ -449,7 +450,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
             const uint4 w = *reinterpret_cast<const uint4 *>(stg_row(r) + 8 * ec);
             uint16_t *dp = Db + (int64_t)m * a.ldd + n;
             if (a.d_vec && n + 8 <= a.Nv) {
-                *reinterpret_cast<uint4 *>(dp) = w;
+                st_nt4(dp, u32x4_t{w.x, w.y, w.z, w.w});   // streaming store: measured 0.4-1.6 % faster NS
             } else {
                 const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll

@@ -563,18 +563,24 @@ def test_gemm_nn_equals_nt_on_transposed_operand(L):
     assert torch.equal(D1, D2)
 
 
-def test_newton_schulz_equals_composed_products(L):
+@pytest.mark.parametrize("rows,cols", [(1024, 1536), (1536, 1024)])
+def test_newton_schulz_equals_composed_products(L, rows, cols):
     """msr_newton_schulz equals its iteration composed from the diagnostic GEMMs bit for
     bit.  The symmetric A and B are stored as their upper 256-tiles and read back as the
     transposed upper tiles; here the full products are computed and their lower tiles
     replaced by the transposed upper ones, which is what those reads see.  4 x 4 tiles
-    per A exercise every K range (both operands transposed, one, none)."""
+    per A exercise every K range (both operands transposed, one, none); the tall case
+    runs on the transpose and writes the output transposed back."""
     from muon_sr_amd.muon import newton_schulz, NS_COEFFS
     a, b, c = NS_COEFFS
     torch.manual_seed(5)
-    batch, m, n = 2, 1024, 1536
-    G = (torch.randn(batch, m, n, device=DEV) * 1e-3).to(torch.bfloat16)
+    batch = 2
+    tall = rows > cols
+    m, n = min(rows, cols), max(rows, cols)
+    G = (torch.randn(batch, rows, cols, device=DEV) * 1e-3).to(torch.bfloat16)
     X = newton_schulz(G, steps=0)
+    if tall:
+        X = X.transpose(1, 2).contiguous()
     T = m // 256
     upper = torch.tensor([[ti <= tj for tj in range(T)] for ti in range(T)], device=DEV)
     upper = upper.repeat_interleave(256, 0).repeat_interleave(256, 1)
@@ -592,6 +598,8 @@ def test_newton_schulz_equals_composed_products(L):
         A = tile_sym(gemm(L.msr_gemm_nt, X, X, None, m, m, n, n, 1.0, 0.0, 0.0))
         B = tile_sym(gemm(L.msr_gemm_nt, A, A, A, m, m, m, m, c, b, a))   # B' = c A A + b A + a I
         X = gemm(L.msr_gemm_nn, B, X, None, m, n, m, n, 1.0, 0.0, 0.0)
+    if tall:
+        X = X.transpose(1, 2)
     assert torch.equal(newton_schulz(G), X)
 
 

@@ -1,12 +1,11 @@
 // Batched Newton-Schulz orthogonalisation on gfx950 bf16 MFMA.
 //
 // Every product of the iteration is one GEMM kernel,
-//     D[m][n] = alpha * sum_k P[m][k] * Q[n][k] + beta * C[m][n]      ("NT")
-//     D[m][n] = alpha * sum_k P[m][k] * Q[k][n] + beta * C[m][n]      ("NN", QK)
-// with P K-contiguous, so each MFMA P fragment is one 16-byte LDS read; a
-// K-contiguous Q fragment is one 16-byte read too, a K-major one (QK) two
-// 8-byte transposing reads (ds_read_b64_tr_b16).  The iterate X (m x n,
-// m <= n) is kept row-major:
+//     D[m][n] = alpha * sum_k P[m][k] * Q[n][k] + beta * C[m][n] (+ diag if m == n)
+// whose operands are read, per K range, either K-contiguous (one 16-byte LDS
+// read per MFMA fragment) or K-major (two 8-byte transposing reads,
+// ds_read_b64_tr_b16): "NT" has both K-contiguous, "NN" a K-major Q.  The
+// iterate X (m x n, m <= n) is kept row-major:
 //     A  = X X^T              NT, P = X,  Q = X   (symmetric: upper tiles only)
 //     B' = c A A + b A + a I  NT, P = A,  Q = A   (A symmetric, so A A = A A^T)
 //     X' = B' X               NN, P = B', Q = X   (= B X + a X)
@@ -21,9 +20,10 @@
 // directly, one slab ahead.  Each wave owns a 128x64 sub-tile = 4x2 tiles of
 // the 32x32x16 bf16 MFMA (fp32 accumulators); with two waves per SIMD, one
 // wave's MFMAs keep the matrix core busy while the other waits at the slab
-// barrier.  LDS rows are 128 B; chunk c of row r is stored at
+// barrier.  K-contiguous LDS rows are 128 B; chunk c of row r is stored at
 // c ^ ((r >> 1) & 7), so the 16 consecutive rows of one 16-lane quarter of a
-// fragment read (256 B) cover all 64 banks once.  Each K substep is one
+// fragment read (256 B) cover all 64 banks once (the K-major layout is
+// described at the loads).  Each K substep is one
 // scheduling region in which the MFMAs are interleaved with the next
 // substep's fragment reads; the next slab's loads are all issued at the start
 // of the slab.
@@ -158,8 +158,8 @@ __device__ __forceinline__ uint16_t *stg_row(int r) {
 //   GM_RK      Q K-major everywhere                  (msr_gemm_nn)
 //   GM_TRI_P   Q K-major; P is a symmetric matrix stored as its upper
 //              256-tiles only, so its row block ti is read K-major (as the
-//              stored block (kb, ti)) for kb < ti         (X' = B X + a X)
-//   GM_TRI_PQ  P and Q the same upper-stored symmetric matrix (B = c A A + b A)
+//              stored block (kb, ti)) for kb < ti         (X' = B' X)
+//   GM_TRI_PQ  P and Q the same upper-stored symmetric matrix (B' = c A A + b A + a I)
 enum : int { GM_RR = 0, GM_RK = 1, GM_TRI_P = 2, GM_TRI_PQ = 3 };
 
 template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, int GM>

@@ -61,6 +61,22 @@ const char *msr_last_error(void);
 int msr_sr_accum(uint16_t *acc, const void *grad, int32_t grad_is_f32, int64_t n, uint32_t seed,
                  int32_t zero_init, int32_t noise_mode, const uint16_t *inject, msr_stream_t stream);
 
+/* (c) SR accumulation fused with the weight-gradient GEMM of a linear layer
+ * y = x W^T: the bf16 weight gradient dW = dy^T x that autograd hands the
+ * accumulation hook (muon_sr/triton_adamw.py:252-265) is accumulated into acc
+ * as the hook's _grad_accum_kernel (:206-229) does, without being written:
+ *   acc[o][i] <- SR_bf16( f32(acc[o][i]) + f32(RNE_bf16( sum_t dy[t][o] x[t][i] )) )
+ * (fp32 products accumulated in fp32; noise of element offset o * in + i, as
+ * msr_sr_accum on the contiguous [out][in] buffer).  No counterpart in the
+ * reference, which runs the GEMM and the accumulation separately.
+ * x: bf16 [tokens][in] (row stride ldx), dy: bf16 [tokens][out] (ldy), acc:
+ * bf16 [out][in] contiguous; in and out multiples of 256, tokens a multiple of
+ * 128 (else MSR_ERR_ARG: use the GEMM and msr_sr_accum).  zero_init, seed,
+ * noise_mode and inject as msr_sr_accum. */
+int msr_linear_wgrad_sr_accum(uint16_t *acc, const uint16_t *x, int64_t ldx, const uint16_t *dy, int64_t ldy,
+                              int64_t tokens, int64_t in_features, int64_t out_features, uint32_t seed,
+                              int32_t zero_init, int32_t noise_mode, const uint16_t *inject, msr_stream_t stream);
+
 /* (c) SR gradient accumulation of many tensors in one launch.
  * Same arithmetic and noise as one msr_sr_accum call per item (noise offsets
  * restart at 0 in every tensor), for the hooks of one backward pass collected

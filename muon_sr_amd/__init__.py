@@ -11,10 +11,12 @@ from ._lib import set_sr_noise, get_sr_noise
 from .adamw_8bit import TritonAdamW8bit, create_dynamic_map
 from .adamw import TritonAdamW, TritonSRAccumulator
 from .muon import TritonMuonSR, TritonMuonSRWithAuxAdam, newton_schulz
+from .linear import SRLinear, linear_wgrad_sr_accum
 
 __all__ = [
     "TritonAdamW8bit",
     "TritonAdamW", "TritonSRAccumulator",
     "TritonMuonSR", "TritonMuonSRWithAuxAdam",
     "newton_schulz", "create_dynamic_map", "set_sr_noise", "get_sr_noise",
+    "SRLinear", "linear_wgrad_sr_accum",
 ]

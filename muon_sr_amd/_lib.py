@@ -57,6 +57,7 @@ SIGNATURES = {
                                    _I64, _I64, _I64, _I64, _F, _F, _F, _P]),
     "msr_gemm_nn": (ctypes.c_int, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
                                    _I64, _I64, _I64, _I64, _F, _F, _F, _P]),
+    "msr_linear_wgrad_sr_accum": (ctypes.c_int, [_P, _P, _I64, _P, _I64, _I64, _I64, _I64, _U32, _I32, _I32, _P, _P]),
 }
 
 _lib = None

@@ -190,6 +190,8 @@ class TritonSRAccumulator:
     @staticmethod
     def _accum_hook(p):
         grad = p.grad
+        if grad is None:   # the gradient went straight into p.acc_grad (SRLinear's fused weight gradient)
+            return
         n = grad.numel()
         seed = random.getrandbits(32)
         if grad.dtype not in (torch.bfloat16, torch.float32):

@@ -62,6 +62,9 @@ struct GemmArgs {
     int tiles;         // tiles per matrix
     int per_xcd;       // 1-D grid over a multiple of 8 matrices, whole matrices per XCD
     int gm;            // operand layouts by K range (GM_*)
+    int sracc;         // 0, or 1 + the noise mode of the SR-accumulating store (D = acc)
+    int zero_init;     // SR-accumulating store: acc reads as zero
+    Noise ns;          // SR-accumulating store: noise of element offset m * ldd + n
 };
 
 // Work-group -> (matrix, tile).  Consecutive work-group ids are dispatched
@@ -160,9 +163,13 @@ __device__ __forceinline__ uint16_t *stg_row(int r) {
 //              256-tiles only, so its row block ti is read K-major (as the
 //              stored block (kb, ti)) for kb < ti         (X' = B' X)
 //   GM_TRI_PQ  P and Q the same upper-stored symmetric matrix (B' = c A A + b A + a I)
-enum : int { GM_RR = 0, GM_RK = 1, GM_TRI_P = 2, GM_TRI_PQ = 3 };
+//   GM_KK      P, Q K-major everywhere (the weight gradient dW = dY^T X of
+//              row-major activations)
+enum : int { GM_RR = 0, GM_RK = 1, GM_TRI_P = 2, GM_TRI_PQ = 3, GM_KK = 4 };
 
-template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, int GM>
+// SRACC >= 0: D is a bf16 accumulator and the store adds to it with stochastic
+// rounding (noise mode SRACC), as msr_sr_accum does with the RNE bf16 product.
+template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, int GM, int SRACC = -1>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     int ti, tj;
     int64_t bz;
@@ -175,10 +182,10 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         bz = blockIdx.y;
     }
     const int m0 = ti * BM, n0 = tj * BN;
-    constexpr bool HAS_KK = GM == GM_TRI_P || GM == GM_TRI_PQ;
-    constexpr bool HAS_RK = GM != GM_RR;
+    constexpr bool HAS_KK = GM == GM_TRI_P || GM == GM_TRI_PQ || GM == GM_KK;
+    constexpr bool HAS_RK = GM == GM_RK || GM == GM_TRI_P || GM == GM_TRI_PQ;
     constexpr bool HAS_RR = GM == GM_RR || GM == GM_TRI_PQ;
-    const int kP = HAS_KK ? m0 : 0;
+    const int kP = GM == GM_KK ? a.K : HAS_KK ? m0 : 0;
     const int kQ = GM == GM_RR ? 0 : GM == GM_TRI_PQ ? n0 : a.K;
 
     const int tid = threadIdx.x;
@@ -440,7 +447,26 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         else stage_out(std::true_type{}, std::false_type{});
     }
     __syncthreads();
-    if constexpr (OUT_D) {
+    if constexpr (SRACC >= 0) {
+        // acc <- SR(f32(acc) + f32(tile)), 8 elements (one noise8 group) per access
+        uint16_t *Db = a.D + bz * a.sD;
+#pragma unroll 4
+        for (int it = 0; it < 16; ++it) {
+            const int r = er + 16 * it;
+            const int64_t o0 = (int64_t)(m0 + r) * a.ldd + n0 + 8 * ec;
+            const uint4 w = *reinterpret_cast<const uint4 *>(stg_row(r) + 8 * ec);
+            uint4 c = make_uint4(0u, 0u, 0u, 0u);
+            if (!a.zero_init) c = *reinterpret_cast<const uint4 *>(Db + o0);
+            const uint32_t gw[4] = {w.x, w.y, w.z, w.w}, cw[4] = {c.x, c.y, c.z, c.w};
+            uint32_t rn[8], o[4];
+            noise8<SRACC>(a.ns, o0, 8, rn);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                o[j] = pack2(sr_bf16(bf16_lo(cw[j]) + bf16_lo(gw[j]), rn[2 * j]),
+                             sr_bf16(bf16_hi(cw[j]) + bf16_hi(gw[j]), rn[2 * j + 1]));
+            *reinterpret_cast<uint4 *>(Db + o0) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+    } else if constexpr (OUT_D) {
         uint16_t *Db = a.D + bz * a.sD;
 #pragma unroll 4
         for (int it = 0; it < 16; ++it) {
@@ -668,7 +694,7 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
         return MSR_ERR_ARG;
     }
     // operand loads address one matrix with 32-bit byte offsets
-    const bool pk = a.gm == GM_TRI_P || a.gm == GM_TRI_PQ, prow = true;
+    const bool pk = a.gm == GM_TRI_P || a.gm == GM_TRI_PQ || a.gm == GM_KK, prow = a.gm != GM_KK;
     const bool qk = a.gm != GM_RR, qrow = a.gm == GM_RR || a.gm == GM_TRI_PQ;
     int64_t span = 0;
     if (prow) span = std::max(span, (int64_t)(a.M - 1) * a.ldp + a.K);
@@ -689,7 +715,10 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
         const dim3 block(GEMM_THREADS);
         const bool c = ab.C != nullptr, d = ab.D != nullptr, dt = ab.DT != nullptr;
         const int gm = ab.gm;
-        if (ab.symmetric) {   // A = X X^T (RR), B = c A A + b A (TRI_PQ)
+        if (ab.sracc > 0) {   // weight gradient accumulated into D with SR
+            if (gm != GM_KK || ab.symmetric || c || !d || dt) { set_error("gemm: unsupported SR-accumulating product"); return (int)MSR_ERR_ARG; }
+            MSR_DISPATCH_NOISE(ab.sracc - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_KK, M>), grid, block, 0, s, ab));
+        } else if (ab.symmetric) {   // A = X X^T (RR), B = c A A + b A (TRI_PQ)
             if (gm == GM_RR && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false, GM_RR>), grid, block, 0, s, ab);
             else if (gm == GM_TRI_PQ && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false, GM_TRI_PQ>), grid, block, 0, s, ab);
             else { set_error("gemm: unsupported symmetric product"); return (int)MSR_ERR_ARG; }
@@ -786,6 +815,50 @@ int msr_gemm_nn(const uint16_t *P, int64_t ldp, int64_t strideP, const uint16_t 
                 int64_t N, int64_t K, int64_t batch, float alpha, float beta, float diag, msr_stream_t stream) {
     return gemm_entry("msr_gemm_nn", 1, P, ldp, strideP, Q, ldq, strideQ, C, ldc, strideC, D, ldd, strideD, M, N, K,
                       batch, alpha, beta, diag, stream);
+}
+
+int msr_linear_wgrad_sr_accum(uint16_t *acc, const uint16_t *x, int64_t ldx, const uint16_t *dy, int64_t ldy,
+                              int64_t tokens, int64_t in_features, int64_t out_features, uint32_t seed,
+                              int32_t zero_init, int32_t noise_mode, const uint16_t *inject, msr_stream_t stream) {
+    if (!acc || !x || !dy || tokens <= 0 || in_features <= 0 || out_features <= 0 || (in_features % BN) ||
+        (out_features % BM) || (tokens % (2 * BK)) || ldx < in_features || ldy < out_features ||
+        in_features >= (1 << 30) || out_features >= (1 << 30) || tokens >= (1 << 30)) {
+        set_error("msr_linear_wgrad_sr_accum: need in and out features multiples of 256 and tokens a multiple of 128 "
+                  "(got %lld, %lld, %lld)", (long long)in_features, (long long)out_features, (long long)tokens);
+        return MSR_ERR_ARG;
+    }
+    if (noise_mode < 0 || noise_mode > 2 || (noise_mode == NOISE_INJECT && !inject)) {
+        set_error("msr_linear_wgrad_sr_accum: bad noise_mode %d", (int)noise_mode);
+        return MSR_ERR_ARG;
+    }
+    if (!aligned(acc, 16) || !aligned(x, 16) || !aligned(dy, 16) || (ldx % 8) || (ldy % 8)) {
+        set_error("msr_linear_wgrad_sr_accum: acc, x and dy must be 16-byte aligned with row strides a multiple of 8");
+        return MSR_ERR_ALIGN;
+    }
+    const size_t ab = 2 * (size_t)in_features * (size_t)out_features;
+    const size_t xb = 2 * ((size_t)(tokens - 1) * (size_t)ldx + (size_t)in_features);
+    const size_t yb = 2 * ((size_t)(tokens - 1) * (size_t)ldy + (size_t)out_features);
+    auto touch = [](const void *p, size_t np, const void *q, size_t nq) {
+        const uintptr_t u = (uintptr_t)p, v = (uintptr_t)q;
+        return u < v + nq && v < u + np;
+    };
+    if (touch(acc, ab, x, xb) || touch(acc, ab, dy, yb)) {
+        set_error("msr_linear_wgrad_sr_accum: acc overlaps x or dy");
+        return MSR_ERR_OVERLAP;
+    }
+    GemmArgs a = {};
+    a.P = dy; a.ldp = ldy; a.sP = 0;   // P[o][t] = dy[t][o], K-major
+    a.Q = x; a.ldq = ldx; a.sQ = 0;    // Q[i][t] = x[t][i], K-major
+    a.C = nullptr;
+    a.D = acc; a.ldd = in_features; a.sD = 0;
+    a.DT = nullptr;
+    a.M = (int)out_features; a.N = (int)in_features; a.K = (int)tokens; a.Mv = a.M; a.Nv = a.N;
+    a.alpha = 1.0f; a.beta = 0.0f; a.diag = 0.0f; a.symmetric = 0; a.gm = GM_KK;
+    a.sracc = 1 + noise_mode;
+    a.zero_init = zero_init != 0;
+    a.ns.key = seed_key(seed, 0);
+    a.ns.inject = inject;
+    return launch_gemm(a, 1, (hipStream_t)stream);
 }
 
 int msr_ns_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, size_t *bytes) {

@@ -68,6 +68,11 @@ def test_argument_validation_without_gpu(lib):
     # K must be a multiple of 128 (the K loop runs two 64-wide slabs per iteration)
     assert lib.msr_gemm_nt(1, 64, 0, 1, 64, 0, None, 0, 0, 1, 256, 0, 256, 256, 64, 1, 1.0, 0.0, 0.0, None) == 1001
     assert lib.msr_gemm_nn(1, 64, 0, 1, 64, 0, None, 0, 0, 1, 256, 0, 256, 256, 64, 1, 1.0, 0.0, 0.0, None) == 1001
+    # fused weight-gradient accumulation: features multiples of 256, tokens of 128, known noise mode
+    assert lib.msr_linear_wgrad_sr_accum(1, 1, 256, 1, 256, 100, 256, 256, 0, 0, 0, None, None) == 1001
+    assert lib.msr_linear_wgrad_sr_accum(1, 1, 300, 1, 256, 128, 300, 256, 0, 0, 0, None, None) == 1001
+    assert lib.msr_linear_wgrad_sr_accum(1, 1, 256, 1, 256, 128, 256, 256, 0, 0, 7, None, None) == 1001
+    assert lib.msr_linear_wgrad_sr_accum(1, 1, 256, 1, 256, 128, 256, 256, 0, 0, 2, None, None) == 1001
 
 
 def test_overlapping_operands_are_rejected(lib):

@@ -482,6 +482,60 @@ def bench_centralize(reps=10):
     return out
 
 
+def bench_wgrad(reps=5, tokens=8192):
+    """Weight gradients of one Llama-3-8B decoder layer (q, k, v, o, gate, up,
+    down) over `tokens` tokens, accumulated into bf16 buffers with SR: this
+    library's fused kernel (msr_linear_wgrad_sr_accum: dW never written)
+    against what the reference's hook does after autograd, a torch bf16 GEMM
+    writing dW then the accumulation (msr_sr_accum).  Flops 2 * tokens * in *
+    out per weight."""
+    import random
+    import torch
+    from muon_sr_amd import _lib
+    from muon_sr_amd.linear import linear_wgrad_sr_accum
+    dev = "cuda:0"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(12)
+    d, kv, ffn = 4096, 1024, 14336
+    shapes = [(d, d), (kv, d), (kv, d), (d, d), (ffn, d), (ffn, d), (d, ffn)]   # (out, in)
+    xs = {fin: (torch.randn(tokens, fin, device=dev, generator=gen)).to(torch.bfloat16) for fin in (d, ffn)}
+    dys = {fout: (torch.randn(tokens, fout, device=dev, generator=gen) * 1e-3).to(torch.bfloat16)
+           for fout in (d, kv, ffn)}
+    ws = [torch.nn.Parameter(torch.zeros(o, i, device=dev, dtype=torch.bfloat16)) for o, i in shapes]
+    accs = [torch.zeros(o, i, device=dev, dtype=torch.bfloat16) for o, i in shapes]
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def fused():
+        for w, (o, i) in zip(ws, shapes):
+            assert linear_wgrad_sr_accum(w, xs[i], dys[o], seed=random.getrandbits(32))
+
+    def unfused():
+        for acc, (o, i) in zip(accs, shapes):
+            dw = dys[o].t() @ xs[i]
+            _lib.check(L.msr_sr_accum(acc.data_ptr(), dw.data_ptr(), 0, dw.numel(), random.getrandbits(32), 0,
+                                      _lib.noise_mode(), None, stream), "msr_sr_accum")
+
+    def timed(fn):
+        fn()
+        sync()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        sync()
+        return s.elapsed_time(e) / reps
+
+    ms, ref_ms = timed(fused), timed(unfused)
+    fl = sum(2.0 * tokens * o * i for o, i in shapes)
+    out = dict(tokens=tokens, weights=len(shapes), tflop=fl / 1e12, fused_ms=ms, fused_tflops=fl / (ms * 1e9),
+               torch_gemm_then_accum_ms=ref_ms, speedup=ref_ms / ms)
+    del xs, dys, ws, accs
+    torch.cuda.empty_cache()
+    return out
+
+
 def copy_calibration():
     """A plain device copy of known size (2^28 fp32: 1 GiB read + 1 GiB written per
     launch).  Profiled with FETCH_SIZE / WRITE_SIZE, it gives the factor that turns
@@ -517,7 +571,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="adamw8bit,sr_accum,ns,centralize,full")
+    ap.add_argument("--configs", default="adamw8bit,sr_accum,ns,centralize,wgrad,full")
     ap.add_argument("--noise", default="philox8", choices=["philox8", "triton"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -553,6 +607,10 @@ def main():
         r = bench_centralize()
         log(f"centralize: {r}")
         configs["centralize_embed_128256x4096"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+    if "wgrad" in todo:
+        r = bench_wgrad()
+        log(f"wgrad: {r}")
+        configs["wgrad_sr_accum_llama3_8b_layer"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
     if "full" in todo:
         r = bench_full(steps_timed=2, warmup=1)
         log(f"full hybrid: {r}")

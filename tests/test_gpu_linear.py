@@ -125,3 +125,26 @@ def test_sr_linear_matches_hook_accumulation(L, fin, fout, T):
         torch.testing.assert_close(ref.bias.acc_grad.float(), fused.bias.acc_grad.float(), rtol=2 ** -6, atol=1e-6)
     finally:
         muon_sr_amd.set_sr_noise(old)
+
+
+def test_sr_linear_edge_cases(L):
+    """No bias, an input without grad, a non-contiguous 3-D input, and an fp32 layer
+    (which returns dW to autograd, so the hook or .grad sees it as for nn.Linear)."""
+    from muon_sr_amd import SRLinear, TritonSRAccumulator
+    torch.manual_seed(3)
+    m = SRLinear(256, 512, bias=False).to(DEV).to(torch.bfloat16)
+    h = TritonSRAccumulator.assign_hooks(m)
+    x = torch.randn(256, 4, 256, device=DEV).to(torch.bfloat16).transpose(0, 1)   # [4, 256, 256], non-contiguous
+    m(x).float().sum().backward()
+    assert m.weight.grad is None and m.weight.acc_grad.shape == (512, 256)
+    dy = torch.ones(4 * 256, 512, device=DEV, dtype=torch.bfloat16)
+    ref = (dy.float().t() @ x.reshape(-1, 256).float())
+    torch.testing.assert_close(m.weight.acc_grad.float(), ref, rtol=2 ** -7, atol=1e-3)
+    for h_ in h:
+        h_.remove()
+    f = SRLinear(256, 256).to(DEV)                       # fp32: unfused, dW returned to autograd
+    xf = torch.randn(128, 256, device=DEV, requires_grad=True)
+    f(xf).sum().backward()
+    assert f.weight.grad is not None and not hasattr(f.weight, "acc_grad")
+    torch.testing.assert_close(f.weight.grad, torch.ones(128, 256, device=DEV).t() @ xf.detach(), rtol=1e-5, atol=1e-4)
+    assert xf.grad is not None and f.bias.grad is not None

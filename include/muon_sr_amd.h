@@ -219,10 +219,12 @@ int msr_quant_table_check(const void *qtable, const float *qmap_signed, const fl
 /* Device self-check of the fast kernel's correctly rounded building blocks
  * against the IEEE operations, over the float bit patterns u in
  * [bits_lo, bits_hi]: kind 0 sqrt, alone and fused into the update's
- * sqrt(v) + eps (u <= bits(2^62)); kind 1 reciprocal and
- * kind 2 quotient m/d for 16 hashed m per d (bits(2^-60) <= u < bits(2));
- * kind 3 the hardware fp32->bf16 round-to-nearest-even of the GEMM epilogues
- * against the bit-level rounding (any u).
+ * sqrt(v) + eps (u <= bits(2^62)); kind 1 reciprocal
+ * (bits(2^-60) <= u < bits(2^32)); kind 2 quotient m/d of the requantization
+ * for 16 hashed m per d (bits(2^-60) <= u < bits(2)); kind 3 the hardware
+ * fp32->bf16 round-to-nearest-even of the GEMM epilogues against the
+ * bit-level rounding (any u); kind 4 the update's quotient n/d for 16 n per d
+ * (+-0 and |n| in [2^-90, 2^60]; bits(2^-60) <= u < bits(2^32)).
  * counts[i] = mismatches found by work-group i.  Test support: no
  * counterpart in the reference. */
 int msr_fastmath_check(int32_t kind, uint32_t bits_lo, uint32_t bits_hi, uint32_t *counts, int32_t n_counts,

@@ -1,6 +1,7 @@
 // 8-bit blockwise AdamW for gfx950 (muon_sr/triton_adamw_8bit.py:27-99): the fused
 // quantized step, the bf16-moment step of excluded tensors, the quantizer
 // diagnostics and the quantizer tables.
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -332,6 +333,11 @@ __global__ __launch_bounds__(F8_THREADS) MSR_F8_ATTR void adamw8bit_fast_kernel(
     const float b1 = vgpr(a.b1), omb1 = vgpr(c.one_m_b1), b2 = vgpr(a.b2), omb2 = vgpr(c.one_m_b2);
     const float step_c = vgpr(c.step_c), eps_c = vgpr(c.eps_c), decay = vgpr(c.decay);
     const uint32_t lo1 = vgpr(QF_LO1), scap = vgpr((uint32_t)QF_SCAP);
+    // div_upd(step_c * m, den) needs |step_c * m| = 0 or in [2^-90, 2^60]: nonzero |m| below
+    // tm = 2^-90 / |step_c| (tm1 = bits(tm) - 1) or |step_c| * max |m| >= 2^60 take the exact
+    // branch (den is in [2^-60, 2^32): eps_c is checked by the launcher, v' < 2^62 below)
+    const float step_abs = vgpr(fabsf(c.step_c));
+    const int32_t tm1 = (int32_t)vgpr(c.step_c != 0.0f ? __float_as_uint(0x1p-90f / fabsf(c.step_c)) - 1u : 0u);
     const char *pb = reinterpret_cast<const char *>(a.p), *gb = reinterpret_cast<const char *>(a.g);
     const char *mb = static_cast<const char *>(a.s1), *vb = static_cast<const char *>(a.s2);
     const uint32_t lane = threadIdx.x & 63u;
@@ -369,6 +375,7 @@ __global__ __launch_bounds__(F8_THREADS) MSR_F8_ATTR void adamw8bit_fast_kernel(
             // a sum of the 8 gradients is finite iff all of them are (or it overflows: exact)
             const float gsum = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
             float mx = 0.0f, vx = 0.0f;
+            uint32_t mnz = 0xffffffffu;   // min of 2 bits(|m|) - 2: (bits of the smallest nonzero |m|) - 1, times 2
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float mq = q1s[byte_of(raw.mc, j)] * raw.ms;            // :65
@@ -377,6 +384,7 @@ __global__ __launch_bounds__(F8_THREADS) MSR_F8_ATTR void adamw8bit_fast_kernel(
                 v[j] = b2 * vq + (omb2 * g[j]) * g[j];                        // :72
                 mx = fmaxf(mx, fabsf(m[j]));
                 vx = fmaxf(vx, v[j]);
+                mnz = min(mnz, (__float_as_uint(m[j]) << 1) - 2u);            // +-0 gives 0xfffffffe
             }
             const float ms = raw.ms, vs = raw.vs;
             halfwave_max2(mx, vx);                                            // :80-81
@@ -384,15 +392,18 @@ __global__ __launch_bounds__(F8_THREADS) MSR_F8_ATTR void adamw8bit_fast_kernel(
             const float vd = vx > 0.0f ? vx : 1.0f;                           // :83
             // Fast-branch conditions as sign bits of differences of non-negative bit patterns:
             // finite gradients and block scales, vs >= +0 (then m' is finite or +-inf and v' >= 0
-            // finite or +inf, never NaN, so the maxima above are exact), max v' < 2^62 and both
-            // divisors in [2^-60, 2).
+            // finite or +inf, never NaN, so the maxima above are exact), max v' < 2^62, both
+            // divisors in [2^-60, 2) and the update's numerators |step_c * m'| zero or in
+            // [2^-90, 2^60) (the block maximum of |m'| bounds them from above).
             const int32_t FMAX = 0x7f7fffff, DLO = 0x21800000, DHI = 0x3fffffff, VXHI = 0x5e7fffff;
+            const int32_t NHI = 0x5d7fffff;   // bits(2^60) - 1
             const int32_t gsb = (int32_t)(__float_as_uint(gsum) & 0x7fffffffu);
             const int32_t msb = (int32_t)(__float_as_uint(ms) & 0x7fffffffu);
             const int32_t vsb = (int32_t)__float_as_uint(vs), vxb = (int32_t)__float_as_uint(vx);
             const int32_t mdb = (int32_t)__float_as_uint(md), vdb = (int32_t)__float_as_uint(vd);
+            const int32_t nxb = (int32_t)__float_as_uint(step_abs * mx), mnb = (int32_t)(mnz >> 1);
             const int32_t neg = (FMAX - gsb) | (FMAX - msb) | vsb | (FMAX - vsb) | (VXHI - vxb) | (mdb - DLO) |
-                                (DHI - mdb) | (vdb - DLO) | (DHI - vdb);
+                                (DHI - mdb) | (vdb - DLO) | (DHI - vdb) | (NHI - nxb) | (mnb - tm1);
             if (__builtin_amdgcn_ballot_w64(neg < 0) != 0) {
                 if (lane == 0) deferred[ndef] = (uint32_t)pr;
                 if (++ndef == F8_DEFER) {
@@ -408,7 +419,7 @@ __global__ __launch_bounds__(F8_THREADS) MSR_F8_ATTR void adamw8bit_fast_kernel(
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float den = __builtin_fmaf(sqrt_rn_x2p32(v[j]), 0x1p-32f, eps_c);   // :74 sqrt(v) + eps
-                const float upd = (p[j] - (step_c * m[j]) / den) * decay;
+                const float upd = (p[j] - div_upd(step_c * m[j], den)) * decay;
                 w[j] = __float_as_uint(upd) + rp[j];                          // :75-78 (SR)
             }
             st_nt4(a.p + o0, u32x4_t{__builtin_amdgcn_perm(w[1], w[0], 0x07060302u), __builtin_amdgcn_perm(w[3], w[2], 0x07060302u),
@@ -546,6 +557,8 @@ __global__ __launch_bounds__(THREADS) void quant_table_check_kernel(const QuantT
 //   kind 2: div_rn(m, d, rcp_rn(d)) vs m/d    (d in [2^-60, 2), 16 hashed m per d with
 //           2^-63 d <= |m| <= d; for |m| < 2^-100 only the sign and zero-ness must agree)
 //   kind 3: rne_bf16x2 (hardware conversion) vs rne_bf16 (any u; both halves)
+//   kind 4: div_upd(n, d) vs n/d              (d in [2^-60, 2^32), 16 n per d: +-0 and
+//           15 hashed n with |n| in [2^-90, 2^60], spread over the quotient's range)
 __device__ __forceinline__ uint32_t mix32(uint32_t x) {
     x ^= x >> 16; x *= 0x7feb352du; x ^= x >> 15; x *= 0x846ca68bu; x ^= x >> 16;
     return x;
@@ -567,6 +580,15 @@ __global__ __launch_bounds__(THREADS) void fastmath_check_kernel(int kind, uint3
         } else if (kind == 3) {
             const float x2 = __uint_as_float(~u);
             bad += rne_bf16x2(x, x2) != pack2(rne_bf16(x), rne_bf16(x2));
+        } else if (kind == 4) {
+            for (uint32_t k = 0; k < 16; ++k) {
+                const uint32_t h = mix32(u * 16u + k);
+                // |n| = 2^t * (1 + f), t in [-90, 59]; k = 0 is a signed zero
+                const int t = (int)(h % 150u) - 90;
+                float n = k == 0 ? 0.0f : ldexpf(1.0f + (float)(mix32(h) >> 8) * 0x1p-24f, t);
+                if (h & 0x80000000u) n = -n;
+                bad += __float_as_uint(div_upd(n, x)) != __float_as_uint(n / x);
+            }
         } else {
             const float y = rcp_rn(x);
             for (uint32_t k = 0; k < 16; ++k) {
@@ -639,6 +661,10 @@ static void launch_quant(int mode, bool vec, const Adam8Args &a, hipStream_t s, 
 static int64_t launch_fast8(int mode, const Adam8Args &a, hipStream_t s, int64_t nfull) {
     const int64_t npairs = nfull / 2;
     if (npairs == 0 || npairs >= ((int64_t)1 << 31)) return 0;   // deferred pairs are recorded as int32
+    // the update's divisor sqrt(v') + eps_c must lie in [2^-60, 2^32) (sqrt(v') < 2^31 is
+    // checked per pair), and step_c must be finite: the same fp32 arithmetic as adam8_consts
+    const float sqrt_bc2 = sqrtf(a.bc2), eps_c = sqrt_bc2 * a.eps, step_c = (a.lr * sqrt_bc2) / a.bc1;
+    if (!(eps_c >= 0x1p-60f && eps_c <= 0x1p30f) || !std::isfinite(step_c)) return 0;
     const unsigned grid = grid_for(npairs, F8_THREADS / 64, MSR_F8_GRID_CAP);
     if (mode == NOISE_TRITON) hipLaunchKernelGGL((adamw8bit_fast_kernel<NOISE_TRITON>), dim3(grid), dim3(F8_THREADS), 0, s, a, npairs);
     else if (mode == NOISE_PHILOX8) hipLaunchKernelGGL((adamw8bit_fast_kernel<NOISE_PHILOX8>), dim3(grid), dim3(F8_THREADS), 0, s, a, npairs);
@@ -845,9 +871,11 @@ int msr_quant_table_check(const void *qtable, const float *qmap_signed, const fl
 int msr_fastmath_check(int32_t kind, uint32_t bits_lo, uint32_t bits_hi, uint32_t *counts, int32_t n_counts,
                        msr_stream_t stream) {
     const uint32_t SQRT_HI = 0x5e800000u, RCP_LO = 0x21800000u, RCP_HI = 0x3fffffffu;   // 2^62, 2^-60, 2 - ulp
+    const uint32_t UPD_HI = 0x4f7fffffu;                                                 // 2^32 - ulp
     const bool range_ok = kind == 0 ? bits_hi <= SQRT_HI
                         : kind == 3 ? true
-                                    : (kind == 1 || kind == 2) && bits_lo >= RCP_LO && bits_hi <= RCP_HI;
+                        : kind == 2 ? bits_lo >= RCP_LO && bits_hi <= RCP_HI
+                                    : (kind == 1 || kind == 4) && bits_lo >= RCP_LO && bits_hi <= UPD_HI;
     if (!counts || n_counts <= 0 || bits_hi < bits_lo || !range_ok) {
         set_error("msr_fastmath_check: bad arguments (kind %d, range %08x..%08x)", (int)kind, bits_lo, bits_hi);
         return MSR_ERR_ARG;

@@ -343,7 +343,7 @@ __device__ __forceinline__ float sqrt_rn_x2p32(float v) {
 }
 __device__ __forceinline__ float sqrt_rn(float v) { return sqrt_rn_x2p32(v) * 0x1p-32f; }
 
-// RN(1/d) for d in [2^-60, 2): v_rcp_f32 and one Newton step.
+// RN(1/d) for d in [2^-60, 2^32): v_rcp_f32 and one Newton step.
 __device__ __forceinline__ float rcp_rn(float d) {
     const float r0 = __builtin_amdgcn_rcpf(d);
     const float e = __builtin_fmaf(-d, r0, 1.0f);
@@ -360,6 +360,20 @@ __device__ __forceinline__ float div_rn(float m, float d, float y) {
     const float q0 = m * y;
     const float r = __builtin_fmaf(-q0, d, m);
     return __builtin_fmaf(r, y, q0);
+}
+
+// RN(n/d) for the update's quotient, for d in [2^-60, 2^32) and n = +-0 or
+// |n| in [2^-90, 2^60] (so the quotient is a normal number or zero).  With
+// y = RN(1/d) and q0 = RN(n*y) within an ulp of n/d, the negated remainder
+// d*q0 - n is exact (|n| >= 2^-90 keeps it out of the subnormal range) and
+// RN(q0 - (d*q0 - n)*y) is the rounded quotient (Markstein's theorem).  The
+// negated form also gives the IEEE sign of a zero quotient: for n = -0 it is
+// -0 (the plain remainder n - d*q0 = +0 would turn it into +0).
+__device__ __forceinline__ float div_upd(float n, float d) {
+    const float y = rcp_rn(d);
+    const float q0 = n * y;
+    const float rn = __builtin_fmaf(d, q0, -n);
+    return __builtin_fmaf(-rn, y, q0);
 }
 
 // Signed code of x = RN(m/d) for the fast kernel (x != -0, |x| <= 1), as the

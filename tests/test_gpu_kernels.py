@@ -334,19 +334,24 @@ def test_quant_table_exhaustive(L):
 
 SQRT_HI = 0x5E800000                     # bits(2^62)
 RCP_LO, RCP_HI = 0x21800000, 0x3FFFFFFF  # bits(2^-60), bits(2) - 1
+UPD_HI = 0x4F7FFFFF                      # bits(2^32) - 1
 
 
 @pytest.mark.parametrize("kind,lo,hi", [
     (0, 0, SQRT_HI),                       # sqrt: every float in [0, 2^62]
-    (1, RCP_LO, RCP_HI),                   # reciprocal: every float in [2^-60, 2)
+    (1, RCP_LO, UPD_HI),                   # reciprocal: every float in [2^-60, 2^32)
     (2, 0x3F800000, RCP_HI),               # quotient: every d in [1, 2), 16 m each
     (2, RCP_LO, RCP_LO + (1 << 23) - 1),   # ... every d in [2^-60, 2^-59)
     (2, 0x30000000, 0x307FFFFF),           # ... every d in [2^-31, 2^-30)
     (3, 0, 0xFFFFFFFF),                    # hardware bf16 rounding: every fp32 bit pattern
+    (4, 0x3F800000, RCP_HI),               # update quotient: every d in [1, 2), 16 n each
+    (4, RCP_LO, RCP_LO + (1 << 23) - 1),   # ... every d in [2^-60, 2^-59)
+    (4, 0x4F000000, UPD_HI),               # ... every d in [2^31, 2^32)
+    (4, 0x30000000, 0x307FFFFF),           # ... every d in [2^-31, 2^-30)
 ])
 def test_fastmath_exhaustive(L, kind, lo, hi):
-    """The fast 8-bit kernel's sqrt, reciprocal and quotient equal the IEEE operations
-    on their whole input ranges (the quotient on a hashed sample of numerators), and
+    """The fast 8-bit kernel's sqrt, reciprocal and quotients equal the IEEE operations
+    on their whole input ranges (the quotients on hashed samples of numerators), and
     the hardware fp32->bf16 conversion of the GEMM epilogues equals the bit-level
     round-to-nearest-even on every fp32 bit pattern."""
     nblk = 4096
@@ -370,10 +375,14 @@ def test_adamw8bit_fast_kernel_vs_oracle(L, mode):
     p0 = rng_bf16(rng, n, 0.02)
     s1, s2 = np.full(n, 127, np.uint8), np.zeros(n, np.uint8)
     a1, a2 = np.zeros(nb, np.float32), np.zeros(nb, np.float32)
+    pair = lambda i: slice(512 * i, 512 * (i + 1))  # noqa: E731
+    # pair 25: negative codes with zero block scales dequantize to -0, so -0 gradients give
+    # m' = -0 and the update's numerator -0 against parameters -0 (fast branch)
+    s1[pair(25)] = 0
+    p0[512 * 25:512 * 25 + 8] = 0x8000
     pd, s1d, s2d, a1d, a2d = u16_to_dev(p0), np_to_dev(s1), np_to_dev(s2), np_to_dev(a1), np_to_dev(a2)
     pe = p0
     lr, b1, b2, eps, wd = 3e-4, 0.9, 0.95, 1e-10, 0.01
-    pair = lambda i: slice(512 * i, 512 * (i + 1))  # noqa: E731
     for step in range(1, 5):
         g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
         if step == 1:
@@ -381,6 +390,8 @@ def test_adamw8bit_fast_kernel_vs_oracle(L, mode):
             g[pair(7)] *= 3e21                  # v' above 2^62: exact branch
             g[pair(11)] *= 1e-22                # block scales below 2^-60: exact branch
             g[pair(13)] = 0.0                   # all-zero pair: fast branch, divisor 1
+            g[pair(21)][9] = 1e-33              # one update numerator below 2^-90: exact branch
+            g[pair(25)][:8] = -0.0
         if step == 2:
             g[pair(5)][7] = -np.inf
             g[pair(17)][:256] *= 1e-30          # one tiny block next to a normal one

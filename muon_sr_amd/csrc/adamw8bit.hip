@@ -207,15 +207,16 @@ __global__ __launch_bounds__((BLOCK / 8 > THREADS) ? BLOCK / 8 : THREADS) void a
 // and walks the tensor in a grid-stride loop, fetching its next pair while it
 // computes the current one.  Per pair the wave first forms the new moments and
 // the two block maxima, then takes one of two branches, uniformly:
-//  * fast: every gradient finite, max v' < 2^62 and both block divisors in
-//    [2^-60, 2).  The update uses sqrt_rn, the requantization quotients use
-//    rcp_rn/div_rn and the codes come from the flat table; all of these equal
-//    the IEEE operations on these ranges (see common.hpp);
+//  * fast: every gradient finite, max v' < 2^62, both block divisors in
+//    [2^-60, 2) and every update numerator |step_c * m'| zero or in
+//    [2^-90, 2^60).  The update uses sqrt_rn and div_upd, the requantization
+//    quotients use rcp_rn/div_rn and the codes come from the flat table; all of
+//    these equal the IEEE operations on these ranges (see common.hpp);
 //  * exact: anything else (non-finite gradients, extreme moments) goes through
 //    the reference arithmetic with IEEE sqrt/division, the double-precision
 //    quotients and the reference search, as in adamw8bit_quant_kernel.
 // Both branches produce the reference's bits; the fast one with about half
-// the VALU work, which bounds this kernel on gfx950.
+// the VALU work.
 // ---------------------------------------------------------------------------
 
 #ifndef MSR_F8_WAVES

@@ -415,6 +415,39 @@ def test_adamw8bit_fast_kernel_vs_oracle(L, mode):
         assert np.array_equal(a2d.cpu().numpy().view(np.uint32), a2.view(np.uint32)), step
 
 
+def test_adamw8bit_eps_zero_takes_general_kernel(L):
+    """eps = 0 puts the update's divisor outside the fast kernel's range (sqrt(v') + eps
+    may be 0 or tiny), so the launcher runs the general kernel on a tensor the fast one
+    would otherwise take: still bit-exact against the oracle, zero-gradient elements
+    (0/0 in the update) included."""
+    rng = np.random.default_rng(23)
+    block, n = 256, (1 << 16) + 512
+    nb = n // block
+    Q1, Q2 = O.create_dynamic_map(True), O.create_dynamic_map(False)
+    q1, q2, qt = np_to_dev(Q1), np_to_dev(Q2), qtable_dev(L)
+    p0 = rng_bf16(rng, n, 0.02)
+    s1, s2 = np.full(n, 127, np.uint8), np.zeros(n, np.uint8)
+    a1, a2 = np.zeros(nb, np.float32), np.zeros(nb, np.float32)
+    pd, s1d, s2d, a1d, a2d = u16_to_dev(p0), np_to_dev(s1), np_to_dev(s2), np_to_dev(a1), np_to_dev(a2)
+    pe = p0
+    for step in (1, 2):
+        g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+        g[1000:1100] = 0.0
+        g0 = O.f32_to_bf16_rne(g)
+        hyper = (3e-4, 0.9, 0.95, 0.0, 0.01, 1 - 0.9 ** step, 1 - 0.95 ** step)
+        seed = 77 + step
+        pe, s1, s2, a1, a2 = O.adamw8bit(pe, g0, s1, s2, a1, a2, Q1, Q2, block, True, *hyper,
+                                         O.NoiseSpec(O.NOISE_PHILOX8, seed))
+        _adam8_call(L, pd, u16_to_dev(g0), s1d, s2d, a1d, a2d, q1, q2, n, block, True, hyper, seed,
+                    O.NOISE_PHILOX8, None, qt=qt)
+        got = dev_to_u16(pd)
+        same = (got == pe) | (np.isnan(O.bf16_to_f32(got)) & np.isnan(O.bf16_to_f32(pe)))
+        assert same.all(), (step, np.flatnonzero(~same)[:10])
+        assert np.array_equal(s1d.cpu().numpy(), s1) and np.array_equal(s2d.cpu().numpy(), s2), step
+        assert np.array_equal(a1d.cpu().numpy().view(np.uint32), a1.view(np.uint32)), step
+        assert np.array_equal(a2d.cpu().numpy().view(np.uint32), a2.view(np.uint32)), step
+
+
 def test_adamw8bit_extreme_moments(L):
     """Huge gradients (v overflows to inf), denormal-scale moments and -0: the
     exact-quotient and table paths against the oracle."""

@@ -415,11 +415,15 @@ def test_adamw8bit_fast_kernel_vs_oracle(L, mode):
         assert np.array_equal(a2d.cpu().numpy().view(np.uint32), a2.view(np.uint32)), step
 
 
-def test_adamw8bit_eps_zero_takes_general_kernel(L):
+@pytest.mark.parametrize("lr,eps", [(3e-4, 0.0), (1e21, 1e-10), (1.6e21, 1e-10), (3e21, 1e-10)])
+def test_adamw8bit_launch_and_branch_conditions(L, lr, eps):
     """eps = 0 puts the update's divisor outside the fast kernel's range (sqrt(v') + eps
     may be 0 or tiny), so the launcher runs the general kernel on a tensor the fast one
-    would otherwise take: still bit-exact against the oracle, zero-gradient elements
-    (0/0 in the update) included."""
+    would otherwise take (zero-gradient elements give 0/0 in the update).  Learning rates
+    of 1e21 to 3e21 put the update's numerators step_c * m' around 2^60, where the fast
+    kernel's waves send the pairs above it to the exact branch (none of the first step's
+    blocks at 1e21, 58 of 258 at 1.6e21, all at 3e21).  Bit-exact against the oracle in
+    every case."""
     rng = np.random.default_rng(23)
     block, n = 256, (1 << 16) + 512
     nb = n // block
@@ -434,7 +438,7 @@ def test_adamw8bit_eps_zero_takes_general_kernel(L):
         g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
         g[1000:1100] = 0.0
         g0 = O.f32_to_bf16_rne(g)
-        hyper = (3e-4, 0.9, 0.95, 0.0, 0.01, 1 - 0.9 ** step, 1 - 0.95 ** step)
+        hyper = (lr, 0.9, 0.95, eps, 0.01, 1 - 0.9 ** step, 1 - 0.95 ** step)
         seed = 77 + step
         pe, s1, s2, a1, a2 = O.adamw8bit(pe, g0, s1, s2, a1, a2, Q1, Q2, block, True, *hyper,
                                          O.NoiseSpec(O.NOISE_PHILOX8, seed))

@@ -65,6 +65,11 @@ struct GemmArgs {
     int sracc;         // 0, or 1 + the noise mode of the SR-accumulating store (D = acc)
     int zero_init;     // SR-accumulating store: acc reads as zero
     Noise ns;          // SR-accumulating store: noise of element offset m * ldd + n
+    // Newton-Schulz epilogues (EPI_* below)
+    const float *alpha_b;   // per-matrix alpha (replaces alpha when not null)
+    float *resid;           // EPI_A, EPI_B: fp32 rounding residual of each diagonal element, [batch][sv]
+    const float *rvec;      // EPI_B: residuals of A's diagonal; EPI_X: residuals of B''s diagonal, [batch][sv]
+    int64_t sv;             // batch stride of resid and rvec
 };
 
 // Work-group -> (matrix, tile).  Consecutive work-group ids are dispatched
@@ -167,9 +172,25 @@ __device__ __forceinline__ uint16_t *stg_row(int r) {
 //              row-major activations)
 enum : int { GM_RR = 0, GM_RK = 1, GM_TRI_P = 2, GM_TRI_PQ = 3, GM_KK = 4 };
 
+// Epilogues of the Newton-Schulz products.  The iteration keeps A, B' and X
+// in bf16 between products; the diagonals of A and B' are the largest
+// entries of those matrices (B' carries a = 3.4445 on it), so their bf16
+// rounding is the largest rounding error of the iteration.  These epilogues
+// carry the rounding residual of every diagonal element in fp32 to the next
+// product:
+//   EPI_A  A = alpha X X^T:  rho[m] = A_mm - bf16(A_mm)                 (resid)
+//   EPI_B  B' = alpha (A A) + beta A + diag I with the diagonal corrected
+//          for rho to first order, B'_mm += rho[m] (beta + 2 alpha A_mm)
+//          (d/dA_mm of beta A_mm + alpha (A A)_mm with A_mm dominant):
+//          r[m] = B'_mm - bf16(B'_mm)                                   (resid)
+//   EPI_X  X' = alpha (B' X + bf16(r[m]) X), the second term as MFMAs of the diagonal
+//          block (see mmdiag)
+// EPI_NONE is the plain alpha P Q^T + beta C + diag I of the diagnostic GEMMs.
+enum : int { EPI_NONE = 0, EPI_A = 1, EPI_B = 2, EPI_X = 3 };
+
 // SRACC >= 0: D is a bf16 accumulator and the store adds to it with stochastic
 // rounding (noise mode SRACC), as msr_sr_accum does with the RNE bf16 product.
-template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, int GM, int SRACC = -1>
+template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, int GM, int SRACC = -1, int EPI = EPI_NONE>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     int ti, tj;
     int64_t bz;
@@ -293,6 +314,40 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
             for (int ni = 0; ni < 2; ++ni)
                 acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], fa[b][mi], acc[mi][ni], 0, 0, 0);
     };
+    // EPI_X: the term r[m] X[m][n] of X' = B' X + r X enters the accumulators as the product
+    // of X with the diagonal matrix bf16(r), over the K block k in [m0, m0 + 256) that holds
+    // the tile's own rows of X (the first 4 slabs of the RK range).  Wave (wm, wn) owns rows
+    // 128 wm .. 128 wm + 127 of the tile, which are slabs 2 wm and 2 wm + 1 of that block: in
+    // slab 2 wm + st, substep ks, the diagonal crosses the 32-row block mi = 2 st + ks / 2,
+    // and lane l's fragment (row r32, k = 8 khalf + e) holds it at e = r32 - 16 (ks & 1) -
+    // 8 khalf.  That is 16 extra MFMAs per wave and no extra memory traffic.
+    uint32_t rb16[4] = {0u, 0u, 0u, 0u};   // bf16(r) at rows 128 wm + 32 mi + r32
+    if constexpr (EPI == EPI_X) {
+        const float *rv = a.rvec + bz * a.sv + m0 + wm * 128 + r32;
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) rb16[mi] = rne_bf16(rv[32 * mi]);
+    }
+    auto mmdiag = [&](int b, auto ST, auto KS) {
+        constexpr int ks = decltype(KS)::value;
+        constexpr int mi = 2 * decltype(ST)::value + (ks >> 1);
+        const int e = r32 - 16 * (ks & 1) - 8 * khalf;
+        const uint32_t v = (unsigned)e < 8u ? rb16[mi] << (16 * (e & 1)) : 0u;
+        const int w = e >> 1;
+        const u32x4_t words = {w == 0 ? v : 0u, w == 1 ? v : 0u, w == 2 ? v : 0u, w == 3 ? v : 0u};
+        const bf16x8_t rf = __builtin_bit_cast(bf16x8_t, words);
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], rf, acc[mi][ni], 0, 0, 0);
+    };
+    // dg: this wave's rows meet the slab pair of the diagonal block being computed
+    auto diag = [&](auto DG, bool dg, int b, int stage, auto KS) {
+        if constexpr (decltype(DG)::value) {
+            if (dg) {
+                if (stage == 0) mmdiag(b, std::integral_constant<int, 0>{}, KS);
+                else mmdiag(b, std::integral_constant<int, 1>{}, KS);
+            }
+        }
+    };
     // Each substep is one scheduling region: its 8 MFMAs interleaved with the
     // fragment reads of the next substep (6 row-major, 8 or 12 with K-major
     // operands: 4 reads per row-major P, 8 per K-major P, 2 or 4 for Q).
@@ -322,25 +377,33 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     // (measured +3..19% over spreading the loads across the substeps).  The
     // last substep's MFMAs overlap the next slab's first fragment reads, in
     // this slab's layouts; after the last slab of a K range these are unused.
-    auto slab = [&](auto PK, auto QK, int stage, int knext, bool pkn, bool qkn) {
+    using K0_ = std::integral_constant<int, 0>;
+    using K1_ = std::integral_constant<int, 1>;
+    using K2_ = std::integral_constant<int, 2>;
+    using K3_ = std::integral_constant<int, 3>;
+    auto slab = [&](auto PK, auto QK, int stage, int knext, bool pkn, bool qkn, auto DG, bool dg) {
         dma(pkn, qkn, stage ^ 1, knext);
         __builtin_amdgcn_sched_barrier(0);
         frags(PK, QK, stage, 1, fa[1], fb[1]);
         mm(0);
+        diag(DG, dg, 0, stage, K0_{});
         pattern(PK, QK);
         __builtin_amdgcn_sched_barrier(0);
         frags(PK, QK, stage, 2, fa[0], fb[0]);
         mm(1);
+        diag(DG, dg, 1, stage, K1_{});
         pattern(PK, QK);
         __builtin_amdgcn_sched_barrier(0);
         frags(PK, QK, stage, 3, fa[1], fb[1]);
         mm(0);
+        diag(DG, dg, 0, stage, K2_{});
         pattern(PK, QK);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(0);   // own loads of the next slab landed, own reads of this stage done
         __syncthreads();                 // everyone's
         frags(PK, QK, stage ^ 1, 0, fa[0], fb[0]);
         mm(1);
+        diag(DG, dg, 1, stage, K3_{});
         pattern(PK, QK);
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -355,7 +418,9 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     // of a range loads the first slab of the next one (selected, not
     // branched), or itself again at the end of K.
     const int KT = a.K / BK, ktP = kP / BK, ktQ = kQ / BK;
-    auto range = [&](auto PK, auto QK, int kt0, int kt1) {
+    // DG: the range is the diagonal block [m0, m0 + 256) of X' = B' X + r X (EPI_X), whose
+    // slab pair (kt - kt0) / 2 holds the rows of waves with wm = (kt - kt0) / 2.
+    auto range = [&](auto PK, auto QK, int kt0, int kt1, auto DG) {
         const bool end = kt1 >= KT;
         const int kafter = end ? (kt1 - 1) * BK : kt1 * BK;
         const bool pka = end ? decltype(PK)::value : kt1 < ktP, qka = end ? decltype(QK)::value : kt1 < ktQ;
@@ -363,22 +428,26 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
 #pragma clang loop unroll(disable)
         for (int kt = kt0; kt < kt1; kt += 2) {
             const bool more = kt + 2 < kt1;
-            slab(PK, QK, 0, (kt + 1) * BK, PK, QK);
+            const bool dg = decltype(DG)::value && ((kt - kt0) >> 1) == wm;
+            slab(PK, QK, 0, (kt + 1) * BK, PK, QK, DG, dg);
             slab(PK, QK, 1, more ? (kt + 2) * BK : kafter, more ? decltype(PK)::value : pka,
-                 more ? decltype(QK)::value : qka);
+                 more ? decltype(QK)::value : qka, DG, dg);
         }
     };
     dma(0 < ktP, 0 < ktQ, 0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if constexpr (HAS_KK) {
-        if (0 < ktP) range(T_{}, T_{}, 0, ktP);
+        if (0 < ktP) range(T_{}, T_{}, 0, ktP, F_{});
     }
-    if constexpr (HAS_RK) {
-        if (ktP < ktQ) range(F_{}, T_{}, ktP, ktQ);
+    if constexpr (EPI == EPI_X) {   // GM_TRI_P: the RK range starts at k = m0 (ktP + 4 <= ktQ)
+        range(F_{}, T_{}, ktP, ktP + 4, T_{});
+        if (ktP + 4 < ktQ) range(F_{}, T_{}, ktP + 4, ktQ, F_{});
+    } else if constexpr (HAS_RK) {
+        if (ktP < ktQ) range(F_{}, T_{}, ktP, ktQ, F_{});
     }
     if constexpr (HAS_RR) {
-        if (ktQ < KT) range(F_{}, F_{}, ktQ, KT);
+        if (ktQ < KT) range(F_{}, F_{}, ktQ, KT, F_{});
     }
 
     // ---------------- epilogue ----------------
@@ -403,6 +472,18 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     // (alpha * acc (+ beta * C)) (+ diag where m == n), rounded to bf16 by the
     // hardware conversion; the multiply is skipped for alpha == 1 (x * 1 == x
     // for every non-NaN x) and the diagonal term outside diagonal tiles.
+    // The Newton-Schulz epilogues (EPI_*) are described at their enum.
+    const float alpha = a.alpha_b ? a.alpha_b[bz] : a.alpha;
+    float rowv[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // EPI_B: rho at rows m0 + wm 128 + 32 mi + r32
+    if constexpr (EPI == EPI_B) {
+        const float *rv = a.rvec + bz * a.sv + m0 + wm * 128 + r32;
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) rowv[mi] = rv[32 * mi];
+    }
+    // Diagonal tiles: the lane's diagonal elements, at most one per 32-row block mi, and
+    // their fp32 rounding residuals (selects in the unrolled loop, stores after it).
+    float res[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    bool has_res[4] = {false, false, false, false};
     auto stage_out = [&](auto scaled, auto dg) {
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
@@ -413,37 +494,58 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
                     const int ml = wm * 128 + mi * 32 + r32;
                     const int nl = wn * 64 + ni * 32 + 8 * r + 4 * khalf;
                     uint2 *sp = reinterpret_cast<uint2 *>(stg_row(ml) + nl);
-                    float v0 = acc[mi][ni][4 * r], v1 = acc[mi][ni][4 * r + 1];
-                    float v2 = acc[mi][ni][4 * r + 2], v3 = acc[mi][ni][4 * r + 3];
+                    float v[4] = {acc[mi][ni][4 * r], acc[mi][ni][4 * r + 1], acc[mi][ni][4 * r + 2],
+                                  acc[mi][ni][4 * r + 3]};
+                    float cv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
                     if constexpr (decltype(scaled)::value) {
-                        v0 = a.alpha * v0;
-                        v1 = a.alpha * v1;
-                        v2 = a.alpha * v2;
-                        v3 = a.alpha * v3;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) v[q] = alpha * v[q];
                     }
                     if constexpr (HAS_C) {
                         const uint2 cw = *sp;
-                        v0 = v0 + a.beta * bf16_lo(cw.x);
-                        v1 = v1 + a.beta * bf16_hi(cw.x);
-                        v2 = v2 + a.beta * bf16_lo(cw.y);
-                        v3 = v3 + a.beta * bf16_hi(cw.y);
+                        cv[0] = bf16_lo(cw.x);
+                        cv[1] = bf16_hi(cw.x);
+                        cv[2] = bf16_lo(cw.y);
+                        cv[3] = bf16_hi(cw.y);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) v[q] = v[q] + a.beta * cv[q];
                     }
                     if constexpr (decltype(dg)::value) {   // m0 == n0 here
-                        v0 = ml == nl ? v0 + a.diag : v0;
-                        v1 = ml == nl + 1 ? v1 + a.diag : v1;
-                        v2 = ml == nl + 2 ? v2 + a.diag : v2;
-                        v3 = ml == nl + 3 ? v3 + a.diag : v3;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const bool on = ml == nl + q;
+                            if constexpr (EPI == EPI_B)
+                                v[q] = on ? v[q] + (a.diag + rowv[mi] * (a.beta + 2.0f * alpha * cv[q])) : v[q];
+                            else if constexpr (EPI != EPI_A)
+                                v[q] = on ? v[q] + a.diag : v[q];
+                        }
                     }
-                    *sp = make_uint2(rne_bf16x2(v0, v1), rne_bf16x2(v2, v3));
+                    const uint2 w = make_uint2(rne_bf16x2(v[0], v[1]), rne_bf16x2(v[2], v[3]));
+                    *sp = w;
+                    if constexpr (decltype(dg)::value && (EPI == EPI_A || EPI == EPI_B)) {
+                        const float rq[4] = {bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)};
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const bool on = ml == nl + q;
+                            res[mi] = on ? v[q] - rq[q] : res[mi];
+                            has_res[mi] = has_res[mi] || on;
+                        }
+                    }
                 }
             }
         }
     };
-    if (ti == tj && a.diag != 0.0f) {
-        if (a.alpha == 1.0f) stage_out(std::false_type{}, std::true_type{});
+    if (ti == tj && (a.diag != 0.0f || EPI == EPI_A || EPI == EPI_B)) {
+        if (alpha == 1.0f) stage_out(std::false_type{}, std::true_type{});
         else stage_out(std::true_type{}, std::true_type{});
+        if constexpr (EPI == EPI_A || EPI == EPI_B) {
+            float *resid = a.resid + bz * a.sv + m0 + wm * 128 + r32;
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+                if (has_res[mi]) resid[32 * mi] = res[mi];
+        }
     } else {
-        if (a.alpha == 1.0f) stage_out(std::false_type{}, std::false_type{});
+        if (alpha == 1.0f) stage_out(std::false_type{}, std::false_type{});
         else stage_out(std::true_type{}, std::false_type{});
     }
     __syncthreads();
@@ -566,28 +668,68 @@ __global__ __launch_bounds__(NORM_THREADS) void sumsq_kernel(const uint16_t *in,
     if (threadIdx.x == 0) partial[b * NPART + blockIdx.x] = red[0];
 }
 
-// d = bf16(bf16(||u||_F) + 1e-7) from the partial sums of matrix b (fixed order).
-__device__ __forceinline__ float norm_divisor(const float *partial, int64_t b) {
+__device__ __forceinline__ float sumsq_of(const float *partial, int64_t b) {
     float s = 0.0f;
     for (int i = 0; i < NPART; ++i) s = s + partial[b * NPART + i];
-    const float nrm = __uint_as_float(rne_bf16(sqrtf(s)) << 16);
+    return s;
+}
+
+// d = bf16(bf16(||u||_F) + 1e-7) from the partial sums of matrix b (fixed order):
+// the reference's bf16 normalisation (muon_sr/muon_sr.py:93), used for steps = 0.
+__device__ __forceinline__ float norm_divisor(const float *partial, int64_t b) {
+    const float nrm = __uint_as_float(rne_bf16(sqrtf(sumsq_of(partial, b))) << 16);
     return __uint_as_float(rne_bf16(nrm + 1e-7f) << 16);
+}
+
+// The iteration's input without a rounding: X0 = u / (||u||_F + 1e-7) is kept
+// as x0 = u 2^-e (exact in bf16: a power-of-two scale, e = the exponent of
+// ||u||_F, so ||x0||_F is in [0.5, 1)) and the factor s0 = 2^e / (||u||_F +
+// 1e-7) goes into the first products: A = s0^2 x0 x0^T, X' = s0 (B' x0 + ...).
+// ||u||_F is the fp32 square root of the fp32 sum of squares.  A sum that
+// overflows (||u|| >= 2^64) takes e = 127 and s0 = 0 (u / inf = 0, as the
+// reference's normalisation gives); NaN propagates.
+__device__ __forceinline__ void prescale_of(const float *partial, int64_t b, int &e, float &s0) {
+    const float d = sqrtf(sumsq_of(partial, b));
+    if (d == __builtin_huge_valf()) {
+        e = 127;
+        s0 = 0.0f;
+        return;
+    }
+    e = 0;
+    if (d == d) (void)frexpf(d, &e);
+    s0 = ldexpf(1.0f / (d + 1e-7f), e);
 }
 
 // Vector form of normalize_kernel (below) for cols % 8 == 0 with 16-byte aligned
 // `in`, S and T rows: each thread moves 8 consecutive bf16 (16 bytes) per access.
 // Rp and Cp are multiples of 8 here, so an 8-wide chunk is entirely inside or
 // entirely outside every extent it is checked against.
+// PRESCALE: x0 = u 2^-e (see prescale_of), and block (0, 0) of matrix b writes
+// alphas[b] = s0^2 and alphas[batch + b] = s0; else x0 = bf16(u / d).
+template <bool PRESCALE>
 __global__ __launch_bounds__(256) void normalize_vec_kernel(const uint16_t *in, int64_t rows, int64_t cols,
                                                             const float *partial, uint16_t *S, int64_t ldS,
                                                             int64_t sS, uint16_t *T, int64_t ldT, int64_t sT,
-                                                            int64_t Rp, int64_t Cp) {
+                                                            int64_t Rp, int64_t Cp, float *alphas) {
     __shared__ __align__(16) uint16_t tile[64][72];
     __shared__ float dsh;
+    __shared__ int esh;
     const int64_t b = blockIdx.z;
-    if (threadIdx.x == 0) dsh = norm_divisor(partial, b);
+    if (threadIdx.x == 0) {
+        if constexpr (PRESCALE) {
+            float s0;
+            prescale_of(partial, b, esh, s0);
+            if (blockIdx.x == 0 && blockIdx.y == 0) {
+                alphas[b] = s0 * s0;
+                alphas[gridDim.z + b] = s0;
+            }
+        } else {
+            dsh = norm_divisor(partial, b);
+        }
+    }
     __syncthreads();
-    const float d = dsh;
+    const float d = PRESCALE ? 1.0f : dsh;
+    const int ne = PRESCALE ? -esh : 0;
     const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
     const uint16_t *x = in + b * rows * cols;
     const int j = threadIdx.x & 7, i0 = threadIdx.x >> 3;
@@ -602,7 +744,9 @@ __global__ __launch_bounds__(256) void normalize_vec_kernel(const uint16_t *in, 
             uint32_t o[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                o[k] = rne_bf16x2(__uint_as_float(u[k] << 16) / d, __uint_as_float(u[k] & 0xffff0000u) / d);
+                const float lo = __uint_as_float(u[k] << 16), hi = __uint_as_float(u[k] & 0xffff0000u);
+                if constexpr (PRESCALE) o[k] = rne_bf16x2(ldexpf(lo, ne), ldexpf(hi, ne));
+                else o[k] = rne_bf16x2(lo / d, hi / d);
             }
             w = make_uint4(o[0], o[1], o[2], o[3]);
         }
@@ -626,25 +770,43 @@ __global__ __launch_bounds__(256) void normalize_vec_kernel(const uint16_t *in, 
 }
 
 // Writes S = x0 in the input layout (Rp x Cp, ld ldS) and T = x0^T (Cp x Rp, ld ldT),
-// x0 = bf16(u / d), d = bf16(bf16(||u||_F) + 1e-7), zeros outside rows x cols.
-// S or T may be null.  64 x 64 tiles, transposed through LDS.
+// x0 = bf16(u / d), d = bf16(bf16(||u||_F) + 1e-7), or with PRESCALE x0 = u 2^-e
+// and the first products' alphas (as normalize_vec_kernel); zeros outside rows x
+// cols.  S or T may be null.  64 x 64 tiles, transposed through LDS.
+template <bool PRESCALE>
 __global__ __launch_bounds__(256) void normalize_kernel(const uint16_t *in, int64_t rows, int64_t cols,
                                                         const float *partial, uint16_t *S, int64_t ldS, int64_t sS,
                                                         uint16_t *T, int64_t ldT, int64_t sT, int64_t Rp,
-                                                        int64_t Cp) {
+                                                        int64_t Cp, float *alphas) {
     __shared__ uint16_t tile[64][66];
     __shared__ float dsh;
+    __shared__ int esh;
     const int64_t b = blockIdx.z;
-    if (threadIdx.x == 0) dsh = norm_divisor(partial, b);
+    if (threadIdx.x == 0) {
+        if constexpr (PRESCALE) {
+            float s0;
+            prescale_of(partial, b, esh, s0);
+            if (blockIdx.x == 0 && blockIdx.y == 0) {
+                alphas[b] = s0 * s0;
+                alphas[gridDim.z + b] = s0;
+            }
+        } else {
+            dsh = norm_divisor(partial, b);
+        }
+    }
     __syncthreads();
-    const float d = dsh;
+    const float d = PRESCALE ? 1.0f : dsh;
+    const int ne = PRESCALE ? -esh : 0;
     const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
     const uint16_t *x = in + b * rows * cols;
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     for (int i = ty; i < 64; i += 4) {
         const int64_t r = r0 + i, c = c0 + tx;
         uint16_t h = 0;
-        if (r < rows && c < cols) h = (uint16_t)rne_bf16(bf16_to_f32(x[r * cols + c]) / d);
+        if (r < rows && c < cols) {
+            const float v = bf16_to_f32(x[r * cols + c]);
+            h = (uint16_t)rne_bf16(PRESCALE ? ldexpf(v, ne) : v / d);
+        }
         tile[i][tx] = h;
         if (S && r < Rp && c < Cp) S[b * sS + r * ldS + c] = h;
     }
@@ -662,7 +824,7 @@ static inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * 
 struct NSLayout {
     int64_t m, n, mp, np;
     bool transposed;
-    size_t off_x[2], off_a, off_b, off_part, total;
+    size_t off_x[2], off_a, off_b, off_part, off_alpha, off_rho, off_r, total;
 };
 
 static NSLayout ns_layout(int64_t batch, int64_t rows, int64_t cols) {
@@ -681,6 +843,9 @@ static NSLayout ns_layout(int64_t batch, int64_t rows, int64_t cols) {
     L.off_a = take(as);
     L.off_b = take(as);
     L.off_part = take((size_t)batch * NPART * 4);
+    L.off_alpha = take((size_t)batch * 2 * 4);     // alphas of the first A and X' products
+    L.off_rho = take((size_t)batch * L.mp * 4);    // residuals of A's diagonal
+    L.off_r = take((size_t)batch * L.mp * 4);      // residuals of B''s diagonal
     L.total = o;
     return L;
 }
@@ -718,13 +883,14 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
         if (ab.sracc > 0) {   // weight gradient accumulated into D with SR
             if (gm != GM_KK || ab.symmetric || c || !d || dt) { set_error("gemm: unsupported SR-accumulating product"); return (int)MSR_ERR_ARG; }
             MSR_DISPATCH_NOISE(ab.sracc - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_KK, M>), grid, block, 0, s, ab));
-        } else if (ab.symmetric) {   // A = X X^T (RR), B = c A A + b A (TRI_PQ)
-            if (gm == GM_RR && !c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false, GM_RR>), grid, block, 0, s, ab);
-            else if (gm == GM_TRI_PQ && c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false, GM_TRI_PQ>), grid, block, 0, s, ab);
+        } else if (ab.symmetric) {   // A = X X^T (RR), B' = c A A + b A + a I (TRI_PQ)
+            if (gm == GM_RR && !c && d && !dt && ab.resid) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false, GM_RR, -1, EPI_A>), grid, block, 0, s, ab);
+            else if (gm == GM_TRI_PQ && c && d && !dt && ab.resid && ab.rvec) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false, GM_TRI_PQ, -1, EPI_B>), grid, block, 0, s, ab);
             else { set_error("gemm: unsupported symmetric product"); return (int)MSR_ERR_ARG; }
-        } else if (gm == GM_TRI_P) {   // X' = B' X: D = X', or DT = X'^T for the tall output
-            if (!c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P>), grid, block, 0, s, ab);
-            else if (!c && !d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, false, true, GM_TRI_P>), grid, block, 0, s, ab);
+        } else if (gm == GM_TRI_P) {   // X' = B' X + r X: D = X', or DT = X'^T for the tall output
+            if (!ab.rvec) { set_error("gemm: X' = B' X needs the diagonal residuals"); return (int)MSR_ERR_ARG; }
+            if (!c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P, -1, EPI_X>), grid, block, 0, s, ab);
+            else if (!c && !d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, false, true, GM_TRI_P, -1, EPI_X>), grid, block, 0, s, ab);
             else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
         } else if (gm == GM_RK) {   // msr_gemm_nn
             if (c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false, GM_RK>), grid, block, 0, s, ab);
@@ -747,6 +913,9 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
         if (ab.C) ab.C += b0 * a.sC;
         if (ab.D) ab.D += b0 * a.sD;
         if (ab.DT) ab.DT += b0 * a.sDT;
+        if (ab.alpha_b) ab.alpha_b += b0;
+        if (ab.resid) ab.resid += b0 * a.sv;
+        if (ab.rvec) ab.rvec += b0 * a.sv;
         return ab;
     };
     // whole matrices per XCD for the largest multiple of 8 matrices (1-D grids
@@ -894,6 +1063,9 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
     uint16_t *A = (uint16_t *)(ws + L.off_a);
     uint16_t *B = (uint16_t *)(ws + L.off_b);
     float *part = (float *)(ws + L.off_part);
+    float *alphas = (float *)(ws + L.off_alpha);   // [0, batch): s0^2, [batch, 2 batch): s0
+    float *rho = (float *)(ws + L.off_rho);
+    float *rr = (float *)(ws + L.off_r);
     const int64_t numel = rows * cols;
     const int64_t xs = L.mp * L.np, as = L.mp * L.mp;
 
@@ -905,16 +1077,24 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
         hipLaunchKernelGGL(sumsq_kernel<false>, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
     int rc = check_launch("sumsq_kernel");
     if (rc) return rc;
-    auto normalize = [&](dim3 grid, uint16_t *S, int64_t ldS, int64_t sS, uint16_t *T, int64_t ldT, int64_t sT,
-                         int64_t Rp, int64_t Cp) {
+    // prescale: x0 = u 2^-e and the first products' alphas (steps >= 1); else the
+    // reference's bf16 normalisation (steps == 0: the output is X0 itself)
+    auto normalize = [&](bool prescale, dim3 grid, uint16_t *S, int64_t ldS, int64_t sS, uint16_t *T, int64_t ldT,
+                         int64_t sT, int64_t Rp, int64_t Cp) {
         const bool v = vec && aligned(S, 16) && (!T || aligned(T, 16)) && ldS % 8 == 0 && sS % 8 == 0 &&
                        ldT % 8 == 0 && sT % 8 == 0 && Rp % 8 == 0 && Cp % 8 == 0;
-        if (v)
-            hipLaunchKernelGGL(normalize_vec_kernel, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, T, ldT,
-                               sT, Rp, Cp);
+        if (v && prescale)
+            hipLaunchKernelGGL(normalize_vec_kernel<true>, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, T,
+                               ldT, sT, Rp, Cp, alphas);
+        else if (v)
+            hipLaunchKernelGGL(normalize_vec_kernel<false>, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, T,
+                               ldT, sT, Rp, Cp, alphas);
+        else if (prescale)
+            hipLaunchKernelGGL(normalize_kernel<true>, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, T, ldT,
+                               sT, Rp, Cp, alphas);
         else
-            hipLaunchKernelGGL(normalize_kernel, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, T, ldT, sT,
-                               Rp, Cp);
+            hipLaunchKernelGGL(normalize_kernel<false>, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, T,
+                               ldT, sT, Rp, Cp, alphas);
         return check_launch("normalize_kernel");
     };
 
@@ -922,13 +1102,13 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
     const int64_t Rp = L.transposed ? L.np : L.mp;
     const int64_t Cp = L.transposed ? L.mp : L.np;
     if (steps == 0) {
-        return normalize(dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch), out, cols,
-                         numel, nullptr, 0, 0, rows, cols);
+        return normalize(false, dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch),
+                         out, cols, numel, nullptr, 0, 0, rows, cols);
     }
     uint16_t *Sx = L.transposed ? nullptr : X[0];
     uint16_t *Tx = L.transposed ? X[0] : nullptr;
-    if ((rc = normalize(dim3((unsigned)(Cp / 64), (unsigned)(Rp / 64), (unsigned)batch), Sx, Cp, xs, Tx, Rp, xs, Rp,
-                        Cp)))
+    if ((rc = normalize(true, dim3((unsigned)(Cp / 64), (unsigned)(Rp / 64), (unsigned)batch), Sx, Cp, xs, Tx, Rp,
+                        xs, Rp, Cp)))
         return rc;
 
     const int mp = (int)L.mp, np = (int)L.np;
@@ -944,8 +1124,11 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
         g.DT = nullptr;
         g.M = mp; g.N = mp; g.K = np; g.Mv = mp; g.Nv = mp;
         g.alpha = 1.0f; g.beta = 0.0f; g.symmetric = 1; g.gm = GM_RR;
+        g.alpha_b = it == 0 ? alphas : nullptr;   // s0^2 x0 x0^T
+        g.resid = rho; g.sv = mp;
         if ((rc = launch_gemm(g, batch, s))) return rc;
-        // B' = c (A A) + b A + a I, reading A's lower tiles as the transposed upper ones; upper tiles stored
+        // B' = c (A A) + b A + a I (diagonal corrected for rho), reading A's lower tiles as the
+        // transposed upper ones; upper tiles stored
         g = GemmArgs{};
         g.P = A; g.ldp = mp; g.sP = as;
         g.Q = A; g.ldq = mp; g.sQ = as;
@@ -953,14 +1136,17 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
         g.D = B; g.ldd = mp; g.sD = as;
         g.M = mp; g.N = mp; g.K = mp; g.Mv = mp; g.Nv = mp;
         g.alpha = c_coef; g.beta = b_coef; g.diag = a_coef; g.symmetric = 1; g.gm = GM_TRI_PQ;
+        g.rvec = rho; g.resid = rr; g.sv = mp;
         if ((rc = launch_gemm(g, batch, s))) return rc;
-        // X' = B' X (= B X + a X), X read K-major, B' lower tiles as the transposed upper ones
+        // X' = B' X + r X (= B X + a X), X read K-major, B' lower tiles as the transposed upper ones
         g = GemmArgs{};
         g.P = B; g.ldp = mp; g.sP = as;
         g.Q = X[cur]; g.ldq = np; g.sQ = xs;
         g.C = nullptr;
         g.M = mp; g.N = np; g.K = mp;
         g.alpha = 1.0f; g.beta = 0.0f; g.symmetric = 0; g.gm = GM_TRI_P;
+        g.alpha_b = it == 0 ? alphas + batch : nullptr;   // s0 (B' x0 + r x0)
+        g.rvec = rr; g.sv = mp;
         if (!last) {
             g.D = X[cur ^ 1]; g.ldd = np; g.sD = xs;
             g.DT = nullptr;

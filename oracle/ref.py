@@ -325,14 +325,15 @@ def muon_param_step(p, g, buf, step, param_idx, lr, weight_decay, beta, nesterov
 NS_COEFFS = (3.4445, -4.7750, 2.0315)
 
 
-def ns_fp32(G, steps: int = 5):
+def ns_fp32(G, steps: int = 5, dtype=None):
     """fp32 restatement of muon_sr/muon_sr.py:82-98 (same iteration, fp32 throughout).
 
-    ``G`` is a torch tensor ``[..., rows, cols]``; returns fp32 of the same shape.
+    ``G`` is a torch tensor ``[..., rows, cols]``; returns fp32 (or ``dtype``, e.g.
+    float64 for large matrices on a GPU) of the same shape.
     """
     import torch
     a, b, c = NS_COEFFS
-    X = G.to(torch.float32)
+    X = G.to(torch.float32 if dtype is None else dtype)
     transposed = X.size(-2) > X.size(-1)
     if transposed:
         X = X.mT

@@ -611,88 +611,104 @@ def test_gemm_nn_equals_nt_on_transposed_operand(L):
     assert torch.equal(D1, D2)
 
 
-@pytest.mark.parametrize("rows,cols", [(1024, 1536), (1536, 1024)])
-def test_newton_schulz_equals_composed_products(L, rows, cols):
-    """msr_newton_schulz equals its iteration composed from the diagnostic GEMMs bit for
-    bit.  The symmetric A and B are stored as their upper 256-tiles and read back as the
-    transposed upper tiles; here the full products are computed and their lower tiles
-    replaced by the transposed upper ones, which is what those reads see.  4 x 4 tiles
-    per A exercise every K range (both operands transposed, one, none); the tall case
-    runs on the transpose and writes the output transposed back."""
+# Newton-Schulz tolerance against the exact iteration (O.ns_fp32: the same quintic in
+# fp32 throughout, pinned by its closed form on singular values): 1e-2 relative
+# Frobenius, the contract's bound.  Measured 0.46-0.83e-2 on Gaussian inputs; the
+# reference's own bf16 op sequence (O.ns_bf16_torch) is 1.7-4.8e-2 from it.
+NS_TOL = 1e-2
+
+
+def ns_emul_step(X, first, a, b, c):
+    """One iteration of this library's Newton-Schulz in float64 from a bf16 iterate X
+    (wide orientation, [batch, m, n]), with its bf16 roundings:
+      first: x0 = X 2^-e (e = exponent of ||X||_F), s = 2^e / (||X||_F + 1e-7), else s = 1;
+      A  = bf16(s^2 x0 x0^T),            rho = diag(s^2 x0 x0^T) - diag(A);
+      B' = c A A + b A + a I + diag(rho (b + 2 c diag(A))),   B = bf16(B'),  r = diag(B') - diag(B);
+      X' = bf16(s (B x0 + bf16(r) * x0)).
+    Returns X' (float64 holding bf16 values)."""
+    rb = lambda t: t.to(torch.bfloat16).double()  # noqa: E731
+    x0 = X.double()
+    if first:
+        nrm = x0.float().pow(2).sum(dim=(-2, -1)).sqrt()          # fp32 sum of squares, as the device
+        e = torch.frexp(nrm).exponent
+        x0 = torch.ldexp(x0, -e.double()[:, None, None])
+        s = (torch.ldexp(torch.ones_like(nrm.double()), e.double()) / (nrm.double() + 1e-7))[:, None, None]
+    else:
+        s = torch.ones(X.size(0), 1, 1, dtype=torch.float64, device=X.device)
+    Af = (s * s) * (x0 @ x0.mT)
+    A = rb(Af)
+    rho = torch.diagonal(Af, dim1=-2, dim2=-1) - torch.diagonal(A, dim1=-2, dim2=-1)
+    dA = torch.diagonal(A, dim1=-2, dim2=-1)
+    Bf = c * (A @ A) + b * A + torch.diag_embed(a + rho * (b + 2 * c * dA))
+    B = rb(Bf)
+    r = torch.diagonal(Bf, dim1=-2, dim2=-1) - torch.diagonal(B, dim1=-2, dim2=-1)
+    return rb(s * (B @ x0 + rb(r)[..., None] * x0))
+
+
+def bf16_ulps(x, ref):
+    """|x - ref| in units of the bf16 spacing at ref (both hold bf16 values)."""
+    ref = ref.double()
+    sp = torch.ldexp(torch.ones_like(ref), torch.frexp(ref).exponent - 8)
+    sp = torch.where(ref == 0, torch.full_like(ref, 2.0 ** -133), sp)
+    return (x.double() - ref).abs() / sp
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(1024, 1536, 2), (1536, 1024, 2), (100, 60, 3), (320, 192, 2)])
+def test_newton_schulz_iterations_vs_emulation(L, rows, cols, batch):
+    """Every iteration of msr_newton_schulz against a float64 emulation of it started from
+    the device's previous iterate (NS with steps = k returns X_k): the prescaled first
+    products, the upper-tile storage of A and B' read back transposed (4 x 4 tiles of A at
+    1024 x 1536 run every K range of the mixed-layout loop), the diagonal residuals and the
+    transposed store of tall outputs.  The device sums in fp32 in its own order, so a few
+    elements round the other way: those few, within 2 bf16 ulps except where a result is
+    far below the matrix's typical magnitude (its ulp is then below the fp32 error of the
+    sum), and the whole within 5e-4 relative Frobenius.  A wrong residual, alpha or tile
+    read moves the result by 1e-3 or more."""
     from muon_sr_amd.muon import newton_schulz, NS_COEFFS
     a, b, c = NS_COEFFS
-    torch.manual_seed(5)
-    batch = 2
-    tall = rows > cols
-    m, n = min(rows, cols), max(rows, cols)
+    torch.manual_seed(rows + cols)
     G = (torch.randn(batch, rows, cols, device=DEV) * 1e-3).to(torch.bfloat16)
-    X = newton_schulz(G, steps=0)
-    if tall:
-        X = X.transpose(1, 2).contiguous()
-    T = m // 256
-    upper = torch.tensor([[ti <= tj for tj in range(T)] for ti in range(T)], device=DEV)
-    upper = upper.repeat_interleave(256, 0).repeat_interleave(256, 1)
-
-    def tile_sym(S):
-        return torch.where(upper, S, S.transpose(1, 2))
-
-    def gemm(f, P, Q, C, M, N, K, ldq, alpha, beta, diag):
-        D = torch.empty(batch, M, N, device=DEV, dtype=torch.bfloat16)
-        check(L, f(P.data_ptr(), K, M * K, Q.data_ptr(), ldq, Q[0].numel(), C.data_ptr() if C is not None else None,
-                   N, M * N, D.data_ptr(), N, M * N, M, N, K, batch, alpha, beta, diag, stream()), "gemm")
-        return D
-
-    for _ in range(5):
-        A = tile_sym(gemm(L.msr_gemm_nt, X, X, None, m, m, n, n, 1.0, 0.0, 0.0))
-        B = tile_sym(gemm(L.msr_gemm_nt, A, A, A, m, m, m, m, c, b, a))   # B' = c A A + b A + a I
-        X = gemm(L.msr_gemm_nn, B, X, None, m, n, m, n, 1.0, 0.0, 0.0)
-    if tall:
-        X = X.transpose(1, 2)
-    assert torch.equal(newton_schulz(G), X)
-
-
-def ns_same_op_fp32(G):
-    """fp32 emulation of the library's NS: bf16 storage of X, A, B' = c A A + b A + a I
-    between products, fp32 accumulation, fused fp32 epilogues."""
-    a, b, c = O.NS_COEFFS
-    rb = lambda x: x.to(torch.bfloat16).float()  # noqa: E731
-    X = G.float()
-    tr = X.size(-2) > X.size(-1)
-    if tr:
-        X = X.mT
-    nrm = rb(X.norm(dim=(-2, -1), keepdim=True))
-    X = rb(X / rb(nrm + 1e-7))
-    eye = torch.eye(X.size(-2))
-    for _ in range(5):
-        A = rb(X @ X.mT)
-        B = rb(c * (A @ A) + b * A + a * eye)
-        X = rb(B @ X)
-    if tr:
-        X = X.mT
-    return X
+    tall = rows > cols
+    wide = lambda t: t.mT if tall else t  # noqa: E731
+    prev = G
+    for k in range(3):
+        Xk1 = newton_schulz(G, steps=k + 1)
+        emu = ns_emul_step(wide(prev), k == 0, a, b, c)
+        u = bf16_ulps(wide(Xk1), emu)
+        frac = (u > 0).double().mean().item()
+        rel = rel_fro(wide(Xk1), emu)
+        big = emu.abs() >= 0.25 * emu.pow(2).mean().sqrt()
+        print(f"NS {rows}x{cols} iteration {k + 1}: max {u.max().item():.0f} ulp ({u[big].max().item():.0f} "
+              f"on typical elements), {frac:.2e} of elements differ, rel {rel:.2e}")
+        assert u[big].max().item() <= 2, (k, u[big].max().item())
+        assert frac <= 5e-3, (k, frac)
+        assert rel <= 5e-4, (k, rel)
+        prev = Xk1
 
 
 @pytest.mark.parametrize("shape", [(256, 256), (3, 128, 320), (2, 320, 128), (1024, 256), (256, 1024),
-                                   (100, 60), (61, 99), (2, 512, 1536)])
+                                   (100, 60), (61, 99), (2, 512, 1536), (64, 64), (37, 1000)])
 def test_newton_schulz_vs_fp32(L, shape):
+    """Within NS_TOL of the exact iteration, and closer to it than the reference's own
+    bf16 op sequence is."""
     from muon_sr_amd.muon import newton_schulz
     torch.manual_seed(sum(shape))
     G = (torch.randn(*shape) * 1e-3).to(torch.bfloat16)
     out = newton_schulz(G.to(DEV)).cpu().float()
-    same = ns_same_op_fp32(G.double().float())
-    exact = O.ns_fp32(G)
+    exact = O.ns_fp32(G.double()).double()
     ref16 = O.ns_bf16_torch(G).float()
-    e_same, e_exact, e_ref = rel_fro(out, same), rel_fro(out, exact), rel_fro(ref16, exact)
-    print(f"NS {shape}: vs same-op fp32 {e_same:.2e}, vs exact NS {e_exact:.2e} (reference bf16 NS: {e_ref:.2e})")
-    assert e_same < 1e-2
-    assert e_exact <= e_ref + 2e-3   # at least as close to exact NS as the reference's bf16 op sequence
+    e_exact, e_ref, e_vs_ref = rel_fro(out, exact), rel_fro(ref16, exact), rel_fro(out, ref16)
+    print(f"NS {shape}: vs exact NS {e_exact:.2e}; reference bf16 NS vs exact {e_ref:.2e}, vs ours {e_vs_ref:.2e}")
+    assert e_exact < NS_TOL
+    assert e_exact < e_ref
 
 
 @pytest.mark.parametrize("shape,offset", [((2, 192, 320), 0), ((3, 61, 99), 0), ((2, 320, 128), 0),
                                           ((2, 192, 320), 1), ((1, 1024, 4096), 0)])
 def test_ns_normalize_exact(L, shape, offset):
-    """steps=0 returns bf16(G / d), d = bf16(bf16(||G||_F) + 1e-7), for the 16-byte and
-    the element-wise prologue (offset 1 makes the input pointer unaligned)."""
+    """steps=0 returns the reference's bf16 normalisation bf16(G / d), d =
+    bf16(bf16(||G||_F) + 1e-7) (muon_sr/muon_sr.py:93), for the 16-byte and the
+    element-wise prologue (offset 1 makes the input pointer unaligned)."""
     from muon_sr_amd.muon import newton_schulz
     torch.manual_seed(7)
     n = int(np.prod(shape))

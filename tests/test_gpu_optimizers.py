@@ -521,41 +521,23 @@ def test_sr_unbiased(L, mode):
 
 
 # ---------------------------------------------------------------------------
-# Llama-3-8B shapes: NS at the real matrix shapes vs a same-op fp32 reference
+# Llama-3-8B (config 5) and 16-layer d=2048 (config 4) shapes: NS at the real matrix
+# shapes against the exact iteration (float64 on the GPU) and the reference's bf16
+# op sequence (torch bf16 GEMMs on the GPU)
 # ---------------------------------------------------------------------------
 
-def _ns_same_op_fp32_gpu(G):
-    """fp32 products on the GPU with bf16 storage between them, as the kernel
-    stores X, A and B' = c A A + b A + a I; TF32 disabled."""
-    a, b, c = O.NS_COEFFS
-    rb = lambda x: x.to(torch.bfloat16).float()  # noqa: E731
-    X = G.float()
-    tr = X.size(-2) > X.size(-1)
-    if tr:
-        X = X.mT.contiguous()
-    nrm = rb(X.norm(dim=(-2, -1), keepdim=True))
-    X = rb(X / rb(nrm + 1e-7))
-    eye = torch.eye(X.size(-2), device=X.device)
-    for _ in range(5):
-        A = rb(X @ X.mT.contiguous())
-        B = rb(c * (A @ A) + b * A + a * eye)
-        X = rb(B @ X)
-    return X.mT if tr else X
-
-
-@pytest.mark.parametrize("shape", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("shape", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336),
+                                   (2048, 2048), (5632, 2048), (2048, 5632)])
 def test_newton_schulz_llama_shapes(L, shape):
     from muon_sr_amd.muon import newton_schulz
-    prev = torch.backends.cuda.matmul.allow_tf32
-    torch.backends.cuda.matmul.allow_tf32 = False
-    try:
-        gen = torch.Generator(device=DEV)
-        gen.manual_seed(sum(shape))
-        G = (torch.randn(*shape, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16)
-        out = newton_schulz(G)
-        ref = _ns_same_op_fp32_gpu(G)
-        e = rel_fro(out.float(), ref)
-        print(f"NS {shape}: rel Frobenius vs same-op fp32 {e:.3e}")
-        assert e < 1e-2
-    finally:
-        torch.backends.cuda.matmul.allow_tf32 = prev
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(sum(shape))
+    G = (torch.randn(*shape, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16)
+    out = newton_schulz(G)
+    exact = O.ns_fp32(G, dtype=torch.float64)
+    ref16 = O.ns_bf16_torch(G)
+    e_exact, e_ref = rel_fro(out, exact), rel_fro(ref16, exact)
+    print(f"NS {shape}: vs exact NS {e_exact:.3e}; reference bf16 NS vs exact {e_ref:.3e}, "
+          f"vs ours {rel_fro(out, ref16):.3e}")
+    assert e_exact < 1e-2
+    assert e_exact < e_ref

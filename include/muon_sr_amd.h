@@ -117,6 +117,22 @@ int msr_centralize_workspace_bytes(int64_t rows, int64_t cols, size_t *bytes);
 int msr_centralize_bf16(const uint16_t *g, uint16_t *out, int64_t rows, int64_t cols, float alpha,
                         void *workspace, size_t workspace_bytes, msr_stream_t stream);
 
+/* msr_centralize_bf16 without a workspace argument and without allocating.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The workspace is a static device array of
+ * MSR_CENTRALIZE_NOALLOC_SCRATCH_BYTES in the library, one per GPU, held until
+ * the process ends; its address is looked up on the first call for a device
+ * (the device of `stream`, or the current device for the null stream).  Sizes
+ * whose msr_centralize_workspace_bytes exceed it return MSR_ERR_WORKSPACE
+ * (4 MiB covers about 500,000 rows of up to 16384 columns, e.g. a 128256 x 4096
+ * embedding).  Same results as msr_centralize_bf16, bit for bit.  Calls that
+ * overlap in time on one GPU share the array and race: serialise them (one
+ * stream, or events). */
+#define MSR_CENTRALIZE_NOALLOC_SCRATCH_BYTES (4 << 20)
+int msr_centralize_bf16_noalloc(const uint16_t *g, uint16_t *out, int64_t rows, int64_t cols, float alpha,
+                                msr_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * (a) 8-bit blockwise AdamW step (bitsandbytes order: decay after the update).
  * Replaces the _adamw_8bit_kernel launch of TritonAdamW8bit.step

@@ -10,6 +10,8 @@
 //   3. centralize_kernel    g' = bf16_rne(g - m)
 // Every sum has a fixed order (per-thread strides, then a fixed LDS tree), so
 // results do not depend on the launch or on the other rows.
+#include <mutex>
+
 #include "common.hpp"
 #include "vecio.hpp"
 #include "../../include/muon_sr_amd.h"
@@ -100,6 +102,68 @@ static size_t cent_ws(int64_t rows, int64_t chunks) {
     return ((size_t)(rows * chunks) * 4 + 255) / 256 * 256 + (size_t)rows * 4;
 }
 
+// The three launches over a workspace of cent_ws(rows, chunks) bytes (validated by the caller).
+static int centralize_launch(const uint16_t *g, uint16_t *out, int64_t rows, int64_t cols, int64_t chunks,
+                             float alpha, char *workspace, hipStream_t s) {
+    CentArgs a;
+    a.g = g; a.out = out; a.rows = rows; a.cols = cols; a.chunks = chunks;
+    a.partial = reinterpret_cast<float *>(workspace);
+    a.mean = reinterpret_cast<float *>(workspace + ((size_t)(rows * chunks) * 4 + 255) / 256 * 256);
+    a.alpha = alpha;
+    a.vec = (cols % 8) == 0 && aligned(g, 16) && aligned(out, 16);
+    const unsigned wgs = (unsigned)(rows * chunks);
+    hipLaunchKernelGGL(row_partial_kernel, dim3(wgs), dim3(CENT_THREADS), 0, s, a);
+    int rc = check_launch("row_partial_kernel");
+    if (rc) return rc;
+    hipLaunchKernelGGL(row_mean_kernel, dim3((unsigned)((rows + CENT_THREADS - 1) / CENT_THREADS)), dim3(CENT_THREADS), 0,
+                       s, a);
+    if ((rc = check_launch("row_mean_kernel"))) return rc;
+    hipLaunchKernelGGL(centralize_kernel, dim3(wgs), dim3(CENT_THREADS), 0, s, a);
+    return check_launch("centralize_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of msr_centralize_bf16_noalloc: a file-scope device array, one copy
+// per GPU for the life of the process.  Its device address is looked up once
+// per device (hipGetSymbolAddress with that device current) and only that
+// address is used by host code: the array's name is a host-side stand-in.
+// Every word a call reads is written earlier in the same call (partials by
+// row_partial_kernel, means by row_mean_kernel), so nothing is cleared.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) char scratch[MSR_CENTRALIZE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static std::mutex scratch_mu;
+static void *scratch_ptr[SCRATCH_MAX_DEVICES];
+
+// Device address of `scratch` on the device of `stream` (the current device for the
+// null stream), looked up on the first call for that device.
+static int scratch_for(hipStream_t stream, char **out) {
+    int dev = 0;
+    hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) { set_error("scratch: no device for the stream (%s)", hipGetErrorString(e)); return (int)e; }
+    if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) { set_error("scratch: device %d out of range", dev); return MSR_ERR_ARG; }
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_ptr[dev]) {
+        int cur = 0;
+        if ((e = hipGetDevice(&cur)) != hipSuccess) { set_error("scratch: hipGetDevice: %s", hipGetErrorString(e)); return (int)e; }
+        if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) {
+            set_error("scratch: hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+            return (int)e;
+        }
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (e != hipSuccess || !p) {
+            set_error("scratch: hipGetSymbolAddress on device %d: %s", dev, hipGetErrorString(e));
+            return e != hipSuccess ? (int)e : MSR_ERR_LAUNCH;
+        }
+        scratch_ptr[dev] = p;
+    }
+    *out = static_cast<char *>(scratch_ptr[dev]);
+    return MSR_OK;
+}
+
 }  // namespace msr
 
 using namespace msr;
@@ -135,22 +199,33 @@ int msr_centralize_bf16(const uint16_t *g, uint16_t *out, int64_t rows, int64_t 
         set_error("msr_centralize_bf16: g, out and the workspace overlap (only out == g is allowed)");
         return MSR_ERR_OVERLAP;
     }
-    CentArgs a;
-    a.g = g; a.out = out; a.rows = rows; a.cols = cols; a.chunks = chunks;
-    a.partial = static_cast<float *>(workspace);
-    a.mean = reinterpret_cast<float *>(static_cast<char *>(workspace) + ((size_t)(rows * chunks) * 4 + 255) / 256 * 256);
-    a.alpha = alpha;
-    a.vec = (cols % 8) == 0 && aligned(g, 16) && aligned(out, 16);
+    return centralize_launch(g, out, rows, cols, chunks, alpha, static_cast<char *>(workspace), (hipStream_t)stream);
+}
+
+int msr_centralize_bf16_noalloc(const uint16_t *g, uint16_t *out, int64_t rows, int64_t cols, float alpha,
+                                msr_stream_t stream) {
+    if (rows < 0 || cols < 0 || (rows > 0 && cols > 0 && (!g || !out))) {
+        set_error("msr_centralize_bf16_noalloc: bad arguments");
+        return MSR_ERR_ARG;
+    }
+    if (rows == 0 || cols == 0) return MSR_OK;
+    const int64_t chunks = (cols + CENT_CHUNK - 1) / CENT_CHUNK;
+    if (rows > (int64_t(1) << 31) / chunks || cent_ws(rows, chunks) > MSR_CENTRALIZE_NOALLOC_SCRATCH_BYTES) {
+        set_error("msr_centralize_bf16_noalloc: %lld rows x %lld chunks need more than the %d bytes of scratch "
+                  "(use msr_centralize_bf16 with a workspace)", (long long)rows, (long long)chunks,
+                  (int)MSR_CENTRALIZE_NOALLOC_SCRATCH_BYTES);
+        return MSR_ERR_WORKSPACE;
+    }
+    const size_t gb = 2 * (size_t)rows * (size_t)cols;
+    if (partial_overlap(g, gb, out, gb)) {
+        set_error("msr_centralize_bf16_noalloc: g and out overlap (only out == g is allowed)");
+        return MSR_ERR_OVERLAP;
+    }
     hipStream_t s = (hipStream_t)stream;
-    const unsigned wgs = (unsigned)(rows * chunks);
-    hipLaunchKernelGGL(row_partial_kernel, dim3(wgs), dim3(CENT_THREADS), 0, s, a);
-    int rc = check_launch("row_partial_kernel");
+    char *ws = nullptr;
+    const int rc = scratch_for(s, &ws);
     if (rc) return rc;
-    hipLaunchKernelGGL(row_mean_kernel, dim3((unsigned)((rows + CENT_THREADS - 1) / CENT_THREADS)), dim3(CENT_THREADS), 0,
-                       s, a);
-    if ((rc = check_launch("row_mean_kernel"))) return rc;
-    hipLaunchKernelGGL(centralize_kernel, dim3(wgs), dim3(CENT_THREADS), 0, s, a);
-    return check_launch("centralize_kernel");
+    return centralize_launch(g, out, rows, cols, chunks, alpha, ws, s);
 }
 
 }  // extern "C"

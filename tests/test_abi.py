@@ -52,6 +52,9 @@ def test_argument_validation_without_gpu(lib):
                                 1, None, None)
     assert rc == 1001 and b"block" in lib.msr_last_error()
     assert lib.msr_sr_accum(None, None, 0, -1, 0, 0, 1, None, None) == 1001
+    # the allocation-free centralization refuses sizes beyond its static scratch before any HIP call
+    assert lib.msr_centralize_bf16_noalloc(1, 1, 1 << 20, 8, 1.0, None) == 1004
+    assert b"scratch" in lib.msr_last_error()
     assert lib.msr_sr_accum(1, 1, 0, 10, 0, 0, 7, None, None) == 1001
     assert lib.msr_sr_accum(1, 1, 0, 10, 0, 0, 2, None, None) == 1001   # INJECT without a buffer
     from muon_sr_amd import _lib

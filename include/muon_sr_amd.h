@@ -162,13 +162,16 @@ int msr_adamw8bit_step(uint16_t *p, const uint16_t *g, void *state1, void *state
  * Replaces the grad->stack copy and the _muon_prepare_kernel launch of
  * _triton_muon_batch_step (muon_sr/triton_muon_sr.py:150-159) and, with
  * count == 1, _run_prepare (:88-98).
- *   grads: HOST array of `count` device pointers, each to numel_each bf16.
+ *   grads: HOST array of `count` device pointers, each to numel_each bf16
+ *          (grad_is_f32 == 0) or fp32 (grad_is_f32 != 0: read as fp32, as the
+ *          reference's kernel reads an fp32 gradient on the per-parameter path,
+ *          :34; its batched path copies gradients into a bf16 stack first).
  *   buf:   bf16 momentum stack [count][numel_each], updated in place (SR).
  *   out:   bf16 pre-NS update [count][numel_each] (RNE).
  * Noise offset of element j of matrix i: i*numel_each + j (stack offset).
  * inject: uint16 [count*numel_each].
  * ------------------------------------------------------------------------- */
-int msr_muon_prepare(const uint16_t *const *grads, uint16_t *buf, uint16_t *out,
+int msr_muon_prepare(const void *const *grads, int32_t grad_is_f32, uint16_t *buf, uint16_t *out,
                      int64_t numel_each, int32_t count, float beta, int32_t nesterov,
                      uint32_t seed, int32_t noise_mode, const uint16_t *inject, msr_stream_t stream);
 

@@ -44,7 +44,7 @@ SIGNATURES = {
     "msr_centralize_bf16_noalloc": (ctypes.c_int, [_P, _P, _I64, _I64, _F, _P]),
     "msr_adamw8bit_step": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32,
                                           _F, _F, _F, _F, _F, _F, _F, _U32, _I32, _P, _P]),
-    "msr_muon_prepare": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _F, _I32, _U32, _I32, _P, _P]),
+    "msr_muon_prepare": (ctypes.c_int, [_P, _I32, _P, _P, _I64, _I32, _F, _I32, _U32, _I32, _P, _P]),
     "msr_muon_apply": (ctypes.c_int, [_P, _P, _I64, _I32, _F, _F, _F, _P, _I32, _P, _P]),
     "msr_ns_workspace_bytes": (ctypes.c_int, [_I64, _I64, _I64, _SIZE_P]),
     "msr_newton_schulz": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _I32, _F, _F, _F, _P, ctypes.c_size_t, _P]),

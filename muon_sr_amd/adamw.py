@@ -179,12 +179,19 @@ class TritonSRAccumulator:
             optimizer.zero_grad()
     """
 
-    # Accumulations are launched many tensors at a time: the hooks of one
-    # backward pass queue their (acc, grad) pairs, and the queue is flushed at
-    # the end of the pass (an autograd final callback), when it holds
-    # `max_deferred_bytes` of gradients, and by reassign_grad_buffer().  The
-    # arithmetic and noise are those of one launch per tensor.  Outside a
-    # backward pass (and outside `deferred()`) each hook launches at once.
+    # By default each hook launches its accumulation at once, as the reference's
+    # does: p.acc_grad holds the sum after every hook (in stream order) and the
+    # gradient is released right away.  With `defer_in_backward = True` (or
+    # inside `deferred()`), hooks queue their (acc, grad) pairs and the queue is
+    # launched many tensors at a time: at the end of the backward pass (an
+    # autograd final callback), when it holds `max_deferred_bytes` of gradients,
+    # and in reassign_grad_buffer().  The arithmetic and noise are those of one
+    # launch per tensor; the differences are that queued gradients stay alive
+    # until the flush (up to max_deferred_bytes per device) and that a queued
+    # p.acc_grad is complete only after it (its first micro-batch's buffer is
+    # allocated uninitialised).  The in-backward flush relies on torch's
+    # private graph-task id and execution-engine callback queue.
+    defer_in_backward = False
     max_deferred_bytes = 512 << 20
 
     @staticmethod
@@ -204,7 +211,7 @@ class TritonSRAccumulator:
         acc = p.acc_grad
         stream = _lib.stream_of(acc)
         f32 = grad.dtype == torch.float32
-        task = torch._C._current_graph_task_id()
+        task = torch._C._current_graph_task_id() if TritonSRAccumulator.defer_in_backward else -1
         if task == -1 and _deferred_depth == 0:
             rc = _lib.lib().msr_sr_accum(acc.data_ptr(), grad.data_ptr(), int(f32), n, seed, int(first),
                                          _lib.noise_mode(), None, stream)

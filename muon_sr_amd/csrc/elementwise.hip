@@ -214,7 +214,7 @@ __global__ __launch_bounds__(THREADS) void adamw_bf16_kernel(AdamWArgs a) {
 constexpr int MAX_TABLE = 240;  // pointers per launch (kernel-argument table)
 
 struct PrepareArgs {
-    const uint16_t *grads[MAX_TABLE];
+    const void *grads[MAX_TABLE];   // bf16, or fp32 (G32)
     uint16_t *buf;       // stack base (already offset to the first matrix of this launch)
     uint16_t *out;
     int64_t numel;
@@ -223,10 +223,12 @@ struct PrepareArgs {
     Noise ns;
 };
 
-template <int MODE, bool NEST, bool VEC>
+// G32: fp32 gradients, read as fp32 (the reference's kernel loads the gradient in its
+// own dtype, muon_sr/triton_muon_sr.py:34)
+template <int MODE, bool NEST, bool VEC, bool G32>
 __global__ __launch_bounds__(THREADS) void muon_prepare_kernel(PrepareArgs a) {
     const int i = blockIdx.y;
-    const uint16_t *g = a.grads[i];
+    const void *g = a.grads[i];
     uint16_t *buf = a.buf + (int64_t)i * a.numel;
     uint16_t *out = a.out + (int64_t)i * a.numel;
     const int64_t base = a.stack_off0 + (int64_t)i * a.numel;
@@ -236,10 +238,14 @@ __global__ __launch_bounds__(THREADS) void muon_prepare_kernel(PrepareArgs a) {
         const int64_t o0 = t << 3;
         const int valid = clamp_valid(a.numel, o0);
         uint32_t wg[4], wb[4];
-        load_bf16x8<VEC>(g, o0, valid, wg);
-        load_bf16x8<VEC>(buf, o0, valid, wb);
         float gf[8], bf[8];
-        unpack8(wg, gf);
+        if constexpr (G32) {
+            load_f32x8<VEC>(static_cast<const float *>(g), o0, valid, gf);
+        } else {
+            load_bf16x8<VEC>(static_cast<const uint16_t *>(g), o0, valid, wg);
+            unpack8(wg, gf);
+        }
+        load_bf16x8<VEC>(buf, o0, valid, wb);
         unpack8(wb, bf);
         uint32_t r[8];
         if (VEC || MODE != NOISE_PHILOX8) {
@@ -467,9 +473,9 @@ int msr_adamw_bf16_step(uint16_t *p, const uint16_t *g, uint16_t *ema, uint16_t 
     return check_launch("msr_adamw_bf16_step");
 }
 
-int msr_muon_prepare(const uint16_t *const *grads, uint16_t *buf, uint16_t *out, int64_t numel_each, int32_t count,
-                     float beta, int32_t nesterov, uint32_t seed, int32_t noise_mode, const uint16_t *inject,
-                     msr_stream_t stream) {
+int msr_muon_prepare(const void *const *grads, int32_t grad_is_f32, uint16_t *buf, uint16_t *out, int64_t numel_each,
+                     int32_t count, float beta, int32_t nesterov, uint32_t seed, int32_t noise_mode,
+                     const uint16_t *inject, msr_stream_t stream) {
     if (numel_each < 0 || count < 0 || (numel_each > 0 && count > 0 && (!grads || !buf || !out))) {
         set_error("msr_muon_prepare: bad arguments");
         return MSR_ERR_ARG;
@@ -477,7 +483,7 @@ int msr_muon_prepare(const uint16_t *const *grads, uint16_t *buf, uint16_t *out,
     MSR_CHECK_MODE(noise_mode, inject);
     if (numel_each == 0 || count == 0) return MSR_OK;
     {
-        const size_t sb = 2 * (size_t)numel_each * (size_t)count, eb = 2 * (size_t)numel_each;
+        const size_t sb = 2 * (size_t)numel_each * (size_t)count, eb = (grad_is_f32 ? 4 : 2) * (size_t)numel_each;
         bool race = (uintptr_t)buf < (uintptr_t)out + sb && (uintptr_t)out < (uintptr_t)buf + sb;
         for (int32_t i = 0; i < count && !race; ++i)
             race = grads[i] && (partial_overlap(grads[i], eb, buf, sb) || partial_overlap(grads[i], eb, out, sb));
@@ -502,9 +508,14 @@ int msr_muon_prepare(const uint16_t *const *grads, uint16_t *buf, uint16_t *out,
         a.ns = make_noise(seed, 0, inject, 0);
         const unsigned gx = grid_for((numel_each + 7) / 8, THREADS, (256 * 32 + cnt - 1) / cnt);
         const dim3 grid(gx, (unsigned)cnt);
-#define LAUNCH_PREP(NEST, V) MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((muon_prepare_kernel<M, NEST, V>), grid, dim3(THREADS), 0, s, a))
-        if (nesterov) { if (vec) { LAUNCH_PREP(true, true); } else { LAUNCH_PREP(true, false); } }
-        else { if (vec) { LAUNCH_PREP(false, true); } else { LAUNCH_PREP(false, false); } }
+#define LAUNCH_PREP(NEST, V, G) MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((muon_prepare_kernel<M, NEST, V, G>), grid, dim3(THREADS), 0, s, a))
+        if (grad_is_f32) {
+            if (nesterov) { if (vec) { LAUNCH_PREP(true, true, true); } else { LAUNCH_PREP(true, false, true); } }
+            else { if (vec) { LAUNCH_PREP(false, true, true); } else { LAUNCH_PREP(false, false, true); } }
+        } else {
+            if (nesterov) { if (vec) { LAUNCH_PREP(true, true, false); } else { LAUNCH_PREP(true, false, false); } }
+            else { if (vec) { LAUNCH_PREP(false, true, false); } else { LAUNCH_PREP(false, false, false); } }
+        }
 #undef LAUNCH_PREP
         int rc = check_launch("msr_muon_prepare");
         if (rc) return rc;

@@ -82,18 +82,31 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
 
 
 def _bf16_contig(t: torch.Tensor) -> torch.Tensor:
+    """The batched path's gradient: the reference copies it into a bf16 stack
+    (muon_sr/triton_muon_sr.py:150-152), an RNE cast for other dtypes."""
     if t.dtype != torch.bfloat16:
         t = t.to(torch.bfloat16)
+    return t.contiguous()
+
+
+def _grad_operand(t: torch.Tensor) -> torch.Tensor:
+    """The per-parameter path's gradient: the reference's prepare kernel loads it in its
+    own dtype and converts to fp32 (muon_sr/triton_muon_sr.py:34), so a bf16 gradient is
+    passed as is and any other as fp32 (exact for fp16 and fp32)."""
+    if t.dtype != torch.bfloat16 and t.dtype != torch.float32:
+        t = t.float()
     return t.contiguous()
 
 
 def _run_prepare(grads, buf_stack, out, beta, nesterov, seed):
     """Momentum + nesterov for `len(grads)` matrices whose momenta are rows of
     `buf_stack`; writes the bf16 pre-NS update rows into `out`
-    (muon_sr/triton_muon_sr.py:18-50, 88-98, 150-159)."""
+    (muon_sr/triton_muon_sr.py:18-50, 88-98, 150-159).  The gradients are all bf16
+    or all fp32."""
     n = grads[0].numel() if len(grads) else 0
+    f32 = bool(len(grads)) and grads[0].dtype == torch.float32
     table = _lib.ptr_array([g.data_ptr() for g in grads])
-    rc = _lib.lib().msr_muon_prepare(table, buf_stack.data_ptr(), out.data_ptr(), n, len(grads), beta,
+    rc = _lib.lib().msr_muon_prepare(table, int(f32), buf_stack.data_ptr(), out.data_ptr(), n, len(grads), beta,
                                      int(bool(nesterov)), seed, _lib.noise_mode(), None, _lib.stream_of(buf_stack))
     _lib.check(rc, "msr_muon_prepare")
 
@@ -116,7 +129,7 @@ def _check_param(p, name):
 
 def _muon_step(p, grad, buf, beta, nesterov, ns_steps, lr, weight_decay, step, param_idx):
     """Single-param Muon step (muon_sr/triton_muon_sr.py:116-120)."""
-    grad = _bf16_contig(grad)
+    grad = _grad_operand(grad)
     update = torch.empty(p.shape, dtype=torch.bfloat16, device=p.device)
     _run_prepare([grad], buf, update, beta, nesterov, _deterministic_seed(step, param_idx, salt=0))
     update_ns = newton_schulz(update, steps=ns_steps)
@@ -373,6 +386,8 @@ class TritonMuonSRWithAuxAdam(_StackedBufsMixin, Optimizer):
                 eps = group["eps"]
                 weight_decay = group["weight_decay"]
                 eight_bit = group.get("optim_bits", 16) == 8
+                if eight_bit:
+                    TritonAdamW8bit._validate_group(group)   # as TritonAdamW8bit.step (triton_adamw_8bit.py:175)
 
                 for i, p in enumerate(group["params"]):
                     assert p.dtype == torch.bfloat16, "only bfloat16 is supported."
@@ -384,6 +399,8 @@ class TritonMuonSRWithAuxAdam(_StackedBufsMixin, Optimizer):
                     if eight_bit:
                         self._step_8bit(p, group, state, lr, beta1, beta2, eps, weight_decay, group_offset + i)
                         continue
+                    if "format_version" in state:   # an 8-bit state in a group no longer set to optim_bits=8
+                        raise ValueError("Cannot change quantization configuration after state initialization")
                     if len(state) == 0:
                         state["step"] = 0
                         state["ema"] = torch.zeros_like(p, dtype=torch.bfloat16, memory_format=torch.contiguous_format)
@@ -416,8 +433,14 @@ class TritonMuonSRWithAuxAdam(_StackedBufsMixin, Optimizer):
             raise ValueError("Parameters/gradients must be contiguous and dense")
         if not p.numel():
             return
+        if state and "format_version" not in state:   # a bf16-moment AdamW state from before optim_bits=8
+            raise ValueError("Cannot change quantization configuration after state initialization")
         if not state:
             state.update(init_8bit_state(p, group["block_size"], 8, group["min_8bit_size"], self._maps))
+        # triton_adamw_8bit.py:192-194
+        expected_bits = 16 if p.numel() < group["min_8bit_size"] else group["optim_bits"]
+        if state.get("block_size") != group["block_size"] or state.get("optim_bits") != expected_bits:
+            raise ValueError("Cannot change quantization configuration after state initialization")
         state["step"] += 1
         seed = (state["step"] * 2654435761 ^ param_index * 1234567891) & 0xFFFFFFFF
         adamw8bit_launch(p.data, g, state, lr, beta1, beta2, eps, weight_decay, seed)

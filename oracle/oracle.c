@@ -308,12 +308,13 @@ void orc_adamw8bit(uint16_t *p, const uint16_t *g,
  * (out_bf16, may be NULL).  The noise offset is the element's position in the
  * launch (the whole stack in the batched path, :154-159); NOISE_TRITON keeps
  * its low 32 bits as the reference's `offsets.to(tl.int32)` does (:44). */
-void orc_muon_prepare(const uint16_t *g, uint16_t *buf, float *out_f32, uint16_t *out_bf16,
+void orc_muon_prepare(const void *g, int32_t g_is_f32, uint16_t *buf, float *out_f32, uint16_t *out_bf16,
                       int64_t n, float beta, int32_t nesterov, const orc_noise_t *ns)
 {
     const float one_m_beta = 1.0f - beta;
     for (int64_t o = 0; o < n; ++o) {
-        float gf = bf16_to_f32(g[o]);
+        /* the gradient in its own dtype (:34): bf16, or fp32 on the per-parameter path */
+        float gf = g_is_f32 ? ((const float *)g)[o] : bf16_to_f32(((const uint16_t *)g)[o]);
         float bf = bf16_to_f32(buf[o]);
         float nb = bf + one_m_beta * (gf - bf);                 /* :37 */
         float upd = nesterov ? gf + beta * (nb - gf) : nb;      /* :39-42 */

@@ -61,7 +61,7 @@ def lib():
         L.orc_adamw_bf16.argtypes = [P, P, P, P, I64, F, F, F, F, F, F, F, NP, NP, NP]
         L.orc_adamw8bit.argtypes = [P, P, P, P, P, P, P, P, P, P, I64, I32, I32,
                                     F, F, F, F, F, F, F, NP, NP, NP]
-        L.orc_muon_prepare.argtypes = [P, P, P, P, I64, F, I32, NP]
+        L.orc_muon_prepare.argtypes = [P, I32, P, P, P, I64, F, I32, NP]
         L.orc_muon_apply.argtypes = [P, P, I64, F, F, F, NP]
         L.orc_num_threads.restype = I32
         L.orc_num_threads.argtypes = []
@@ -235,12 +235,14 @@ def adamw8bit(p, g, state1, state2, absmax1, absmax2, q1, q2, block, quantized,
 
 
 def muon_prepare(g, buf, beta, nesterov, noise: NoiseSpec):
-    """Returns (new_buf_bf16, update_f32, update_bf16_rne)."""
-    g = np.ascontiguousarray(g, dtype=np.uint16)
+    """Returns (new_buf_bf16, update_f32, update_bf16_rne).  ``g``: bf16 bits (uint16) or
+    float32 (read as fp32, as the reference's kernel reads an fp32 gradient)."""
+    f32 = np.asarray(g).dtype == np.float32
+    g = np.ascontiguousarray(g, dtype=np.float32 if f32 else np.uint16)
     buf = np.array(buf, dtype=np.uint16, copy=True)
     out32 = np.zeros(buf.shape, dtype=np.float32)
     out16 = np.zeros(buf.shape, dtype=np.uint16)
-    lib().orc_muon_prepare(_ptr(g), _ptr(buf), _ptr(out32), _ptr(out16), buf.size,
+    lib().orc_muon_prepare(_ptr(g), int(f32), _ptr(buf), _ptr(out32), _ptr(out16), buf.size,
                            _f(beta), int(bool(nesterov)), noise.ref())
     return buf, out32, out16
 

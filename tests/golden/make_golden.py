@@ -28,6 +28,9 @@ from __future__ import annotations
 import os
 import sys
 
+# importing the reference must not write bytecode into its (read-only) checkout
+sys.dont_write_bytecode = True
+
 os.environ["TRITON_INTERPRET"] = "1"
 
 import numpy as np  # noqa: E402

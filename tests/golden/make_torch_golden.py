@@ -16,6 +16,9 @@ from __future__ import annotations
 import os
 import sys
 
+# importing the reference must not write bytecode into its (read-only) checkout
+sys.dont_write_bytecode = True
+
 import numpy as np
 import torch
 

@@ -95,7 +95,7 @@ def test_overlapping_operands_are_rejected(lib):
     assert lib.msr_adamw8bit_step(A, B, C, D, C + 32, D + 4096, 1, 1, None, 1024, 256, 1, 1e-3, 0.9, 0.99, 1e-8,
                                   0.0, 0.1, 0.01, 0, 1, None, None) == OVERLAP
     grads = _lib.ptr_array([A, A + 128])
-    assert lib.msr_muon_prepare(grads, B, B + 64, 64, 2, 0.95, 1, 0, 1, None, None) == OVERLAP
+    assert lib.msr_muon_prepare(grads, 0, B, B + 64, 64, 2, 0.95, 1, 0, 1, None, None) == OVERLAP
     params = _lib.ptr_array([A, A + 64])
     seeds = _lib.ptr_array([1, 2], ctypes.c_uint32)
     assert lib.msr_muon_apply(params, B, 64, 2, 0.02, 0.0, 1.0, seeds, 1, None, None) == OVERLAP

@@ -496,7 +496,7 @@ def test_muon_prepare_reference_vectors(L, golden, nest):
     g, buf = u16_to_dev(k("in_g")), u16_to_dev(k("in_buf"))
     out = torch.empty_like(buf)
     tbl = ptr_array([g.data_ptr()])
-    check(L, L.msr_muon_prepare(tbl, buf.data_ptr(), out.data_ptr(), g.numel(), 1, 0.95, nest, int(k("seed")),
+    check(L, L.msr_muon_prepare(tbl, 0, buf.data_ptr(), out.data_ptr(), g.numel(), 1, 0.95, nest, int(k("seed")),
                                 O.NOISE_TRITON, None, stream()))
     assert np.array_equal(dev_to_u16(buf), k("out_buf"))
     rne = torch.from_numpy(k("out_upd_f32")).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
@@ -518,8 +518,32 @@ def test_muon_prepare_stack_vs_oracle(L, rows, cols, mode):
     buf = u16_to_dev(buf0)
     out = torch.empty_like(buf)
     inj_d = np_to_dev(inj.view(np.int16)) if mode == O.NOISE_INJECT else None
-    check(L, L.msr_muon_prepare(ptr_array([t.data_ptr() for t in gd]), buf.data_ptr(), out.data_ptr(), numel, count,
-                                0.95, 1, seed, mode, ptr(inj_d), stream()))
+    check(L, L.msr_muon_prepare(ptr_array([t.data_ptr() for t in gd]), 0, buf.data_ptr(), out.data_ptr(), numel,
+                                count, 0.95, 1, seed, mode, ptr(inj_d), stream()))
+    assert np.array_equal(dev_to_u16(buf), eb)
+    assert np.array_equal(dev_to_u16(out), eu)
+
+
+@pytest.mark.parametrize("numel,offset", [(4096, 0), (1000 + 3, 0), (4096, 1)])
+@pytest.mark.parametrize("mode", [O.NOISE_TRITON, O.NOISE_PHILOX8])
+def test_muon_prepare_fp32_grads_vs_oracle(L, numel, offset, mode):
+    """fp32 gradients are read as fp32 (the reference's per-parameter path), 16-byte
+    and element-wise loads (offset 1 misaligns the gradient)."""
+    rng = np.random.default_rng(numel + mode)
+    count = 3
+    grads = [(rng.standard_normal(numel) * 1e-3).astype(np.float32) for _ in range(count)]
+    buf0 = rng_bf16(rng, count * numel, 1e-3)
+    seed = 12345
+    eb, _, eu = O.muon_prepare(np.concatenate(grads), buf0, 0.95, True, O.NoiseSpec(mode, seed))
+    gd = []
+    for g in grads:
+        t = torch.zeros(numel + offset, dtype=torch.float32, device=DEV)
+        t[offset:] = torch.from_numpy(g).to(DEV)
+        gd.append(t)
+    buf = u16_to_dev(buf0)
+    out = torch.empty_like(buf)
+    check(L, L.msr_muon_prepare(ptr_array([t[offset:].data_ptr() for t in gd]), 1, buf.data_ptr(), out.data_ptr(),
+                                numel, count, 0.95, 1, seed, mode, None, stream()))
     assert np.array_equal(dev_to_u16(buf), eb)
     assert np.array_equal(dev_to_u16(out), eu)
 

@@ -422,8 +422,13 @@ def test_adamw8bit_checkpoint_validation(L):
 # TritonSRAccumulator: hooks through a real backward, against the oracle
 # ---------------------------------------------------------------------------
 
+@pytest.mark.parametrize("defer", [False, True])
 @pytest.mark.parametrize("mode_name", ["triton", "philox8"])
-def test_sr_accumulator_hooks_vs_oracle(L, noise, mode_name):
+def test_sr_accumulator_hooks_vs_oracle(L, noise, mode_name, defer):
+    """Hooks through a real backward.  By default (as the reference) p.acc_grad holds the
+    running sum right after each hook, checked by a hook registered after the
+    accumulator's; with defer_in_backward the launches are batched at the end of the
+    pass and the final sums are the same."""
     from muon_sr_amd import TritonSRAccumulator
     noise(mode_name)
     mode = O.NOISE_TRITON if mode_name == "triton" else O.NOISE_PHILOX8
@@ -431,31 +436,83 @@ def test_sr_accumulator_hooks_vs_oracle(L, noise, mode_name):
     model = torch.nn.Sequential(torch.nn.Linear(64, 200), torch.nn.GELU(), torch.nn.Linear(200, 7))
     model = model.to(device=DEV, dtype=torch.bfloat16)
     seen = []      # (param name, grad bits) in hook order, captured before the accumulator runs
+    after = []     # (param name, acc_grad bits) right after the accumulator's hook
     names = {id(p): n for n, p in model.named_parameters()}
     capture = [p.register_post_accumulate_grad_hook(lambda p: seen.append((names[id(p)], dev_to_u16(p.grad))))
                for p in model.parameters()]
-    hooks = TritonSRAccumulator.assign_hooks(model)
-    assert len(hooks) == 4
-    random.seed(1234)
-    for mb in range(3):
-        x = torch.randn(16, 64, device=DEV, dtype=torch.bfloat16)
-        model(x).float().square().mean().backward()
-        for p in model.parameters():
-            assert p.grad is None and hasattr(p, "acc_grad")
-    TritonSRAccumulator.reassign_grad_buffer(model)
+    old_defer = TritonSRAccumulator.defer_in_backward
+    TritonSRAccumulator.defer_in_backward = defer
+    try:
+        hooks = TritonSRAccumulator.assign_hooks(model)
+        assert len(hooks) == 4
+        check = [p.register_post_accumulate_grad_hook(lambda p: after.append((names[id(p)], dev_to_u16(p.acc_grad))))
+                 for p in model.parameters()]
+        random.seed(1234)
+        for mb in range(3):
+            x = torch.randn(16, 64, device=DEV, dtype=torch.bfloat16)
+            model(x).float().square().mean().backward()
+            for p in model.parameters():
+                assert p.grad is None and hasattr(p, "acc_grad")
+        TritonSRAccumulator.reassign_grad_buffer(model)
+    finally:
+        TritonSRAccumulator.defer_in_backward = old_defer
     # replay: one getrandbits(32) per hook call, in hook order
     rs = random.Random(1234)
     acc = {}
-    for name, g in seen:
+    assert len(seen) == 12 and len(after) == 12
+    for (name, g), (name2, a) in zip(seen, after):
         seed = rs.getrandbits(32)
         prev = acc.get(name, np.zeros_like(g))
         acc[name] = O.sr_accum(prev, g, O.NoiseSpec(mode, seed))
-    assert len(seen) == 12
+        assert name2 == name
+        if not defer:
+            assert np.array_equal(a, acc[name]), name
     for name, p in model.named_parameters():
         assert not hasattr(p, "acc_grad")
         assert np.array_equal(dev_to_u16(p.grad).ravel(), acc[name].ravel()), name
-    for h in hooks + capture:
+    for h in hooks + capture + check:
         h.remove()
+
+
+def test_muon_fp32_gradients_vs_oracle(L, noise):
+    """fp32 gradients: the per-parameter path reads them as fp32 (the reference's prepare
+    kernel loads the gradient in its own dtype, muon_sr/triton_muon_sr.py:34); the
+    batch_ns path rounds them to bf16 first (it copies them into a bf16 stack, :150-152)."""
+    from muon_sr_amd import TritonMuonSR
+    from muon_sr_amd.muon import newton_schulz
+    noise("triton")
+    rng = np.random.default_rng(17)
+    shape = (256, 384)
+
+    def gpu_ns(U):
+        return dev_to_u16(newton_schulz(u16_to_dev(U.ravel()).view(U.shape))).reshape(U.shape)
+
+    for batch_ns in (False, True):
+        p0 = [O.f32_to_bf16_rne((rng.standard_normal(int(np.prod(shape))) * 0.02).astype(np.float32)).reshape(shape)
+              for _ in range(2)]
+        ps = [torch.nn.Parameter(u16_to_dev(x.ravel()).view(shape)) for x in p0]
+        for p in ps:
+            p.grad_dtype = None   # allow fp32 gradients on bf16 parameters (mixed-precision training)
+        opt = TritonMuonSR(ps, lr=0.02, weight_decay=0.01, batch_ns=batch_ns)
+        params, bufs = [x.copy() for x in p0], [np.zeros(shape, np.uint16) for _ in range(2)]
+        for step in (1, 2):
+            g32 = [(rng.standard_normal(int(np.prod(shape))) * 1e-3).astype(np.float32).reshape(shape)
+                   for _ in range(2)]
+            for p, g in zip(ps, g32):
+                p.grad = torch.from_numpy(g).to(DEV)
+            opt.step()
+            if batch_ns:
+                params, sb = O.muon_batch_step(params, [O.f32_to_bf16_rne(g.ravel()).reshape(shape) for g in g32],
+                                               {shape: np.stack(bufs)}, step, 0.02, 0.01, 0.95, True, gpu_ns,
+                                               O.NOISE_TRITON)
+                bufs = list(sb[shape])
+            else:
+                out = [O.muon_param_step(params[j], g32[j], bufs[j], step, j, 0.02, 0.01, 0.95, True, gpu_ns,
+                                         O.NOISE_TRITON) for j in range(2)]
+                params, bufs = [o[0] for o in out], [o[1] for o in out]
+            for j, p in enumerate(ps):
+                assert np.array_equal(dev_to_u16(p.data).ravel(), params[j].ravel()), (batch_ns, step, j)
+                assert np.array_equal(dev_to_u16(opt.state[p]["momentum_buffer"]).ravel(), bufs[j].ravel())
 
 
 # ---------------------------------------------------------------------------
@@ -518,6 +575,210 @@ def test_sr_unbiased(L, mode):
         assert set(np.unique(x)) <= {1.0, 1.0 + ulp}
         sigma = ulp * np.sqrt(prob * (1 - prob) / draws)
         assert abs(x.mean() - t) <= 3 * sigma, (f, x.mean() - t, sigma)
+
+
+# ---------------------------------------------------------------------------
+# Config 5's composition: the hybrid with batch_ns, a bf16 AdamW group and an
+# optim_bits=8 AdamW group, against the oracle chain
+# ---------------------------------------------------------------------------
+
+def _hybrid_oracle_step(step, pstate, grads, muon_idx, shapes, adam_idx, adam8_idx, mode, gpu_ns, hp):
+    """One TritonMuonSRWithAuxAdam(batch_ns=True) step composed from the oracle kernels,
+    following muon_sr/triton_muon_sr.py:128-177 (Muon, global step), :339-371 (AdamW,
+    per-parameter steps, seed index group_offset + i) and muon_sr/triton_adamw_8bit.py:
+    152-204 (8-bit states, seed (n * 2654435761 ^ idx * 1234567891))."""
+    # Muon: shape groups in first-occurrence order, every step counts (global step)
+    groups = {}
+    for i in muon_idx:
+        groups.setdefault(shapes[i], []).append(i)
+    for shape_idx, (shape, idxs) in enumerate(groups.items()):
+        active = [i for i in idxs if grads[i] is not None]
+        if not active:
+            continue
+        bufs = pstate["bufs"][shape]
+        if len(active) == len(idxs):
+            g = np.concatenate([grads[i].ravel() for i in idxs])
+            nb, _, u16 = O.muon_prepare(g, bufs.ravel(), hp["momentum"], True,
+                                        O.NoiseSpec(mode, O.deterministic_seed(step, shape_idx, 0)))
+            pstate["bufs"][shape] = nb.reshape(bufs.shape)
+            X = gpu_ns(u16.reshape(len(idxs), *shape))
+            for b, i in enumerate(idxs):
+                pstate["p"][i] = O.muon_apply(pstate["p"][i].ravel(), X[b].ravel(), hp["muon_lr"], hp["muon_wd"],
+                                              O.ns_scale(shape),
+                                              O.NoiseSpec(mode, O.deterministic_seed(step, shape_idx * 10000 + b, 1))
+                                              ).reshape(shape)
+        else:
+            for i in active:
+                b = idxs.index(i)
+                newp, nbuf = O.muon_param_step(pstate["p"][i], grads[i], bufs[b], step, shape_idx * 10000 + b,
+                                               hp["muon_lr"], hp["muon_wd"], hp["momentum"], True, gpu_ns, mode)
+                pstate["p"][i] = newp
+                bufs[b] = nbuf
+    b1, b2 = hp["betas"]
+    for i in adam_idx:          # bf16-moment AdamW, PyTorch order
+        if grads[i] is None:
+            continue
+        st = pstate["adam"].setdefault(i, dict(step=0, e=np.zeros(grads[i].size, np.uint16),
+                                              s=np.zeros(grads[i].size, np.uint16)))
+        st["step"] += 1
+        bc, bcs = O.adamw_bias_corrections(b1, b2, st["step"])
+        seed = O.deterministic_seed(st["step"], i)
+        pstate["p"][i], st["e"], st["s"] = O.adamw_bf16(
+            pstate["p"][i].ravel(), grads[i].ravel(), st["e"], st["s"], hp["lr"], b1, b2, hp["eps"], hp["wd"], bc, bcs,
+            O.NoiseSpec(mode, seed, 0), O.NoiseSpec(mode, seed, 1), O.NoiseSpec(mode, seed, 2))
+        pstate["p"][i] = pstate["p"][i].reshape(shapes[i])
+    Q1, Q2 = O.create_dynamic_map(True), O.create_dynamic_map(False)
+    for i in adam8_idx:         # blockwise 8-bit AdamW (16-bit moments below min_8bit_size)
+        if grads[i] is None:
+            continue
+        n = grads[i].size
+        quant = n >= 4096
+        if i not in pstate["adam8"]:
+            nb = -(-n // 256)
+            pstate["adam8"][i] = dict(step=0, s=(np.full(n, 127, np.uint8), np.zeros(n, np.uint8),
+                                                 np.zeros(nb, np.float32), np.zeros(nb, np.float32))
+                                      if quant else (np.zeros(n, np.uint16), np.zeros(n, np.uint16)))
+        st = pstate["adam8"][i]
+        st["step"] += 1
+        k = st["step"]
+        seed = (k * 2654435761 ^ i * 1234567891) & 0xFFFFFFFF
+        if quant:
+            out = O.adamw8bit(pstate["p"][i].ravel(), grads[i].ravel(), *st["s"], Q1, Q2, 256, True, hp["lr"], b1, b2,
+                              hp["eps"], hp["wd"], 1 - b1 ** k, 1 - b2 ** k, O.NoiseSpec(mode, seed))
+        else:
+            out = O.adamw8bit(pstate["p"][i].ravel(), grads[i].ravel(), *st["s"], None, None, None, None, 256, False,
+                              hp["lr"], b1, b2, hp["eps"], hp["wd"], 1 - b1 ** k, 1 - b2 ** k,
+                              O.NoiseSpec(mode, seed), O.NoiseSpec(mode, seed, 1), O.NoiseSpec(mode, seed, 2))
+        pstate["p"][i] = out[0].reshape(shapes[i])
+        st["s"] = tuple(out[1:])
+
+
+@pytest.mark.parametrize("mode_name", ["triton", "philox8"])
+def test_hybrid_batch_ns_with_8bit_group_vs_oracle(L, noise, mode_name):
+    """Config 5's step, small: TritonMuonSRWithAuxAdam(batch_ns=True) with a Muon group of
+    two shapes (one gradient missing in step 2, so that shape falls back to per-parameter
+    steps with index shape_idx * 10000 + i), a bf16 AdamW group (one gradient missing in
+    step 2) and an optim_bits=8 AdamW group (one tensor below min_8bit_size), 3 steps.
+    Bit-exact against the oracle chain, with this library's Newton-Schulz substituted."""
+    from muon_sr_amd import TritonMuonSRWithAuxAdam
+    from muon_sr_amd.muon import newton_schulz
+    noise(mode_name)
+    mode = O.NOISE_TRITON if mode_name == "triton" else O.NOISE_PHILOX8
+    rng = np.random.default_rng(5)
+    shapes = [(256, 512), (512, 256), (256, 512), (256, 512), (300,), (64, 100), (130, 301), (1000,)]
+    muon_idx, adam_idx, adam8_idx = [0, 1, 2, 3], [4, 5], [6, 7]
+    hp = dict(muon_lr=0.02, muon_wd=0.01, momentum=0.95, lr=3e-4, betas=(0.9, 0.95), eps=1e-10, wd=0.01)
+    p0 = [O.f32_to_bf16_rne((rng.standard_normal(int(np.prod(s))) * 0.02).astype(np.float32)).reshape(s)
+          for s in shapes]
+    ps = [torch.nn.Parameter(u16_to_dev(x.ravel()).view(s)) for x, s in zip(p0, shapes)]
+    opt = TritonMuonSRWithAuxAdam([
+        dict(params=[ps[i] for i in muon_idx], use_muon=True, lr=hp["muon_lr"], weight_decay=hp["muon_wd"]),
+        dict(params=[ps[i] for i in adam_idx], use_muon=False, lr=hp["lr"], betas=hp["betas"], eps=hp["eps"],
+             weight_decay=hp["wd"]),
+        dict(params=[ps[i] for i in adam8_idx], use_muon=False, lr=hp["lr"], betas=hp["betas"], eps=hp["eps"],
+             weight_decay=hp["wd"], optim_bits=8),
+    ], batch_ns=True)
+
+    def gpu_ns(U):
+        return dev_to_u16(newton_schulz(u16_to_dev(U.ravel()).view(U.shape))).reshape(U.shape)
+
+    pstate = dict(p=[x.copy() for x in p0], adam={}, adam8={},
+                  bufs={(256, 512): np.zeros((3, 256, 512), np.uint16), (512, 256): np.zeros((1, 512, 256), np.uint16)})
+    for step in (1, 2, 3):
+        grads = [O.f32_to_bf16_rne((rng.standard_normal(int(np.prod(s))) * 1e-3).astype(np.float32)).reshape(s)
+                 for s in shapes]
+        if step == 2:
+            grads[2] = None
+            grads[4] = None
+        for p, g in zip(ps, grads):
+            p.grad = None if g is None else u16_to_dev(g.ravel()).view(p.shape)
+        opt.step()
+        _hybrid_oracle_step(step, pstate, grads, muon_idx, shapes, adam_idx, adam8_idx, mode, gpu_ns, hp)
+        for i, p in enumerate(ps):
+            assert np.array_equal(dev_to_u16(p.data).ravel(), pstate["p"][i].ravel()), (step, i)
+        rows = {}
+        for i in muon_idx:
+            b = rows.get(shapes[i], 0)
+            rows[shapes[i]] = b + 1
+            assert opt.state[ps[i]]["step"] == step
+            assert np.array_equal(dev_to_u16(opt.state[ps[i]]["momentum_buffer"]).ravel(),
+                                  pstate["bufs"][shapes[i]][b].ravel()), (step, i)
+        for i in adam_idx:
+            if i in pstate["adam"]:
+                st = opt.state[ps[i]]
+                assert st["step"] == pstate["adam"][i]["step"]
+                assert np.array_equal(dev_to_u16(st["ema"]).ravel(), pstate["adam"][i]["e"]), (step, i)
+                assert np.array_equal(dev_to_u16(st["ema_squared"]).ravel(), pstate["adam"][i]["s"]), (step, i)
+        for i in adam8_idx:
+            st, exp = opt.state[ps[i]], pstate["adam8"][i]
+            assert st["step"] == exp["step"]
+            if st["optim_bits"] == 8:
+                got = (st["state1"].cpu().numpy().ravel(), st["state2"].cpu().numpy().ravel(),
+                       st["absmax1"].cpu().numpy(), st["absmax2"].cpu().numpy())
+            else:
+                got = (dev_to_u16(st["state1"]).ravel(), dev_to_u16(st["state2"]).ravel())
+            for a, b in zip(got, exp["s"]):
+                assert np.array_equal(a, b), (step, i)
+    assert opt._global_step == 3
+
+
+def test_hybrid_8bit_group_validation(L):
+    """The hybrid's optim_bits=8 groups validate as TritonAdamW8bit does on every step
+    (muon_sr/triton_adamw_8bit.py:175) and refuse a changed quantization configuration
+    (:192-194)."""
+    from muon_sr_amd import TritonMuonSRWithAuxAdam
+    p = torch.nn.Parameter(torch.zeros(64, 128, device=DEV, dtype=torch.bfloat16))
+    opt = TritonMuonSRWithAuxAdam([dict(params=[p], use_muon=False, optim_bits=8)])
+    p.grad = torch.full_like(p, 1e-3)
+    opt.step()
+    opt.param_groups[0]["block_size"] = 128
+    with pytest.raises(ValueError, match="Cannot change quantization configuration"):
+        opt.step()
+    opt.param_groups[0]["block_size"] = 256
+    opt.param_groups[0]["eps"] = -1.0
+    with pytest.raises(ValueError, match="eps"):
+        opt.step()
+    opt.param_groups[0]["eps"] = 1e-10
+    opt.param_groups[0]["optim_bits"] = 16
+    with pytest.raises(ValueError, match="Cannot change quantization configuration"):
+        opt.step()
+    opt.param_groups[0]["optim_bits"] = 8
+    opt.step()
+
+
+def test_adamw8bit_full_embedding_vs_oracle(L, noise):
+    """One 8-bit step at a Llama-3-8B embedding's full size (128256 x 4096 = 525,336,576
+    elements, 2,052,096 blocks) from a nonzero state, bit-exact against the C oracle
+    (reference noise stream)."""
+    from muon_sr_amd.adamw_8bit import adamw8bit_launch, init_8bit_state
+    noise("triton")
+    rows, cols = 128256, 4096
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(8)
+    p = (torch.randn(rows, cols, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+    g = (torch.randn(rows, cols, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16)
+    st = init_8bit_state(p, 256, 8, 4096, {})
+    st["state1"].copy_(torch.randint(0, 256, st["state1"].shape, device=DEV, generator=gen, dtype=torch.int32)
+                       .to(torch.uint8))
+    st["state2"].copy_(torch.randint(0, 256, st["state2"].shape, device=DEV, generator=gen, dtype=torch.int32)
+                       .to(torch.uint8))
+    st["absmax1"].copy_(torch.rand(st["absmax1"].shape, device=DEV, generator=gen) * 1e-3)
+    st["absmax2"].copy_(torch.rand(st["absmax2"].shape, device=DEV, generator=gen) * 1e-6)
+    host = [dev_to_u16(p).ravel(), dev_to_u16(g).ravel(), st["state1"].cpu().numpy().ravel(),
+            st["state2"].cpu().numpy().ravel(), st["absmax1"].cpu().numpy(), st["absmax2"].cpu().numpy()]
+    seed = (7 * 2654435761 ^ 1 * 1234567891) & 0xFFFFFFFF
+    pt = torch.nn.Parameter(p)
+    st["step"] = 7   # the 7th step (bias corrections 1 - b^7), as the class sets it before the launch
+    adamw8bit_launch(pt, g, st, 3e-4, 0.9, 0.95, 1e-10, 0.01, seed)
+    torch.cuda.synchronize()
+    b1, b2 = 0.9, 0.95
+    exp = O.adamw8bit(*host, O.create_dynamic_map(True), O.create_dynamic_map(False), 256, True, 3e-4, b1, b2, 1e-10,
+                      0.01, 1 - b1 ** 7, 1 - b2 ** 7, O.NoiseSpec(O.NOISE_TRITON, seed))
+    assert np.array_equal(dev_to_u16(pt.data).ravel(), exp[0])
+    assert np.array_equal(st["state1"].cpu().numpy().ravel(), exp[1])
+    assert np.array_equal(st["state2"].cpu().numpy().ravel(), exp[2])
+    assert np.array_equal(st["absmax1"].cpu().numpy(), exp[3])
+    assert np.array_equal(st["absmax2"].cpu().numpy(), exp[4])
 
 
 # ---------------------------------------------------------------------------

@@ -255,6 +255,26 @@ def test_muon_prepare_matches_reference(golden, nest):
     assert np.array_equal(u16, rne)
 
 
+def test_muon_prepare_fp32_gradient(golden):
+    """The fp32-gradient path (the reference's per-parameter launch reads the gradient in
+    its own dtype, muon_sr/triton_muon_sr.py:34): fp32 gradients holding bf16 values give
+    the reference vectors' results exactly, and other fp32 values are not rounded to bf16
+    first (an update computed from the bf16-rounded gradient differs)."""
+    z = golden("elementwise")
+    k = lambda s: z[f"prepare/1/{s}"]  # noqa: E731
+    g32 = (k("in_g").astype(np.uint32) << 16).view(np.float32)
+    spec = O.NoiseSpec(O.NOISE_TRITON, int(k("seed")))
+    buf, u32, _ = O.muon_prepare(g32, k("in_buf"), 0.95, True, spec)
+    assert np.array_equal(buf, k("out_buf"))
+    assert np.array_equal(u32.view(np.uint32), k("out_upd_f32").view(np.uint32))
+    rng = np.random.default_rng(0)
+    g = (rng.standard_normal(4096) * 1e-3).astype(np.float32)
+    b0 = O.f32_to_bf16_rne((rng.standard_normal(4096) * 1e-3).astype(np.float32))
+    _, u_f32, _ = O.muon_prepare(g, b0, 0.95, True, spec)
+    _, u_b16, _ = O.muon_prepare(O.f32_to_bf16_rne(g), b0, 0.95, True, spec)
+    assert (u_f32 != u_b16).mean() > 0.9
+
+
 def test_muon_apply_matches_reference(golden):
     z = golden("elementwise")
     out = O.muon_apply(z["apply/in_p"], z["apply/in_u"], 0.02, 0.01, float(z["apply/scale"]),

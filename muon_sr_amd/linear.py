@@ -11,7 +11,9 @@ the zero first buffer are those of the hook (:252-265).  The input gradient
 and the bias go through autograd as usual (the bias through the hook, if one
 is assigned).  Shapes or dtypes the fused kernel does not take (features not
 multiples of 256, token counts not multiples of 128, non-bf16 tensors) return
-``dW`` to autograd instead, so the hook accumulates it as for ``nn.Linear``.
+``dW`` to autograd instead, so the hook accumulates it as for ``nn.Linear``;
+so do operands the kernel cannot address (misaligned views, or an operand of
+2 GiB or more, e.g. an LM head's dy at 8,372 tokens or more).
 """
 import random
 
@@ -22,11 +24,26 @@ from . import _lib
 __all__ = ["linear_wgrad_sr_accum", "SRLinear"]
 
 
+def wgrad_shape_fits(out_f: int, in_f: int, tokens: int, ldx: int, ldy: int, x_ptr: int, dy_ptr: int) -> bool:
+    """Every precondition msr_linear_wgrad_sr_accum checks on its operands (host-only):
+    features multiples of 256 and tokens a multiple of 128 (each below 2^30); x and dy
+    16-byte aligned with row strides that are multiples of 8 elements and at least the
+    row length; and each operand spanning less than 2 GiB, since its loads address it
+    with 32-bit byte offsets ((tokens - 1) * ld + features elements)."""
+    if not (0 < tokens < (1 << 30) and 0 < in_f < (1 << 30) and 0 < out_f < (1 << 30)):
+        return False
+    if in_f % 256 or out_f % 256 or tokens % 128:
+        return False
+    if ldx < in_f or ldy < out_f or ldx % 8 or ldy % 8 or x_ptr % 16 or dy_ptr % 16:
+        return False
+    return ((tokens - 1) * ldx + in_f) * 2 < (1 << 31) and ((tokens - 1) * ldy + out_f) * 2 < (1 << 31)
+
+
 def _fits(weight: torch.Tensor, x2: torch.Tensor, dy2: torch.Tensor) -> bool:
     out_f, in_f = weight.shape
     return (weight.dtype == x2.dtype == dy2.dtype == torch.bfloat16 and x2.is_cuda and
-            in_f % 256 == 0 and out_f % 256 == 0 and x2.shape[0] % 128 == 0 and x2.shape[0] > 0 and
-            x2.stride(1) == 1 and dy2.stride(1) == 1)
+            x2.stride(1) == 1 and dy2.stride(1) == 1 and x2.shape[0] == dy2.shape[0] and
+            wgrad_shape_fits(out_f, in_f, x2.shape[0], x2.stride(0), dy2.stride(0), x2.data_ptr(), dy2.data_ptr()))
 
 
 def linear_wgrad_sr_accum(weight: torch.Tensor, x2: torch.Tensor, dy2: torch.Tensor, seed: int = None) -> bool:

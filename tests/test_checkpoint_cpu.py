@@ -58,3 +58,4 @@ def test_hybrid_rejects_incompatible_8bit_state():
     sd["state"] = {0: bad}
     with pytest.raises(ValueError, match="Incompatible state format"):
         opt.load_state_dict(sd)
+

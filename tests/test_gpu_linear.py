@@ -148,3 +148,22 @@ def test_sr_linear_edge_cases(L):
     assert f.weight.grad is not None and not hasattr(f.weight, "acc_grad")
     torch.testing.assert_close(f.weight.grad, torch.ones(128, 256, device=DEV).t() @ xf.detach(), rtol=1e-5, atol=1e-4)
     assert xf.grad is not None and f.bias.grad is not None
+
+
+def test_sr_linear_falls_back_on_unaddressable_operands(L):
+    """A misaligned activation view fails the fused kernel's 16-byte alignment: the
+    predicate sends it to the unfused path (dW returned to autograd) instead of letting
+    msr_linear_wgrad_sr_accum raise inside backward."""
+    from muon_sr_amd import SRLinear
+    from muon_sr_amd.linear import linear_wgrad_sr_accum
+    w = torch.zeros(256, 256, device=DEV, dtype=torch.bfloat16)
+    buf = torch.randn(128 * 256 + 1, device=DEV).to(torch.bfloat16)
+    x2 = buf[1:].view(128, 256)                      # 2-byte misaligned
+    dy2 = torch.randn(128, 256, device=DEV).to(torch.bfloat16)
+    assert not linear_wgrad_sr_accum(w, x2, dy2) and not hasattr(w, "acc_grad")
+    m = SRLinear(256, 256, bias=False).to(DEV).to(torch.bfloat16)
+    x = buf[1:].view(128, 256).requires_grad_(False)
+    m(x).float().sum().backward()
+    assert m.weight.grad is not None and not hasattr(m.weight, "acc_grad")
+    torch.testing.assert_close(m.weight.grad.float(), torch.ones(256, 128, device=DEV) @ x.float(), rtol=2 ** -7,
+                               atol=1e-3)

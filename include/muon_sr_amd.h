@@ -212,6 +212,26 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
                       msr_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * (b) Newton-Schulz and the Muon parameter update in one pass.
+ * Replaces the _newton_schulz call and the _run_apply launches of one chunk of
+ * _triton_muon_batch_step (muon_sr/triton_muon_sr.py:160-169), and of
+ * _triton_muon_step (:116-120) with batch == 1.  Equal, bit for bit, to
+ * msr_newton_schulz(upd -> X) followed by msr_muon_apply(params, X, ...), but
+ * the last product's store applies the update to the parameters directly: X is
+ * never written and the apply pass does not run.
+ *   upd:    bf16 pre-NS update stack [batch][rows][cols] (read only)
+ *   params: HOST array of `batch` device pointers, each to rows*cols bf16
+ *   seeds:  HOST array of `batch` seeds (salt-1 deterministic seeds)
+ *   p <- SR(p*(1-lr*wd) - lr*(f32(bf16(X))*scale)), noise offset = element index in p.
+ * steps >= 1; workspace as msr_ns_workspace_bytes(batch, rows, cols).
+ * inject: uint16 [batch][rows*cols].
+ * ------------------------------------------------------------------------- */
+int msr_muon_ns_apply(const uint16_t *upd, uint16_t *const *params, const uint32_t *seeds, int64_t batch,
+                      int64_t rows, int64_t cols, int32_t steps, float a, float b, float c, float lr,
+                      float weight_decay, float scale, int32_t noise_mode, const uint16_t *inject,
+                      void *workspace, size_t workspace_bytes, msr_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Diagnostics (no counterpart in the reference; used by the parity tests).
  * ------------------------------------------------------------------------- */
 

@@ -45,6 +45,17 @@ constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int GEMM_THREADS = 512;
 constexpr int CHUNKS = BM * BK / 8;  // 16-byte chunks per operand slab (2048)
 
+// Muon apply fused into the store of the last Newton-Schulz product
+// (msr_muon_ns_apply): matrix b of a launch updates params p[b] with seed[b].
+constexpr int APPLY_MAX = 128;   // matrices per launch (kernel-argument table)
+struct ApplyTab {
+    uint16_t *p[APPLY_MAX];
+    uint32_t seed[APPLY_MAX];
+    const uint16_t *inject;      // uint16 [count][numel] of this launch (NOISE_INJECT), or null
+    int64_t numel;
+    float lr, decay, scale;      // decay = 1 - lr * wd
+};
+
 struct GemmArgs {
     const uint16_t *P; int64_t ldp, sP;
     const uint16_t *Q; int64_t ldq, sQ;
@@ -70,7 +81,54 @@ struct GemmArgs {
     float *resid;           // EPI_A, EPI_B: fp32 rounding residual of each diagonal element, [batch][sv]
     const float *rvec;      // EPI_B: residuals of A's diagonal; EPI_X: residuals of B''s diagonal, [batch][sv]
     int64_t sv;             // batch stride of resid and rvec
+    int apply1;             // 0, or 1 + the noise mode of the fused apply store (then D / DT only mark the layout)
+    ApplyTab ap;            // apply1 > 0: the parameters the D / DT store updates instead of writing
 };
+
+// p[off + j] <- SR(p*(1 - lr*wd) - lr*(f32(u_j)*scale)) for the j < valid bf16 values u
+// (packed in u[4]) of one 8-element chunk: the arithmetic and noise of
+// muon_apply_kernel (muon_sr/triton_muon_sr.py:53-80); off is the element index in p.
+// vec: the chunk is 16-byte aligned and off a multiple of 8.
+// The parameter chunk of apply_chunk (loaded ahead so that the loads of a thread's
+// chunks overlap).
+__device__ __forceinline__ u32x4_t apply_load(const uint16_t *P, int64_t off, int valid, bool vec) {
+    if (vec && valid == 8) return ld_nt4(P + off);
+    uint32_t wp[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        if (j < valid) wp[j >> 1] |= (uint32_t)P[off + j] << (16 * (j & 1));
+    return u32x4_t{wp[0], wp[1], wp[2], wp[3]};
+}
+
+template <int MODE>
+__device__ __forceinline__ void apply_chunk(const ApplyTab &ap, uint16_t *P, const Noise &ns, int64_t off, int valid,
+                                            bool vec, const uint32_t u[4], u32x4_t pw) {
+    const uint32_t wp[4] = {pw.x, pw.y, pw.z, pw.w};
+    uint32_t r[8];
+    if (vec && valid == 8) {
+        noise8<MODE>(ns, off, 8, r);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = j < valid ? noise1<MODE>(ns, off + j) : 0u;
+    }
+    uint32_t op[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float uf = (j & 1) ? bf16_hi(u[j >> 1]) : bf16_lo(u[j >> 1]);
+        const float pf = (j & 1) ? bf16_hi(wp[j >> 1]) : bf16_lo(wp[j >> 1]);
+        const float t1 = uf * ap.scale;                                   // :70
+        float pj = pf * ap.decay;                                         // :72
+        pj = pj - ap.lr * t1;                                             // :73
+        op[j] = sr_bf16(pj, r[j]);                                        // :75-80
+    }
+    if (vec && valid == 8) {
+        st_nt4(P + off, u32x4_t{pack2(op[0], op[1]), pack2(op[2], op[3]), pack2(op[4], op[5]), pack2(op[6], op[7])});
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (j < valid) P[off + j] = (uint16_t)op[j];
+    }
+}
 
 // Work-group -> (matrix, tile).  Consecutive work-group ids are dispatched
 // round-robin over the 8 XCDs (each with its own L2), so tiles that share
@@ -190,7 +248,9 @@ enum : int { EPI_NONE = 0, EPI_A = 1, EPI_B = 2, EPI_X = 3 };
 
 // SRACC >= 0: D is a bf16 accumulator and the store adds to it with stochastic
 // rounding (noise mode SRACC), as msr_sr_accum does with the RNE bf16 product.
-template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, int GM, int SRACC = -1, int EPI = EPI_NONE>
+// APPLY >= 0 (with OUT_D or OUT_DT): the store applies the Muon update to the
+// parameters of a.ap with noise mode APPLY instead of writing D / DT.
+template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, int GM, int SRACC = -1, int EPI = EPI_NONE, int APPLY = -1>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     int ti, tj;
     int64_t bz;
@@ -568,6 +628,23 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
                              sr_bf16(bf16_hi(cw[j]) + bf16_hi(gw[j]), rn[2 * j + 1]));
             *reinterpret_cast<uint4 *>(Db + o0) = make_uint4(o[0], o[1], o[2], o[3]);
         }
+    } else if constexpr (OUT_D && APPLY >= 0) {
+        uint16_t *Pp = a.ap.p[bz];
+        Noise ns;
+        ns.key = seed_key(a.ap.seed[bz], 0);
+        ns.inject = a.ap.inject ? a.ap.inject + bz * a.ap.numel : nullptr;
+        const int n = n0 + 8 * ec;
+#pragma unroll 2
+        for (int it = 0; it < 16; ++it) {
+            const int r = er + 16 * it;
+            const int m = m0 + r;
+            if (m >= a.Mv || n >= a.Nv) continue;
+            const uint4 w = *reinterpret_cast<const uint4 *>(stg_row(r) + 8 * ec);
+            const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+            const int64_t off = (int64_t)m * a.ldd + n;
+            const int valid = min(8, a.Nv - n);
+            apply_chunk<APPLY>(a.ap, Pp, ns, off, valid, a.d_vec != 0, u, apply_load(Pp, off, valid, a.d_vec != 0));
+        }
     } else if constexpr (OUT_D) {
         uint16_t *Db = a.D + bz * a.sD;
 #pragma unroll 4
@@ -590,7 +667,33 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     // Transposed copy: T[n][m] = tile[m][n].  Lanes of a wave take 64
     // consecutive n (a conflict-free LDS row read per element) and each stores
     // 8 consecutive m (16 bytes) of its row n.
-    if constexpr (OUT_DT) {
+    if constexpr (OUT_DT && APPLY >= 0) {
+        uint16_t *Pp = a.ap.p[bz];
+        Noise ns;
+        ns.key = seed_key(a.ap.seed[bz], 0);
+        ns.inject = a.ap.inject ? a.ap.inject + bz * a.ap.numel : nullptr;
+        const int nl = tid & 255;
+        const int n = n0 + nl;
+        const int c0 = (tid >> 8) * 16;
+        u32x4_t pw[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int m = m0 + 8 * (c0 + i);
+            pw[i] = (n < a.Nv && m < a.Mv) ? apply_load(Pp, (int64_t)n * a.lddt + m, min(8, a.Mv - m), a.dt_vec != 0)
+                                           : u32x4_t{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int c = c0 + i;
+            uint32_t u[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                u[j] = (uint32_t)stg_row(8 * c + 2 * j)[nl] | ((uint32_t)stg_row(8 * c + 2 * j + 1)[nl] << 16);
+            const int m = m0 + 8 * c;
+            if (n >= a.Nv || m >= a.Mv) continue;
+            apply_chunk<APPLY>(a.ap, Pp, ns, (int64_t)n * a.lddt + m, min(8, a.Mv - m), a.dt_vec != 0, u, pw[i]);
+        }
+    } else if constexpr (OUT_DT) {
         uint16_t *Tb = a.DT + bz * a.sDT;
         const int64_t ldt = a.lddt;
         const int tm0 = m0, tn0 = n0, tMv = a.Mv, tNv = a.Nv;
@@ -874,6 +977,13 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
     a.tiles_n = a.N / BN;
     a.d_vec = a.D && aligned(a.D, 16) && (a.ldd % 8) == 0 && (a.sD % 8) == 0;
     a.dt_vec = a.DT && aligned(a.DT, 16) && (a.lddt % 8) == 0 && (a.sDT % 8) == 0;
+    if (a.apply1) {   // the store goes to the parameters of the table, each its own allocation
+        if (batch > APPLY_MAX) { set_error("gemm: more than %d matrices in an apply launch", APPLY_MAX); return MSR_ERR_ARG; }
+        bool al = true;
+        for (int64_t i = 0; i < batch; ++i) al = al && aligned(a.ap.p[i], 16);
+        a.d_vec = a.D && al && (a.ldd % 8) == 0;
+        a.dt_vec = a.DT && al && (a.lddt % 8) == 0;
+    }
     const int64_t tiles = a.symmetric ? (int64_t)a.tiles_m * (a.tiles_m + 1) / 2 : (int64_t)a.tiles_m * a.tiles_n;
     a.tiles = (int)tiles;
     auto launch = [&](const GemmArgs &ab, dim3 grid) {
@@ -889,7 +999,11 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
             else { set_error("gemm: unsupported symmetric product"); return (int)MSR_ERR_ARG; }
         } else if (gm == GM_TRI_P) {   // X' = B' X + r X: D = X', or DT = X'^T for the tall output
             if (!ab.rvec) { set_error("gemm: X' = B' X needs the diagonal residuals"); return (int)MSR_ERR_ARG; }
-            if (!c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P, -1, EPI_X>), grid, block, 0, s, ab);
+            if (ab.apply1 > 0) {   // the last product of msr_muon_ns_apply: D / DT are the parameters
+                if (c || d == dt) { set_error("gemm: unsupported apply epilogue"); return (int)MSR_ERR_ARG; }
+                if (d) { MSR_DISPATCH_NOISE(ab.apply1 - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P, -1, EPI_X, M>), grid, block, 0, s, ab)); }
+                else { MSR_DISPATCH_NOISE(ab.apply1 - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, false, true, GM_TRI_P, -1, EPI_X, M>), grid, block, 0, s, ab)); }
+            } else if (!c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P, -1, EPI_X>), grid, block, 0, s, ab);
             else if (!c && !d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, false, true, GM_TRI_P, -1, EPI_X>), grid, block, 0, s, ab);
             else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
         } else if (gm == GM_RK) {   // msr_gemm_nn
@@ -916,6 +1030,13 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
         if (ab.alpha_b) ab.alpha_b += b0;
         if (ab.resid) ab.resid += b0 * a.sv;
         if (ab.rvec) ab.rvec += b0 * a.sv;
+        if (ab.apply1) {   // the launch's matrix 0 is matrix b0 of the table (batch <= APPLY_MAX)
+            for (int64_t i = 0; i + b0 < APPLY_MAX; ++i) {
+                ab.ap.p[i] = a.ap.p[i + b0];
+                ab.ap.seed[i] = a.ap.seed[i + b0];
+            }
+            if (ab.ap.inject) ab.ap.inject += b0 * a.ap.numel;
+        }
         return ab;
     };
     // whole matrices per XCD for the largest multiple of 8 matrices (1-D grids
@@ -1036,28 +1157,23 @@ int msr_ns_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, size_t *by
     return MSR_OK;
 }
 
-int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows, int64_t cols, int32_t steps,
-                      float a_coef, float b_coef, float c_coef, void *workspace, size_t workspace_bytes,
-                      msr_stream_t stream) {
-    if (!in || !out || batch < 0 || rows <= 0 || cols <= 0 || steps < 0) { set_error("msr_newton_schulz: bad arguments"); return MSR_ERR_ARG; }
-    if (batch == 0) return MSR_OK;
-    const NSLayout L = ns_layout(batch, rows, cols);
-    if (!workspace || workspace_bytes < L.total) {
-        set_error("msr_newton_schulz: workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
-        return MSR_ERR_WORKSPACE;
-    }
-    if (L.mp > (1 << 30) || L.np > (1 << 30)) { set_error("msr_newton_schulz: matrix too large"); return MSR_ERR_ARG; }
-    {
-        // the input is consumed before the output is written, so in and out may
-        // share memory; neither may share the workspace
-        const uintptr_t w = (uintptr_t)workspace, i0 = (uintptr_t)in, o0 = (uintptr_t)out;
-        const size_t io = 2 * (size_t)batch * (size_t)rows * (size_t)cols;
-        if ((w < i0 + io && i0 < w + L.total) || (w < o0 + io && o0 < w + L.total)) {
-            set_error("msr_newton_schulz: the workspace overlaps the input or the output");
-            return MSR_ERR_OVERLAP;
-        }
-    }
-    hipStream_t s = (hipStream_t)stream;
+}  // extern "C"
+
+// The fused Muon apply of msr_muon_ns_apply (host tables of `batch` entries).
+struct NSApply {
+    uint16_t *const *params;
+    const uint32_t *seeds;
+    float lr, weight_decay, scale;
+    int noise_mode;
+    const uint16_t *inject;
+};
+
+// Newton-Schulz of `batch` matrices; with `ap`, the last product updates the
+// parameters instead of writing `out` (which is then unused).  Arguments are
+// validated by the callers.
+static int ns_run(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows, int64_t cols, int32_t steps,
+                  float a_coef, float b_coef, float c_coef, void *workspace, const NSLayout &L, hipStream_t s,
+                  const NSApply *ap) {
     char *ws = static_cast<char *>(workspace);
     uint16_t *X[2] = {(uint16_t *)(ws + L.off_x[0]), (uint16_t *)(ws + L.off_x[1])};
     uint16_t *A = (uint16_t *)(ws + L.off_a);
@@ -1160,10 +1276,106 @@ int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t 
             g.DT = out; g.lddt = cols; g.sDT = numel;  // out[n][m], n = rows, m = cols
             g.Mv = (int)L.m; g.Nv = (int)L.n;
         }
-        if ((rc = launch_gemm(g, batch, s))) return rc;
+        if (last && ap) {
+            // the store updates params[b] (the layout of out) in launches of up to APPLY_MAX matrices
+            g.apply1 = 1 + ap->noise_mode;
+            g.ap.numel = numel;
+            g.ap.lr = ap->lr;
+            g.ap.decay = 1.0f - ap->lr * ap->weight_decay;          // :72
+            g.ap.scale = ap->scale;
+            for (int64_t b0 = 0; b0 < batch; b0 += APPLY_MAX) {
+                const int64_t nb = std::min<int64_t>(APPLY_MAX, batch - b0);
+                GemmArgs ga = g;
+                ga.P += b0 * g.sP;
+                ga.Q += b0 * g.sQ;
+                ga.alpha_b = g.alpha_b ? g.alpha_b + b0 : nullptr;
+                ga.rvec += b0 * g.sv;
+                for (int64_t i = 0; i < nb; ++i) {
+                    ga.ap.p[i] = ap->params[b0 + i];
+                    ga.ap.seed[i] = ap->seeds[b0 + i];
+                }
+                ga.ap.inject = ap->inject ? ap->inject + b0 * numel : nullptr;
+                if ((rc = launch_gemm(ga, nb, s))) return rc;
+            }
+        } else if ((rc = launch_gemm(g, batch, s))) {
+            return rc;
+        }
         cur ^= 1;
     }
     return MSR_OK;
+}
+
+extern "C" {
+
+int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows, int64_t cols, int32_t steps,
+                      float a_coef, float b_coef, float c_coef, void *workspace, size_t workspace_bytes,
+                      msr_stream_t stream) {
+    if (!in || !out || batch < 0 || rows <= 0 || cols <= 0 || steps < 0) { set_error("msr_newton_schulz: bad arguments"); return MSR_ERR_ARG; }
+    if (batch == 0) return MSR_OK;
+    const NSLayout L = ns_layout(batch, rows, cols);
+    if (!workspace || workspace_bytes < L.total) {
+        set_error("msr_newton_schulz: workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
+        return MSR_ERR_WORKSPACE;
+    }
+    if (L.mp > (1 << 30) || L.np > (1 << 30)) { set_error("msr_newton_schulz: matrix too large"); return MSR_ERR_ARG; }
+    {
+        // the input is consumed before the output is written, so in and out may
+        // share memory; neither may share the workspace
+        const uintptr_t w = (uintptr_t)workspace, i0 = (uintptr_t)in, o0 = (uintptr_t)out;
+        const size_t io = 2 * (size_t)batch * (size_t)rows * (size_t)cols;
+        if ((w < i0 + io && i0 < w + L.total) || (w < o0 + io && o0 < w + L.total)) {
+            set_error("msr_newton_schulz: the workspace overlaps the input or the output");
+            return MSR_ERR_OVERLAP;
+        }
+    }
+    return ns_run(in, out, batch, rows, cols, steps, a_coef, b_coef, c_coef, workspace, L, (hipStream_t)stream, nullptr);
+}
+
+int msr_muon_ns_apply(const uint16_t *upd, uint16_t *const *params, const uint32_t *seeds, int64_t batch, int64_t rows,
+                      int64_t cols, int32_t steps, float a_coef, float b_coef, float c_coef, float lr,
+                      float weight_decay, float scale, int32_t noise_mode, const uint16_t *inject, void *workspace,
+                      size_t workspace_bytes, msr_stream_t stream) {
+    if (!upd || batch < 0 || rows <= 0 || cols <= 0 || steps < 1 || (batch > 0 && (!params || !seeds))) {
+        set_error("msr_muon_ns_apply: bad arguments (steps must be >= 1)");
+        return MSR_ERR_ARG;
+    }
+    if (noise_mode < 0 || noise_mode > 2 || (noise_mode == NOISE_INJECT && !inject)) {
+        set_error("msr_muon_ns_apply: bad noise_mode %d", (int)noise_mode);
+        return MSR_ERR_ARG;
+    }
+    if (batch == 0) return MSR_OK;
+    const NSLayout L = ns_layout(batch, rows, cols);
+    if (!workspace || workspace_bytes < L.total) {
+        set_error("msr_muon_ns_apply: workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
+        return MSR_ERR_WORKSPACE;
+    }
+    if (L.mp > (1 << 30) || L.np > (1 << 30)) { set_error("msr_muon_ns_apply: matrix too large"); return MSR_ERR_ARG; }
+    {
+        // the parameters are written while the update stack and the workspace are read: no
+        // parameter may share memory with them or with another parameter
+        const size_t pb = 2 * (size_t)rows * (size_t)cols, ub = pb * (size_t)batch;
+        auto touch = [](const void *x, size_t nx, const void *y, size_t ny) {
+            return (uintptr_t)x < (uintptr_t)y + ny && (uintptr_t)y < (uintptr_t)x + nx;
+        };
+        if (touch(upd, ub, workspace, L.total)) {
+            set_error("msr_muon_ns_apply: the workspace overlaps the update stack");
+            return MSR_ERR_OVERLAP;
+        }
+        for (int64_t i = 0; i < batch; ++i) {
+            if (!params[i]) { set_error("msr_muon_ns_apply: null parameter pointer %lld", (long long)i); return MSR_ERR_ARG; }
+            bool race = touch(params[i], pb, upd, ub) || touch(params[i], pb, workspace, L.total);
+            for (int64_t j = 0; j < i && !race; ++j) race = touch(params[i], pb, params[j], pb);
+            if (race) {
+                set_error("msr_muon_ns_apply: parameter %lld overlaps another parameter, the update stack or the workspace",
+                          (long long)i);
+                return MSR_ERR_OVERLAP;
+            }
+        }
+    }
+    NSApply ap{params, seeds, lr, weight_decay, scale, (int)noise_mode, inject};
+    // `out` only marks the output layout for the last product: the store writes params[b]
+    return ns_run(upd, const_cast<uint16_t *>(upd), batch, rows, cols, steps, a_coef, b_coef, c_coef, workspace, L,
+                  (hipStream_t)stream, &ap);
 }
 
 }  // extern "C"

@@ -6,11 +6,12 @@ constructor signatures, param-group keys, state keys (``step``,
 ``momentum_buffer``; ``ema``/``ema_squared`` for AdamW groups), seeds,
 shape-group order and checkpoint behaviour.
 
-One Muon step of a shape group runs three library calls:
-  prepare  momentum lerp + nesterov, SR store of the momentum stack, RNE bf16
-           update (grads read through a pointer table: no stack copy);
-  NS       batched Newton-Schulz on bf16 MFMA (msr_newton_schulz);
-  apply    p <- SR(p*(1-lr*wd) - lr*scale*update) for every matrix of a chunk.
+One Muon step of a shape group runs two library calls:
+  prepare   momentum lerp + nesterov, SR store of the momentum stack, RNE bf16
+            update (grads read through a pointer table: no stack copy);
+  NS+apply  batched Newton-Schulz on bf16 MFMA whose last product applies
+            p <- SR(p*(1-lr*wd) - lr*scale*update) to every matrix of a chunk
+            (msr_muon_ns_apply: the NS output is never written).
 
 Extension (additive, off by default): an AdamW group of the hybrid optimizer
 with ``optim_bits=8`` runs the blockwise 8-bit AdamW of TritonAdamW8bit
@@ -121,6 +122,32 @@ def _run_apply(params, upd_stack, lr, weight_decay, scale, seeds):
     _lib.check(rc, "msr_muon_apply")
 
 
+def _ns_apply(upd_stack, params, lr, weight_decay, scale, seeds, ns_steps):
+    """Newton-Schulz of `upd_stack` [k, *param shape] and the Muon update of the k
+    parameters: the reference's _newton_schulz + _run_apply per parameter
+    (muon_sr/triton_muon_sr.py:105-120, 160-169).  For wide matrices (rows <= cols)
+    this is one library call (msr_muon_ns_apply) whose last product applies the update
+    (no NS output is written).  Tall matrices, whose last product stores transposed
+    (the fused apply measured 6-10 % slower there), parameters of more than 2 dims (NS
+    over their leading dims as a batch, one apply over the whole tensor) and
+    ns_steps = 0 (NS is then only the bf16 normalisation) run the two calls
+    separately; the results are the same bit for bit."""
+    if ns_steps < 1 or upd_stack.dim() != 3 or upd_stack.shape[1] > upd_stack.shape[2]:
+        _run_apply(params, newton_schulz(upd_stack, steps=ns_steps), lr, weight_decay, scale, seeds)
+        return
+    L = _lib.lib()
+    k, rows, cols = upd_stack.shape
+    nbytes = _lib.ctypes.c_size_t(0)
+    _lib.check(L.msr_ns_workspace_bytes(k, rows, cols, _lib.ctypes.byref(nbytes)), "msr_ns_workspace_bytes")
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=upd_stack.device)
+    a, b, c = NS_COEFFS
+    table = _lib.ptr_array([p.data_ptr() for p in params])
+    seed_arr = _lib.ptr_array(seeds, _lib.ctypes.c_uint32)
+    rc = L.msr_muon_ns_apply(upd_stack.data_ptr(), table, seed_arr, k, rows, cols, ns_steps, a, b, c, lr, weight_decay,
+                             scale, _lib.noise_mode(), None, ws.data_ptr(), nbytes.value, _lib.stream_of(upd_stack))
+    _lib.check(rc, "msr_muon_ns_apply")
+
+
 def _check_param(p, name):
     _lib.require_gpu(p, name, RuntimeError)
     if not p.is_contiguous():
@@ -132,9 +159,8 @@ def _muon_step(p, grad, buf, beta, nesterov, ns_steps, lr, weight_decay, step, p
     grad = _grad_operand(grad)
     update = torch.empty(p.shape, dtype=torch.bfloat16, device=p.device)
     _run_prepare([grad], buf, update, beta, nesterov, _deterministic_seed(step, param_idx, salt=0))
-    update_ns = newton_schulz(update, steps=ns_steps)
-    _run_apply([p.data], update_ns, lr, weight_decay, _ns_scale(update_ns.shape),
-               [_deterministic_seed(step, param_idx, salt=1)])
+    _ns_apply(update.unsqueeze(0), [p.data], lr, weight_decay, _ns_scale(p.shape),
+              [_deterministic_seed(step, param_idx, salt=1)], ns_steps)
 
 
 def _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns_steps, lr, weight_decay, step):
@@ -163,11 +189,9 @@ def _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns
             k = max(1, NS_BATCH_NUMEL // work[0].numel())
             scale = _ns_scale(shape)
             for start in range(0, Na, k):
-                update_ns = newton_schulz(work[start:start + k], steps=ns_steps)
                 chunk = ordered[start:start + k]
                 seeds = [_deterministic_seed(step, shape_idx * 10000 + start + j, salt=1) for j in range(len(chunk))]
-                _run_apply([p.data for p in chunk], update_ns, lr, weight_decay, scale, seeds)
-                del update_ns
+                _ns_apply(work[start:start + k], [p.data for p in chunk], lr, weight_decay, scale, seeds, ns_steps)
             del work
         else:
             for p in active:

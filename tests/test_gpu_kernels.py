@@ -764,3 +764,48 @@ def test_newton_schulz_batch_invariant_and_steps0(L):
     nrm = G.float().norm(dim=(-2, -1), keepdim=True).to(torch.bfloat16).float()
     exp = (G.float() / (nrm + 1e-7).to(torch.bfloat16).float()).to(torch.bfloat16).float()
     assert rel_fro(X0, exp) < 1e-2
+
+
+@pytest.mark.parametrize("batch,rows,cols", [(3, 256, 512), (2, 640, 256), (3, 100, 60), (130, 256, 256), (2, 61, 99)])
+@pytest.mark.parametrize("mode", [O.NOISE_TRITON, O.NOISE_PHILOX8, O.NOISE_INJECT])
+def test_muon_ns_apply_equals_ns_then_apply(L, batch, rows, cols, mode):
+    """msr_muon_ns_apply (the apply done by the last Newton-Schulz product's store) equals
+    msr_newton_schulz followed by msr_muon_apply bit for bit: wide, tall and padded shapes,
+    columns that are no multiple of 8 (element-wise stores and noise), more than 128
+    matrices (several apply launches) and misaligned parameters."""
+    import ctypes
+    from muon_sr_amd.muon import newton_schulz, NS_COEFFS
+    a, b, c = NS_COEFFS
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(batch * rows + cols + mode)
+    U = (torch.randn(batch, rows, cols, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16)
+    numel = rows * cols
+    misalign = (batch % 2 == 1)
+    store = torch.randn(batch * (numel + 8), device=DEV, generator=gen).mul(0.02).to(torch.bfloat16)
+    # parameter i at element offset i*(numel+8) (+1 for odd i when misaligned)
+    offs = [i * (numel + 8) + (1 if misalign and i % 2 else 0) for i in range(batch)]
+    p_ref = [store[o:o + numel].clone() for o in offs]
+    seeds = [(0x9E3779B9 * (i + 1)) & 0xFFFFFFFF for i in range(batch)]
+    inj = torch.randint(0, 65536, (batch * numel,), device=DEV, generator=gen, dtype=torch.int32).to(torch.int16) \
+        if mode == O.NOISE_INJECT else None
+    lr, wd, scale = 0.02, 0.01, max(1.0, rows / cols) ** 0.5
+    X = newton_schulz(U)
+    pref_stack = torch.stack(p_ref)
+    seeds_c = ptr_array(seeds, ctypes.c_uint32)
+    check(L, L.msr_muon_apply(ptr_array([t.data_ptr() for t in pref_stack]), X.data_ptr(), numel, batch, lr, wd, scale,
+                              seeds_c, mode, ptr(inj), stream()), "msr_muon_apply")
+    nb = ctypes.c_size_t(0)
+    check(L, L.msr_ns_workspace_bytes(batch, rows, cols, ctypes.byref(nb)), "ws")
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    params = [store[o:o + numel] for o in offs]
+    before = store.clone()
+    check(L, L.msr_muon_ns_apply(U.data_ptr(), ptr_array([t.data_ptr() for t in params]), seeds_c, batch, rows, cols, 5,
+                                 a, b, c, lr, wd, scale, mode, ptr(inj), ws.data_ptr(), nb.value, stream()),
+          "msr_muon_ns_apply")
+    for i in range(batch):
+        assert torch.equal(params[i].view(torch.int16), pref_stack[i].view(torch.int16)), i
+    # memory between and around the parameters is untouched
+    mask = torch.ones(store.numel(), dtype=torch.bool, device=DEV)
+    for o in offs:
+        mask[o:o + numel] = False
+    assert torch.equal(store[mask].view(torch.int16), before[mask].view(torch.int16))

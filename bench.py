@@ -44,12 +44,12 @@ def sync():
 
 class LaunchTimer:
     """HIP events recorded on the launch stream immediately before and after
-    every call of one C-ABI entry point, so the pair brackets that launch (and
-    not the Python work of the optimizer step around it)."""
+    every call of the named C-ABI entry points, so each pair brackets that
+    launch (and not the Python work of the optimizer step around it)."""
 
-    def __init__(self, name):
+    def __init__(self, *names):
         from muon_sr_amd import _lib
-        self.name = name
+        self.names = set(names)
         self.real = _lib.lib()
         self.pairs = []
         self.on = False
@@ -58,7 +58,7 @@ class LaunchTimer:
         class Proxy:
             def __getattr__(self, attr):
                 fn = getattr(timer.real, attr)
-                if attr != timer.name:
+                if attr not in timer.names:
                     return fn
 
                 def timed(*args):
@@ -87,6 +87,10 @@ class LaunchTimer:
 
     def mean_ms(self):
         return self.total_ms() / max(1, len(self.pairs))
+
+    def median_ms(self):
+        ts = sorted(s.elapsed_time(e) for s, e in self.pairs)
+        return ts[len(ts) // 2] if ts else 0.0
 
     def total_ms(self):
         return sum(s.elapsed_time(e) for s, e in self.pairs)
@@ -126,12 +130,12 @@ def bench_adamw8bit(steps, warmup, n=N8):
         lt.on = False
         sync()
         wall = (time.perf_counter() - t0) * 1e3 / steps
-    kms = lt.mean_ms()
+    kms = lt.median_ms()      # the median launch (timed steps, median)
     nbytes = B8_PER_ELEM * n
     st = opt.state[p]
     assert st["optim_bits"] == 8 and st["state1"].dtype == torch.uint8
-    out = dict(ms_per_step=wall, kernel_ms=kms, gbps=nbytes / (wall * 1e6), kernel_gbps=nbytes / (kms * 1e6),
-               bytes_per_step=nbytes)
+    out = dict(ms_per_step=wall, kernel_ms=kms, kernel_ms_mean=lt.mean_ms(), gbps=nbytes / (wall * 1e6),
+               kernel_gbps=nbytes / (kms * 1e6), bytes_per_step=nbytes)
     del grads, opt, p
     torch.cuda.empty_cache()
     return out
@@ -171,10 +175,21 @@ def cpu_baseline_adamw8bit(budget_s=8.0):
         steps += 1
     gbps = B8_PER_ELEM * n * steps / t / 1e9
     threads = int(O.lib().orc_num_threads())
-    return dict(value=round(gbps, 4), unit="GB/s", cores=threads, kind="port",
+    return dict(value=round(gbps, 4), unit="GB/s", cores=threads, host_cpus=os.cpu_count(), kind="port",
                 sample=f"{steps} steps of the C oracle (restatement of muon_sr/triton_adamw_8bit.py:56-89, "
                        f"OpenMP over blocks) on 2^24 of the 2^28 elements (same per-element work), {t:.1f} s, "
                        f"{threads} threads of {host_cpu()}")
+
+
+def host_threads():
+    """Threads for the host-core baselines: every CPU the process sees
+    (os.cpu_count()), capped by the job's CPU share when the environment states
+    one (OMP_NUM_THREADS; a GPU box of this pool gives a one-GPU job 16 threads)."""
+    n = os.cpu_count() or 1
+    share = os.environ.get("OMP_NUM_THREADS")
+    if share and share.isdigit() and int(share) > 0:
+        n = min(n, int(share))
+    return n
 
 
 def cpu_baselines_torch(budget_s=6.0):
@@ -188,8 +203,9 @@ def cpu_baselines_torch(budget_s=6.0):
     import torch
     import oracle as O
     from oracle import torch_ref as T
+    torch.set_num_threads(host_threads())
     threads = torch.get_num_threads()
-    out = {"cores": threads, "kind": "port", "host": host_cpu()}
+    out = {"cores": threads, "host_cpus": os.cpu_count(), "kind": "port", "host": host_cpu()}
     gen = torch.Generator().manual_seed(1)
 
     def bf(shape, std):
@@ -383,10 +399,10 @@ def bench_muon(shapes, steps_timed, warmup, label):
     for _ in range(warmup):
         opt.step()
     sync()
-    # the Newton-Schulz + apply calls alone (normalization, the 5 iterations of every
-    # chunk and the parameter update in the last product's store), bracketed on their
-    # stream, beside the whole step (prepare, NS + apply)
-    with LaunchTimer("msr_muon_ns_apply") as lt:
+    # the Newton-Schulz calls alone (normalization and the 5 iterations of every chunk;
+    # for wide matrices also the parameter update done by the last product's store),
+    # bracketed on their stream, beside the whole step (prepare, NS, apply)
+    with LaunchTimer("msr_muon_ns_apply", "msr_newton_schulz") as lt:
         t0 = time.perf_counter()
         lt.on = True
         for _ in range(steps_timed):
@@ -606,10 +622,23 @@ def main():
     r8 = bench_adamw8bit(args.steps, args.warmup)
     log(f"adamw8bit: {r8}")
     configs = {"adamw8bit_2^28": {k: round(v, 4) for k, v in r8.items()}}
+    other = "triton" if args.noise == "philox8" else "philox8"
+    if "adamw8bit" in todo:   # the same step with the other noise stream (triton: the reference's bits)
+        muon_sr_amd.set_sr_noise(other)
+        r = bench_adamw8bit(max(5, args.steps // 2), 2)
+        muon_sr_amd.set_sr_noise(args.noise)
+        log(f"adamw8bit ({other} noise): {r}")
+        configs[f"adamw8bit_2^28_{other}_noise"] = {k: round(v, 4) for k, v in r.items()}
     if "sr_accum" in todo:
         r = bench_sr_accum()
         log(f"sr_accum: {r}")
         configs["sr_accum_24L_d2048"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+        muon_sr_amd.set_sr_noise(other)
+        r = bench_sr_accum(micro=6)
+        muon_sr_amd.set_sr_noise(args.noise)
+        log(f"sr_accum ({other} noise): {r}")
+        configs[f"sr_accum_24L_d2048_{other}_noise"] = {k: round(v, 4) if isinstance(v, float) else v
+                                                        for k, v in r.items()}
     if "ns" in todo:
         r = bench_muon(config4_shapes(), steps_timed=3, warmup=1, label="config4")
         log(f"muon config4: {r}")
@@ -654,7 +683,11 @@ def main():
                    "weight_decay": 0.01, "sr_noise": args.noise, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
+                     "traffic_source": "profiles/adamw8bit_2e28_hbm_traffic.txt: rocprofv3 --pmc FETCH_SIZE and "
+                                       "WRITE_SIZE runs of this kernel, scaled by a copy calibration (committed "
+                                       "counter run, not measured in this run)",
                      "kernel": "adamw8bit_fast_kernel", "kernel_ms": round(r8["kernel_ms"], 4),
+                     "kernel_ms_stat": "median of the timed launches (HIP events on the launch stream)",
                      "bytes_per_launch": r8["bytes_per_step"]},
         "cpu_baseline": cpu,
         "configs": configs,

@@ -314,13 +314,117 @@ __device__ __forceinline__ void adam8_pair_exact(const Adam8Args &a, const Raw8 
     }
 }
 
-#ifdef MSR_F8_WPE
-#define MSR_F8_ATTR __attribute__((amdgpu_waves_per_eu(MSR_F8_WPE, MSR_F8_WPE)))
-#else
-#define MSR_F8_ATTR
-#endif
+// Wave-uniform constants of the fast branch, held in VGPRs (see vgpr()).
+struct F8Consts {
+    float b1, omb1, b2, omb2, step_c, eps_c, decay, step_abs;
+    uint32_t lo1, scap;
+    int32_t tm1;
+};
+
+__device__ __forceinline__ F8Consts f8_consts(const Adam8Args &a) {
+    const Adam8Consts c = adam8_consts(a);
+    F8Consts k;
+    k.b1 = vgpr(a.b1); k.omb1 = vgpr(c.one_m_b1); k.b2 = vgpr(a.b2); k.omb2 = vgpr(c.one_m_b2);
+    k.step_c = vgpr(c.step_c); k.eps_c = vgpr(c.eps_c); k.decay = vgpr(c.decay);
+    k.lo1 = vgpr(QF_LO1); k.scap = vgpr((uint32_t)QF_SCAP);
+    // div_upd(step_c * m, den) needs |step_c * m| = 0 or in [2^-90, 2^60]: nonzero |m| below
+    // tm = 2^-90 / |step_c| (tm1 = bits(tm) - 1) or |step_c| * max |m| >= 2^60 take the exact
+    // branch (den is in [2^-60, 2^32): eps_c is checked by the launcher, v' < 2^62 below)
+    k.step_abs = vgpr(fabsf(c.step_c));
+    k.tm1 = (int32_t)vgpr(c.step_c != 0.0f ? __float_as_uint(0x1p-90f / fabsf(c.step_c)) - 1u : 0u);
+    return k;
+}
+
+// One pair of quantization blocks (the wave's 64 lanes x 8 elements, pair index pr) on the
+// fast branch.  Returns false, having written nothing, when some lane of the pair needs the
+// exact arithmetic (the caller then defers the pair to adam8_pair_exact).
 template <int MODE>
-__global__ __launch_bounds__(F8_THREADS) MSR_F8_ATTR void adamw8bit_fast_kernel(Adam8Args a, int64_t npairs) {
+__device__ __forceinline__ bool adam8_pair_fast(const Adam8Args &a, const F8Consts &k, const Raw8 &raw, int64_t pr,
+                                                uint32_t lane, const float *q1s, const float *q2s,
+                                                const uint32_t *s_flat) {
+    float p[8], g[8], m[8], v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        p[j] = bf16_at(raw.p, j);
+        g[j] = bf16_at(raw.g, j);
+    }
+    // a sum of the 8 gradients is finite iff all of them are (or it overflows: exact)
+    const float gsum = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
+    float mx = 0.0f, vx = 0.0f;
+    uint32_t mnz = 0xffffffffu;   // min of 2 bits(|m|) - 2: (bits of the smallest nonzero |m|) - 1, times 2
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float mq = q1s[byte_of(raw.mc, j)] * raw.ms;                    // :65
+        const float vq = q2s[byte_of(raw.vc, j)] * raw.vs;                    // :66
+        m[j] = k.b1 * mq + k.omb1 * g[j];                                     // :71
+        v[j] = k.b2 * vq + (k.omb2 * g[j]) * g[j];                            // :72
+        mx = fmaxf(mx, fabsf(m[j]));
+        vx = fmaxf(vx, v[j]);
+        mnz = min(mnz, (__float_as_uint(m[j]) << 1) - 2u);                    // +-0 gives 0xfffffffe
+    }
+    const float ms = raw.ms, vs = raw.vs;
+    halfwave_max2(mx, vx);                                                    // :80-81
+    const float md = mx > 0.0f ? mx : 1.0f;                                   // :82
+    const float vd = vx > 0.0f ? vx : 1.0f;                                   // :83
+    // Fast-branch conditions as sign bits of differences of non-negative bit patterns:
+    // finite gradients and block scales, vs >= +0 (then m' is finite or +-inf and v' >= 0
+    // finite or +inf, never NaN, so the maxima above are exact), max v' < 2^62, both
+    // divisors in [2^-60, 2) and the update's numerators |step_c * m'| zero or in
+    // [2^-90, 2^60) (the block maximum of |m'| bounds them from above).
+    const int32_t FMAX = 0x7f7fffff, DLO = 0x21800000, DHI = 0x3fffffff, VXHI = 0x5e7fffff;
+    const int32_t NHI = 0x5d7fffff;   // bits(2^60) - 1
+    const int32_t gsb = (int32_t)(__float_as_uint(gsum) & 0x7fffffffu);
+    const int32_t msb = (int32_t)(__float_as_uint(ms) & 0x7fffffffu);
+    const int32_t vsb = (int32_t)__float_as_uint(vs), vxb = (int32_t)__float_as_uint(vx);
+    const int32_t mdb = (int32_t)__float_as_uint(md), vdb = (int32_t)__float_as_uint(vd);
+    const int32_t nxb = (int32_t)__float_as_uint(k.step_abs * mx), mnb = (int32_t)(mnz >> 1);
+    const int32_t neg = (FMAX - gsb) | (FMAX - msb) | vsb | (FMAX - vsb) | (VXHI - vxb) | (mdb - DLO) |
+                        (DHI - mdb) | (vdb - DLO) | (DHI - vdb) | (NHI - nxb) | (mnb - k.tm1);
+    if (__builtin_amdgcn_ballot_w64(neg < 0) != 0) return false;
+    const int64_t o0 = pr * F8_PAIR + lane * 8;
+    const int64_t qb = pr * 2 + (lane >> 5);
+    uint32_t rp[8], w[8];
+    noise8<MODE>(a.ns_p, o0, 8, rp);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float den = __builtin_fmaf(sqrt_rn_x2p32(v[j]), 0x1p-32f, k.eps_c);   // :74 sqrt(v) + eps
+        const float upd = (p[j] - div_upd(k.step_c * m[j], den)) * k.decay;
+        w[j] = __float_as_uint(upd) + rp[j];                                  // :75-78 (SR)
+    }
+    st_nt4(a.p + o0, u32x4_t{__builtin_amdgcn_perm(w[1], w[0], 0x07060302u), __builtin_amdgcn_perm(w[3], w[2], 0x07060302u),
+                             __builtin_amdgcn_perm(w[5], w[4], 0x07060302u), __builtin_amdgcn_perm(w[7], w[6], 0x07060302u)});
+    const float ym = rcp_rn(md), yv = rcp_rn(vd);
+    uint32_t rm[8], rv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        rm[j] = qf_signed(div_rn(m[j], md, ym), s_flat, k.lo1, k.scap);            // :82,84
+        rv[j] = qf_unsigned(div_rn(v[j], vd, yv), s_flat + QF_SIGNED, k.lo1);     // :83,85
+    }
+    st_nt2(static_cast<uint8_t *>(a.s1) + o0, u32x2_t{pack_codes(rm[0], rm[1], rm[2], rm[3]), pack_codes(rm[4], rm[5], rm[6], rm[7])});
+    st_nt2(static_cast<uint8_t *>(a.s2) + o0, u32x2_t{pack_codes(rv[0], rv[1], rv[2], rv[3]), pack_codes(rv[4], rv[5], rv[6], rv[7])});
+    if ((lane & 31) == 0) {
+        a.absmax1[qb] = mx;                                                   // :86
+        a.absmax2[qb] = vx;                                                   // :87
+    }
+    return true;
+}
+
+// Raw inputs of pair pr, loaded into VGPRs (the deferred exact pairs).
+__device__ __forceinline__ Raw8 fetch_pair(const Adam8Args &a, int64_t pr, uint32_t lane) {
+    const char *pb = reinterpret_cast<const char *>(a.p), *gb = reinterpret_cast<const char *>(a.g);
+    const char *mb = static_cast<const char *>(a.s1), *vb = static_cast<const char *>(a.s2);
+    Raw8 r;
+    r.p = ld_nt4(pb + pr * (2 * F8_PAIR) + lane * 16u);
+    r.g = ld_nt4(gb + pr * (2 * F8_PAIR) + lane * 16u);
+    r.mc = ld_nt2(mb + pr * F8_PAIR + lane * 8u);
+    r.vc = ld_nt2(vb + pr * F8_PAIR + lane * 8u);
+    r.ms = a.absmax1[pr * 2 + (lane >> 5)];
+    r.vs = a.absmax2[pr * 2 + (lane >> 5)];
+    return r;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(F8_THREADS) void adamw8bit_fast_kernel(Adam8Args a, int64_t npairs) {
     __shared__ float q1s[256], q2s[256];
     __shared__ uint32_t s_flat[QF_TOTAL];
     __shared__ uint32_t s_deferred[F8_THREADS / 64][F8_DEFER];
@@ -330,121 +434,31 @@ __global__ __launch_bounds__(F8_THREADS) MSR_F8_ATTR void adamw8bit_fast_kernel(
     }
     for (int i = threadIdx.x; i < QF_TOTAL; i += F8_THREADS) s_flat[i] = a.qtable->flat[i];
     __syncthreads();
-    const Adam8Consts c = adam8_consts(a);
-    const float b1 = vgpr(a.b1), omb1 = vgpr(c.one_m_b1), b2 = vgpr(a.b2), omb2 = vgpr(c.one_m_b2);
-    const float step_c = vgpr(c.step_c), eps_c = vgpr(c.eps_c), decay = vgpr(c.decay);
-    const uint32_t lo1 = vgpr(QF_LO1), scap = vgpr((uint32_t)QF_SCAP);
-    // div_upd(step_c * m, den) needs |step_c * m| = 0 or in [2^-90, 2^60]: nonzero |m| below
-    // tm = 2^-90 / |step_c| (tm1 = bits(tm) - 1) or |step_c| * max |m| >= 2^60 take the exact
-    // branch (den is in [2^-60, 2^32): eps_c is checked by the launcher, v' < 2^62 below)
-    const float step_abs = vgpr(fabsf(c.step_c));
-    const int32_t tm1 = (int32_t)vgpr(c.step_c != 0.0f ? __float_as_uint(0x1p-90f / fabsf(c.step_c)) - 1u : 0u);
-    const char *pb = reinterpret_cast<const char *>(a.p), *gb = reinterpret_cast<const char *>(a.g);
-    const char *mb = static_cast<const char *>(a.s1), *vb = static_cast<const char *>(a.s2);
+    const F8Consts k = f8_consts(a);
     const uint32_t lane = threadIdx.x & 63u;
     // the pair index is wave-uniform: addresses are a scalar base plus a fixed lane offset
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int64_t wstride = (int64_t)gridDim.x * (F8_THREADS / 64);
-    auto fetch = [&](int64_t pr, Raw8 &r) {
-        r.p = ld_nt4(pb + pr * (2 * F8_PAIR) + lane * 16u);
-        r.g = ld_nt4(gb + pr * (2 * F8_PAIR) + lane * 16u);
-        r.mc = ld_nt2(mb + pr * F8_PAIR + lane * 8u);
-        r.vc = ld_nt2(vb + pr * F8_PAIR + lane * 8u);
-        r.ms = a.absmax1[pr * 2 + (lane >> 5)];
-        r.vs = a.absmax2[pr * 2 + (lane >> 5)];
-    };
     int64_t pr = (int64_t)blockIdx.x * (F8_THREADS / 64) + wave;
-    // Pairs that need the exact arithmetic are skipped by the streaming loop (nothing is
-    // written for them) and recorded in the wave's LDS list; they are done after the loop,
-    // so the exact code does not add to the loop's registers.
     uint32_t *deferred = s_deferred[wave];
-    // One pair in flight: the next pair is fetched while the current one is computed.
     for (;;) {
         int ndef = 0;
         Raw8 nxt;
-        if (pr < npairs) fetch(pr, nxt);
+        if (pr < npairs) nxt = fetch_pair(a, pr, lane);
         for (; pr < npairs; pr += wstride) {
             const Raw8 raw = nxt;
-            if (pr + wstride < npairs) fetch(pr + wstride, nxt);
-            float p[8], g[8], m[8], v[8];
-            const u32x4_t pw = raw.p;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                p[j] = bf16_at(pw, j);
-                g[j] = bf16_at(raw.g, j);
-            }
-            // a sum of the 8 gradients is finite iff all of them are (or it overflows: exact)
-            const float gsum = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
-            float mx = 0.0f, vx = 0.0f;
-            uint32_t mnz = 0xffffffffu;   // min of 2 bits(|m|) - 2: (bits of the smallest nonzero |m|) - 1, times 2
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float mq = q1s[byte_of(raw.mc, j)] * raw.ms;            // :65
-                const float vq = q2s[byte_of(raw.vc, j)] * raw.vs;            // :66
-                m[j] = b1 * mq + omb1 * g[j];                                 // :71
-                v[j] = b2 * vq + (omb2 * g[j]) * g[j];                        // :72
-                mx = fmaxf(mx, fabsf(m[j]));
-                vx = fmaxf(vx, v[j]);
-                mnz = min(mnz, (__float_as_uint(m[j]) << 1) - 2u);            // +-0 gives 0xfffffffe
-            }
-            const float ms = raw.ms, vs = raw.vs;
-            halfwave_max2(mx, vx);                                            // :80-81
-            const float md = mx > 0.0f ? mx : 1.0f;                           // :82
-            const float vd = vx > 0.0f ? vx : 1.0f;                           // :83
-            // Fast-branch conditions as sign bits of differences of non-negative bit patterns:
-            // finite gradients and block scales, vs >= +0 (then m' is finite or +-inf and v' >= 0
-            // finite or +inf, never NaN, so the maxima above are exact), max v' < 2^62, both
-            // divisors in [2^-60, 2) and the update's numerators |step_c * m'| zero or in
-            // [2^-90, 2^60) (the block maximum of |m'| bounds them from above).
-            const int32_t FMAX = 0x7f7fffff, DLO = 0x21800000, DHI = 0x3fffffff, VXHI = 0x5e7fffff;
-            const int32_t NHI = 0x5d7fffff;   // bits(2^60) - 1
-            const int32_t gsb = (int32_t)(__float_as_uint(gsum) & 0x7fffffffu);
-            const int32_t msb = (int32_t)(__float_as_uint(ms) & 0x7fffffffu);
-            const int32_t vsb = (int32_t)__float_as_uint(vs), vxb = (int32_t)__float_as_uint(vx);
-            const int32_t mdb = (int32_t)__float_as_uint(md), vdb = (int32_t)__float_as_uint(vd);
-            const int32_t nxb = (int32_t)__float_as_uint(step_abs * mx), mnb = (int32_t)(mnz >> 1);
-            const int32_t neg = (FMAX - gsb) | (FMAX - msb) | vsb | (FMAX - vsb) | (VXHI - vxb) | (mdb - DLO) |
-                                (DHI - mdb) | (vdb - DLO) | (DHI - vdb) | (NHI - nxb) | (mnb - tm1);
-            if (__builtin_amdgcn_ballot_w64(neg < 0) != 0) {
-                if (lane == 0) deferred[ndef] = (uint32_t)pr;
-                if (++ndef == F8_DEFER) {
-                    pr += wstride;
-                    break;
-                }
-                continue;
-            }
-            const int64_t o0 = pr * F8_PAIR + lane * 8;
-            const int64_t qb = pr * 2 + (lane >> 5);
-            uint32_t rp[8], w[8];
-            noise8<MODE>(a.ns_p, o0, 8, rp);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float den = __builtin_fmaf(sqrt_rn_x2p32(v[j]), 0x1p-32f, eps_c);   // :74 sqrt(v) + eps
-                const float upd = (p[j] - div_upd(step_c * m[j], den)) * decay;
-                w[j] = __float_as_uint(upd) + rp[j];                          // :75-78 (SR)
-            }
-            st_nt4(a.p + o0, u32x4_t{__builtin_amdgcn_perm(w[1], w[0], 0x07060302u), __builtin_amdgcn_perm(w[3], w[2], 0x07060302u),
-                                     __builtin_amdgcn_perm(w[5], w[4], 0x07060302u), __builtin_amdgcn_perm(w[7], w[6], 0x07060302u)});
-            const float ym = rcp_rn(md), yv = rcp_rn(vd);
-            uint32_t rm[8], rv[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                rm[j] = qf_signed(div_rn(m[j], md, ym), s_flat, lo1, scap);               // :82,84
-                rv[j] = qf_unsigned(div_rn(v[j], vd, yv), s_flat + QF_SIGNED, lo1);       // :83,85
-            }
-            st_nt2(static_cast<uint8_t *>(a.s1) + o0, u32x2_t{pack_codes(rm[0], rm[1], rm[2], rm[3]), pack_codes(rm[4], rm[5], rm[6], rm[7])});
-            st_nt2(static_cast<uint8_t *>(a.s2) + o0, u32x2_t{pack_codes(rv[0], rv[1], rv[2], rv[3]), pack_codes(rv[4], rv[5], rv[6], rv[7])});
-            if ((lane & 31) == 0) {
-                a.absmax1[qb] = mx;                                           // :86
-                a.absmax2[qb] = vx;                                           // :87
+            if (pr + wstride < npairs) nxt = fetch_pair(a, pr + wstride, lane);
+            if (adam8_pair_fast<MODE>(a, k, raw, pr, lane, q1s, q2s, s_flat)) continue;
+            if (lane == 0) deferred[ndef] = (uint32_t)pr;
+            if (++ndef == F8_DEFER) {
+                pr += wstride;
+                break;
             }
         }
         __builtin_amdgcn_wave_barrier();   // lane 0's list writes precede the wave's reads
         for (int i = 0; i < ndef; ++i) {
             const int64_t pe = (int64_t)__builtin_amdgcn_readfirstlane(deferred[i]);
-            Raw8 r;
-            fetch(pe, r);
-            adam8_pair_exact<MODE>(a, r, pe * F8_PAIR + lane * 8, pe * 2 + (lane >> 5), q1s, q2s);
+            adam8_pair_exact<MODE>(a, fetch_pair(a, pe, lane), pe * F8_PAIR + lane * 8, pe * 2 + (lane >> 5), q1s, q2s);
         }
         if (pr >= npairs) break;
     }

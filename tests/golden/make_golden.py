@@ -2,7 +2,7 @@
 
 Run in the development container only (the GPU box has no reference checkout):
 
-    python tests/golden/make_golden.py [/path/to/reference]
+    python tests/golden/make_golden.py [/path/to/reference] [--only name,name]
 
 It imports bab2min/muon_sr 0.1.2 with ``TRITON_INTERPRET=1`` so that its Triton
 kernels execute on CPU tensors through Triton's interpreter (numpy, IEEE fp32,
@@ -25,6 +25,7 @@ truncating behaviour explicitly (``prepare_rounding = "trunc"``).
 """
 from __future__ import annotations
 
+import copy
 import os
 import sys
 
@@ -37,7 +38,7 @@ import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-REF = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+REF = sys.argv[1] if len(sys.argv) > 1 and not sys.argv[1].startswith("--") else "/root/reference"
 sys.path.insert(0, REF)
 
 import triton  # noqa: E402
@@ -315,13 +316,124 @@ def gen_ns_and_trajectories():
     np.savez_compressed(os.path.join(HERE, "ns_traj.npz"), **out)
 
 
+# ---------------------------------------------------------------------------
+# 5. Checkpoints written by the reference's classes
+# ---------------------------------------------------------------------------
+
+def _structure(sd):
+    """Keys, dtypes and shapes of a state_dict, and its param groups (plain data)."""
+    st = {int(i): {k: ((str(v.dtype), tuple(v.shape)) if torch.is_tensor(v) else v) for k, v in d.items()}
+          for i, d in sd["state"].items()}
+    return {"state": st, "param_groups": [dict(g) for g in sd["param_groups"]]}
+
+
+def _case(opt, ps, gen, steps_before, grad_std, missing=()):
+    """Run steps_before steps, record the state_dict and parameters, then one more step and its results."""
+    rec = {"p0": [p.detach().clone() for p in ps]}
+    for step in range(1, steps_before + 2):
+        grads = []
+        for j, p in enumerate(ps):
+            g = (torch.randn(*p.shape, generator=gen) * grad_std).to(torch.bfloat16)
+            p.grad = None if (step, j) in missing else g
+            grads.append(None if p.grad is None else g.clone())
+        if step == steps_before + 1:
+            # the checkpoint: torch.save of the reference's own state_dict() (views of the
+            # batch_ns stacks are saved with their storage, as a user's torch.save would)
+            rec["state_dict"] = copy.deepcopy(opt.state_dict())   # its entries are live objects
+            rec["p_ckpt"] = [p.detach().clone() for p in ps]
+            rec["grads_next"] = grads
+        opt.step()
+    rec["p_next"] = [p.detach().clone() for p in ps]
+    rec["state_next"] = {j: {k: (v.clone() if torch.is_tensor(v) else v) for k, v in opt.state[p].items()}
+                         for j, p in enumerate(ps) if p in opt.state}
+    rec["structure_next"] = _structure(opt.state_dict())
+    return rec
+
+
+def _adamw8bit_reference_steps(opt, ps, gen, steps):
+    """TritonAdamW8bit.step (muon_sr/triton_adamw_8bit.py:169-204) refuses CPU tensors, so the
+    interpreter cannot run it; this calls the class's own _init_state and kernel with the
+    step's seed and bias corrections, in the step's parameter order, for `steps` steps."""
+    for _ in range(steps):
+        index = 0
+        for group in opt.param_groups:
+            opt._validate_group(group)
+            b1, b2 = group["betas"]
+            for p in group["params"]:
+                param_index = index
+                index += 1
+                g = p.grad
+                if g is None:
+                    continue
+                state = opt.state[p]
+                if not state:
+                    state.update(opt._init_state(p, group))
+                state["step"] += 1
+                n = state["step"]
+                seed = (n * 2654435761 ^ param_index * 1234567891) & 0xFFFFFFFF
+                r8._adamw_8bit_kernel[(triton.cdiv(p.numel(), group["block_size"]),)](
+                    p, g, state["state1"], state["state2"],
+                    state.get("absmax1", p), state.get("absmax2", p),
+                    state.get("qmap1", p), state.get("qmap2", p), p.numel(),
+                    group["lr"], b1, b2, group["eps"], group["weight_decay"],
+                    1 - b1 ** n, 1 - b2 ** n, seed, BLOCK=group["block_size"],
+                    QUANTIZED=state["optim_bits"] == 8)
+
+
+class _StepAs8bit:
+    """Gives _case an optimizer whose step() runs _adamw8bit_reference_steps once."""
+    def __init__(self, opt, ps, gen):
+        self.opt, self.ps = opt, ps
+        self.state = opt.state
+
+    def step(self):
+        _adamw8bit_reference_steps(self.opt, self.ps, None, 1)
+
+    def state_dict(self):
+        return self.opt.state_dict()
+
+
+def gen_checkpoints():
+    gen = torch.Generator().manual_seed(4242)
+    cases = {}
+
+    def params(shapes, std=0.02):
+        return [torch.nn.Parameter((torch.randn(*s, generator=gen) * std).to(torch.bfloat16)) for s in shapes]
+
+    # TritonMuonSR(batch_ns=True): stacks of two shapes plus a single one; the global step is
+    # restored from the per-parameter steps on load (muon_sr/triton_muon_sr.py:13-15, 218-226)
+    ps = params([(32, 48), (48, 32), (32, 48), (16, 16)])
+    opt = rm.TritonMuonSR(ps, lr=0.02, weight_decay=0.01, batch_ns=True)
+    cases["muon_batch"] = _case(opt, ps, gen, 2, 1e-3)
+    # TritonAdamW: two groups (the second with centralization), a missing gradient in step 1
+    ps = params([(10, 30), (64,), (8, 16)])
+    opt = ra.TritonAdamW([{"params": ps[:2]}, {"params": ps[2:], "lr": 2e-3, "weight_decay": 0.1,
+                                                 "centralization": 0.5}],
+                         lr=1e-3, betas=(0.9, 0.95), eps=1e-8)
+    cases["adamw"] = _case(opt, ps, gen, 2, 1e-3, missing={(1, 1)})
+    # TritonMuonSRWithAuxAdam(batch_ns=True): Muon group and AdamW group
+    ps = params([(32, 48), (48, 32), (32, 48), (40,), (8, 8)])
+    opt = rm.TritonMuonSRWithAuxAdam(
+        [{"params": ps[:3], "use_muon": True, "weight_decay": 0.01},
+         {"params": ps[3:], "use_muon": False, "lr": 3e-4, "betas": (0.9, 0.95), "eps": 1e-10,
+          "weight_decay": 0.01}],
+        batch_ns=True)
+    cases["hybrid_batch"] = _case(opt, ps, gen, 2, 1e-3)
+    # TritonAdamW8bit: an 8-bit tensor with a ragged last block, a tensor below min_8bit_size
+    # (bf16 moments) and an optim_bits=16 group
+    ps = params([(40, 260), (30, 40), (8, 64)])
+    opt = r8.TritonAdamW8bit([{"params": ps[:2]}, {"params": ps[2:], "optim_bits": 16}],
+                             lr=3e-4, betas=(0.9, 0.95), eps=1e-10, weight_decay=0.01)
+    cases["adamw8bit"] = _case(_StepAs8bit(opt, ps, gen), ps, gen, 2, 1e-3)
+    torch.save(cases, os.path.join(HERE, "checkpoints.pt"))
+
+
 if __name__ == "__main__":
+    only = sys.argv[sys.argv.index("--only") + 1].split(",") if "--only" in sys.argv else None
     print("reference version", muon_sr.__version__)
-    gen_quantize(np.random.default_rng(7))
-    print("quantize done")
-    gen_adamw8bit()
-    print("adamw8bit done")
-    gen_elementwise()
-    print("elementwise done")
-    gen_ns_and_trajectories()
-    print("ns/trajectories done")
+    for name, fn in (("quantize", lambda: gen_quantize(np.random.default_rng(7))), ("adamw8bit", gen_adamw8bit),
+                     ("elementwise", gen_elementwise), ("ns_traj", gen_ns_and_trajectories),
+                     ("checkpoints", gen_checkpoints)):
+        if only is None or name in only:
+            fn()
+            print(name, "done")

@@ -59,3 +59,47 @@ def test_hybrid_rejects_incompatible_8bit_state():
     with pytest.raises(ValueError, match="Incompatible state format"):
         opt.load_state_dict(sd)
 
+
+
+def _reference_checkpoints():
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "checkpoints.pt")
+    return torch.load(path, weights_only=True)
+
+
+@pytest.mark.parametrize("case", ["adamw", "adamw8bit", "muon_batch", "hybrid_batch"])
+def test_reference_checkpoint_loads_and_saves_unchanged(case):
+    """A state_dict the reference's own class wrote (tests/golden/checkpoints.pt) loads into
+    this library's class and comes back out of state_dict() unchanged: same param groups,
+    state keys, dtypes, shapes and values (muon_sr/triton_adamw_8bit.py:207-241,
+    muon_sr/muon_sr.py:149-158)."""
+    from muon_sr_amd import TritonAdamW, TritonMuonSR
+    rec = _reference_checkpoints()[case]
+    ps = [torch.nn.Parameter(p.clone()) for p in rec["p_ckpt"]]
+    if case == "adamw":
+        opt = TritonAdamW([{"params": ps[:2]}, {"params": ps[2:], "lr": 2e-3, "weight_decay": 0.1,
+                                                 "centralization": 0.5}], lr=1e-3, betas=(0.9, 0.95), eps=1e-8)
+    elif case == "adamw8bit":
+        opt = TritonAdamW8bit([{"params": ps[:2]}, {"params": ps[2:], "optim_bits": 16}],
+                              lr=3e-4, betas=(0.9, 0.95), eps=1e-10, weight_decay=0.01)
+    elif case == "muon_batch":
+        opt = TritonMuonSR(ps, lr=0.02, weight_decay=0.01, batch_ns=True)
+    else:
+        opt = TritonMuonSRWithAuxAdam(
+            [{"params": ps[:3], "use_muon": True, "weight_decay": 0.01},
+             {"params": ps[3:], "use_muon": False, "lr": 3e-4, "betas": (0.9, 0.95), "eps": 1e-10,
+              "weight_decay": 0.01}], batch_ns=True)
+    ref = rec["state_dict"]
+    opt.load_state_dict(ref)
+    out = opt.state_dict()
+    assert out["param_groups"] == ref["param_groups"]
+    assert sorted(out["state"]) == sorted(ref["state"])
+    for i, st in ref["state"].items():
+        assert sorted(out["state"][i]) == sorted(st), i
+        for k, v in st.items():
+            w = out["state"][i][k]
+            if torch.is_tensor(v):
+                assert w.dtype == v.dtype and w.shape == v.shape and torch.equal(w.view(-1).view(torch.uint8) if w.dtype == torch.bfloat16 else w,
+                                                                                  v.view(-1).view(torch.uint8) if v.dtype == torch.bfloat16 else v), (i, k)
+            else:
+                assert w == v, (i, k)

@@ -42,7 +42,7 @@ _SR_MASK = -65536   # 0xFFFF0000 as int32
 def sr_store(dst: torch.Tensor, src: torch.Tensor) -> None:
     """dst (bf16) <- src (fp32) stochastically rounded: add a uniform 16-bit
     integer to the fp32 bit pattern, keep the upper 16 bits."""
-    bits = torch.randint(0, 1 << 16, src.shape, dtype=torch.int32)
+    bits = torch.randint(0, 1 << 16, src.shape, dtype=torch.int32, device=src.device)
     bits += src.contiguous().view(torch.int32)
     bits &= _SR_MASK
     dst.copy_(bits.view(torch.float32))
@@ -238,7 +238,7 @@ class _MuonGroups:
                 shapes.setdefault(tuple(p.shape), []).append(p)
             entry = []
             for shape, ps in shapes.items():
-                stack = torch.zeros(len(ps), *shape, dtype=torch.bfloat16)
+                stack = torch.zeros(len(ps), *shape, dtype=torch.bfloat16, device=ps[0].device)
                 index = {}
                 for i, p in enumerate(ps):
                     index[id(p)] = i

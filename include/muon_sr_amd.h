@@ -198,8 +198,9 @@ int msr_muon_apply(uint16_t *const *params, const uint16_t *upd, int64_t numel_e
  *   X = G/(||G||_F + 1e-7);  repeat: A = X X^T; B = b A + c A A; X = a X + B X,
  * evaluated as B' = c A A + b A + a I, X = B' X: products accumulate in fp32,
  * A, B' and X are stored in bf16 between GEMMs.  The normalised input is not
- * rounded (G is scaled by a power of two and the rest of 1/(||G||_F + 1e-7)
- * goes into the first products), and the bf16 rounding residuals of the
+ * rounded (G itself, or G scaled by a power of two when ||G||_F is below 2^-16
+ * or above 2^17, is the first iterate, and 1/(||G||_F + 1e-7) goes into the
+ * first products' scale factors), and the bf16 rounding residuals of the
  * diagonals of A and B' are carried in fp32 into the next product.  Within
  * 1e-2 relative Frobenius of the exact iteration on Gaussian inputs.
  * steps == 0 returns the reference's bf16 normalisation bf16(G / bf16(bf16(
@@ -230,6 +231,34 @@ int msr_muon_ns_apply(const uint16_t *upd, uint16_t *const *params, const uint32
                       int64_t rows, int64_t cols, int32_t steps, float a, float b, float c, float lr,
                       float weight_decay, float scale, int32_t noise_mode, const uint16_t *inject,
                       void *workspace, size_t workspace_bytes, msr_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (b) The whole Muon step of one chunk: momentum prologue, Newton-Schulz and
+ * the parameter update.  Replaces, for one NS chunk of a shape group, the
+ * grad->stack copy and _muon_prepare_kernel (muon_sr/triton_muon_sr.py:18-50,
+ * 150-159), _newton_schulz (muon_sr/muon_sr.py:82-98) and the _run_apply
+ * launches (triton_muon_sr.py:53-80, 160-169); with batch == 1, first == 0,
+ * _triton_muon_step (:88-120).  Equal, bit for bit, to msr_muon_prepare over the
+ * chunk's rows of the stack, then msr_newton_schulz, then msr_muon_apply (or,
+ * with out, without the apply), but the update is made inside the
+ * Newton-Schulz prologue, which writes it straight into the first iterate
+ * (with its sum of squares): the update stack is never written or read.
+ *   grads:  HOST array of `batch` device pointers (bf16, or fp32 with grads_f32)
+ *   buf:    bf16 momentum of the chunk's first matrix, [batch][rows][cols],
+ *           updated in place (SR); `first` = that matrix's index in its stack:
+ *           noise offset of element j of matrix i = (first + i)*rows*cols + j
+ *   params/apply_seeds: HOST arrays of `batch` (as msr_muon_ns_apply), or
+ *   params == NULL and out: bf16 [batch][rows][cols] receives the NS output.
+ * steps >= 1; workspace as msr_ns_workspace_bytes(batch, rows, cols).
+ * inject_prepare: uint16 indexed by the stack offset above; inject_apply as
+ * msr_muon_ns_apply's.
+ * ------------------------------------------------------------------------- */
+int msr_muon_fused_step(const void *const *grads, int32_t grads_f32, uint16_t *buf, int64_t first, int64_t batch,
+                        int64_t rows, int64_t cols, float beta, int32_t nesterov, uint32_t prepare_seed,
+                        int32_t steps, float a, float b, float c, uint16_t *out, uint16_t *const *params,
+                        const uint32_t *apply_seeds, float lr, float weight_decay, float scale,
+                        int32_t noise_mode, const uint16_t *inject_prepare, const uint16_t *inject_apply,
+                        void *workspace, size_t workspace_bytes, msr_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Diagnostics (no counterpart in the reference; used by the parity tests).

@@ -50,6 +50,8 @@ SIGNATURES = {
     "msr_newton_schulz": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _I32, _F, _F, _F, _P, ctypes.c_size_t, _P]),
     "msr_muon_ns_apply": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _I32, _F, _F, _F, _F, _F, _F, _I32, _P,
                                          _P, ctypes.c_size_t, _P]),
+    "msr_muon_fused_step": (ctypes.c_int, [_P, _I32, _P, _I64, _I64, _I64, _I64, _F, _I32, _U32, _I32, _F, _F, _F,
+                                           _P, _P, _P, _F, _F, _F, _I32, _P, _P, _P, ctypes.c_size_t, _P]),
     "msr_noise_fill": (ctypes.c_int, [_P, _I64, _I64, _U32, _U32, _I32, _P]),
     "msr_quantize": (ctypes.c_int, [_P, _P, _I64, _P, _I32, _P, _P]),
     "msr_quant_table_bytes": (ctypes.c_size_t, []),

@@ -196,6 +196,17 @@ __device__ __forceinline__ uint32_t noise1(const Noise &ns, int64_t o) {
 }
 
 // ---------------------------------------------------------------------------
+// Muon momentum (muon_sr/triton_muon_sr.py:37-42): the new momentum nb (stored with
+// SR) and the pre-Newton-Schulz update (stored RNE), in the reference's fp32 order.
+// ---------------------------------------------------------------------------
+template <bool NEST>
+__device__ __forceinline__ void muon_momentum(float g, float b, float beta, float one_m_beta, float &nb,
+                                              float &upd) {
+    nb = b + one_m_beta * (g - b);            // :37
+    upd = NEST ? g + beta * (nb - g) : nb;    // :39-42
+}
+
+// ---------------------------------------------------------------------------
 // 8-bit quantizer
 // ---------------------------------------------------------------------------
 

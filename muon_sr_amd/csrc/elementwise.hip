@@ -257,8 +257,8 @@ __global__ __launch_bounds__(THREADS) void muon_prepare_kernel(PrepareArgs a) {
         uint32_t ob[8], ou[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float nb = bf[j] + one_m_beta * (gf[j] - bf[j]);        // :37
-            const float upd = NEST ? gf[j] + a.beta * (nb - gf[j]) : nb;  // :39-42
+            float nb, upd;
+            muon_momentum<NEST>(gf[j], bf[j], a.beta, one_m_beta, nb, upd);   // :37-42
             ob[j] = sr_bf16(nb, r[j]);                                    // :44-49
             ou[j] = rne_bf16(upd);                                        // :50
         }

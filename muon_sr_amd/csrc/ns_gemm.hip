@@ -43,7 +43,6 @@ typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int GEMM_THREADS = 512;
-constexpr int CHUNKS = BM * BK / 8;  // 16-byte chunks per operand slab (2048)
 
 // Muon apply fused into the store of the last Newton-Schulz product
 // (msr_muon_ns_apply): matrix b of a launch updates params p[b] with seed[b].
@@ -784,55 +783,20 @@ __device__ __forceinline__ float norm_divisor(const float *partial, int64_t b) {
     return __uint_as_float(rne_bf16(nrm + 1e-7f) << 16);
 }
 
-// The iteration's input without a rounding: X0 = u / (||u||_F + 1e-7) is kept
-// as x0 = u 2^-e (exact in bf16: a power-of-two scale, e = the exponent of
-// ||u||_F, so ||x0||_F is in [0.5, 1)) and the factor s0 = 2^e / (||u||_F +
-// 1e-7) goes into the first products: A = s0^2 x0 x0^T, X' = s0 (B' x0 + ...).
-// ||u||_F is the fp32 square root of the fp32 sum of squares.  A sum that
-// overflows (||u|| >= 2^64) takes e = 127 and s0 = 0 (u / inf = 0, as the
-// reference's normalisation gives); NaN propagates.
-__device__ __forceinline__ void prescale_of(const float *partial, int64_t b, int &e, float &s0) {
-    const float d = sqrtf(sumsq_of(partial, b));
-    if (d == __builtin_huge_valf()) {
-        e = 127;
-        s0 = 0.0f;
-        return;
-    }
-    e = 0;
-    if (d == d) (void)frexpf(d, &e);
-    s0 = ldexpf(1.0f / (d + 1e-7f), e);
-}
-
 // Vector form of normalize_kernel (below) for cols % 8 == 0 with 16-byte aligned
 // `in`, S and T rows: each thread moves 8 consecutive bf16 (16 bytes) per access.
 // Rp and Cp are multiples of 8 here, so an 8-wide chunk is entirely inside or
 // entirely outside every extent it is checked against.
-// PRESCALE: x0 = u 2^-e (see prescale_of), and block (0, 0) of matrix b writes
-// alphas[b] = s0^2 and alphas[batch + b] = s0; else x0 = bf16(u / d).
-template <bool PRESCALE>
 __global__ __launch_bounds__(256) void normalize_vec_kernel(const uint16_t *in, int64_t rows, int64_t cols,
                                                             const float *partial, uint16_t *S, int64_t ldS,
                                                             int64_t sS, uint16_t *T, int64_t ldT, int64_t sT,
-                                                            int64_t Rp, int64_t Cp, float *alphas) {
+                                                            int64_t Rp, int64_t Cp) {
     __shared__ __align__(16) uint16_t tile[64][72];
     __shared__ float dsh;
-    __shared__ int esh;
     const int64_t b = blockIdx.z;
-    if (threadIdx.x == 0) {
-        if constexpr (PRESCALE) {
-            float s0;
-            prescale_of(partial, b, esh, s0);
-            if (blockIdx.x == 0 && blockIdx.y == 0) {
-                alphas[b] = s0 * s0;
-                alphas[gridDim.z + b] = s0;
-            }
-        } else {
-            dsh = norm_divisor(partial, b);
-        }
-    }
+    if (threadIdx.x == 0) dsh = norm_divisor(partial, b);
     __syncthreads();
-    const float d = PRESCALE ? 1.0f : dsh;
-    const int ne = PRESCALE ? -esh : 0;
+    const float d = dsh;
     const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
     const uint16_t *x = in + b * rows * cols;
     const int j = threadIdx.x & 7, i0 = threadIdx.x >> 3;
@@ -848,8 +812,7 @@ __global__ __launch_bounds__(256) void normalize_vec_kernel(const uint16_t *in, 
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const float lo = __uint_as_float(u[k] << 16), hi = __uint_as_float(u[k] & 0xffff0000u);
-                if constexpr (PRESCALE) o[k] = rne_bf16x2(ldexpf(lo, ne), ldexpf(hi, ne));
-                else o[k] = rne_bf16x2(lo / d, hi / d);
+                o[k] = rne_bf16x2(lo / d, hi / d);
             }
             w = make_uint4(o[0], o[1], o[2], o[3]);
         }
@@ -873,33 +836,19 @@ __global__ __launch_bounds__(256) void normalize_vec_kernel(const uint16_t *in, 
 }
 
 // Writes S = x0 in the input layout (Rp x Cp, ld ldS) and T = x0^T (Cp x Rp, ld ldT),
-// x0 = bf16(u / d), d = bf16(bf16(||u||_F) + 1e-7), or with PRESCALE x0 = u 2^-e
-// and the first products' alphas (as normalize_vec_kernel); zeros outside rows x
-// cols.  S or T may be null.  64 x 64 tiles, transposed through LDS.
-template <bool PRESCALE>
+// x0 = bf16(u / d), d = bf16(bf16(||u||_F) + 1e-7) (the reference's bf16
+// normalisation: the output of steps == 0); zeros outside rows x cols.  S or T
+// may be null.  64 x 64 tiles, transposed through LDS.
 __global__ __launch_bounds__(256) void normalize_kernel(const uint16_t *in, int64_t rows, int64_t cols,
                                                         const float *partial, uint16_t *S, int64_t ldS, int64_t sS,
                                                         uint16_t *T, int64_t ldT, int64_t sT, int64_t Rp,
-                                                        int64_t Cp, float *alphas) {
+                                                        int64_t Cp) {
     __shared__ uint16_t tile[64][66];
     __shared__ float dsh;
-    __shared__ int esh;
     const int64_t b = blockIdx.z;
-    if (threadIdx.x == 0) {
-        if constexpr (PRESCALE) {
-            float s0;
-            prescale_of(partial, b, esh, s0);
-            if (blockIdx.x == 0 && blockIdx.y == 0) {
-                alphas[b] = s0 * s0;
-                alphas[gridDim.z + b] = s0;
-            }
-        } else {
-            dsh = norm_divisor(partial, b);
-        }
-    }
+    if (threadIdx.x == 0) dsh = norm_divisor(partial, b);
     __syncthreads();
-    const float d = PRESCALE ? 1.0f : dsh;
-    const int ne = PRESCALE ? -esh : 0;
+    const float d = dsh;
     const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
     const uint16_t *x = in + b * rows * cols;
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
@@ -908,7 +857,7 @@ __global__ __launch_bounds__(256) void normalize_kernel(const uint16_t *in, int6
         uint16_t h = 0;
         if (r < rows && c < cols) {
             const float v = bf16_to_f32(x[r * cols + c]);
-            h = (uint16_t)rne_bf16(PRESCALE ? ldexpf(v, ne) : v / d);
+            h = (uint16_t)rne_bf16(v / d);
         }
         tile[i][tx] = h;
         if (S && r < Rp && c < Cp) S[b * sS + r * ldS + c] = h;
@@ -922,12 +871,213 @@ __global__ __launch_bounds__(256) void normalize_kernel(const uint16_t *in, int6
     }
 }
 
+// ---------------------------------------------------------------------------
+// The iteration's prologue (steps >= 1): the update u (bf16) goes into the
+// workspace's first iterate X0 (transposed for tall matrices, zero padding),
+// with the sum of squares of each 64 x 64 tile of u, in one pass.  u comes
+// either from a bf16 input (SRC_COPY: msr_newton_schulz) or from the Muon
+// momentum step itself (SRC_PREPARE: msr_muon_fused_step, the arithmetic and
+// noise of muon_prepare_kernel, muon_sr/triton_muon_sr.py:18-50: the momentum
+// is updated in place and u is never written to memory).
+//
+// Sum of squares, in a fixed order whatever the source: thread t of a tile
+// handles rows t/8 and t/8 + 32 of the tile, columns 8 (t%8) .. 8 (t%8) + 7,
+// adding u^2 in fp32 element by element; the tile's 256 sums are reduced by
+// an LDS tree into tpart[b][tile] (tiles in row-major order over the padded
+// extents; padding adds +0); ns_finalize_kernel sums a matrix's tiles (thread
+// t: tiles t, t + 256, ...; then an LDS tree).
+//
+// Scaling: X0 = u / (||u||_F + 1e-7) is not rounded.  With e the exponent of
+// ||u||_F, X0 is kept as x0 = u when |e| <= PRO_ELIM (the first products then
+// multiply by s = 1 / (||u|| + 1e-7): A = s^2 x0 x0^T, X' = s (B' x0 + ...)),
+// else as x0 = u 2^-e with s0 = 2^e s (ns_rescale_kernel; bounded values keep
+// products in range).  Both are the same numbers: bf16 products are exact in
+// fp32 and every fp32 rounding of the products commutes with the power-of-two
+// scale while no partial result leaves the normal range.
+// ---------------------------------------------------------------------------
+
+constexpr int PRO_MAX = 96;       // matrices per prologue launch (kernel-argument table)
+constexpr int PRO_ELIM = 16;
+enum ProSrc : int { SRC_COPY = 0, SRC_PREPARE = 1 };
+
+struct PrologueArgs {
+    const uint16_t *in;              // SRC_COPY: u, [batch][rows][cols] (matrix 0 of this launch)
+    const void *grad[PRO_MAX];       // SRC_PREPARE: gradients (bf16, or fp32 with G32)
+    uint16_t *buf;                   // SRC_PREPARE: momentum of matrix 0 of this launch, [batch][rows][cols]
+    int64_t noise0;                  // SRC_PREPARE: noise offset of matrix 0 of this launch
+    float beta;
+    Noise ns;
+    int64_t rows, cols;
+    uint16_t *S; int64_t ldS, sS;    // X0 in the input layout (wide), or null
+    uint16_t *T; int64_t ldT, sT;    // X0 = u^T (tall), or null
+    int64_t Rp, Cp;                  // padded extents of u's layout
+    float *tpart;                    // [batch][ntiles] (matrix 0 of this launch)
+    int64_t ntx, ntiles;
+};
+
+template <int SRC, int MODE, bool NEST, bool G32, bool VEC>
+__global__ __launch_bounds__(256) void ns_prologue_kernel(PrologueArgs a) {
+    __shared__ __align__(16) uint16_t tile[64][72];
+    __shared__ float red[256];
+    const int64_t b = blockIdx.z;
+    const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+    const int64_t numel = a.rows * a.cols;
+    const int j = threadIdx.x & 7, i0 = threadIdx.x >> 3;
+    const float one_m_beta = 1.0f - a.beta;
+    float s = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int i = i0 + 32 * h;
+        const int64_t r = r0 + i, c = c0 + 8 * j;
+        uint32_t w[4] = {0u, 0u, 0u, 0u};   // u as bf16 pairs
+        if (r < a.rows && c < a.cols) {
+            const int64_t off = r * a.cols + c;
+            const int valid = (int)min<int64_t>(8, a.cols - c);
+            if constexpr (SRC == SRC_COPY) {
+                load_bf16x8<VEC>(a.in + b * numel, off, valid, w);
+            } else {
+                float gf[8], bf[8];
+                uint32_t wb[4];
+                if constexpr (G32) {
+                    load_f32x8<VEC>(static_cast<const float *>(a.grad[b]) + off, 0, valid, gf);
+                } else {
+                    uint32_t wg[4];
+                    load_bf16x8<VEC>(static_cast<const uint16_t *>(a.grad[b]) + off, 0, valid, wg);
+                    unpack8(wg, gf);
+                }
+                uint16_t *bp = a.buf + b * numel + off;
+                load_bf16x8<VEC>(bp, 0, valid, wb);
+                unpack8(wb, bf);
+                const int64_t o0 = a.noise0 + b * numel + off;
+                uint32_t rn[8];
+                if (VEC || MODE != NOISE_PHILOX8) {
+                    noise8<MODE>(a.ns, o0, valid, rn);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) rn[k] = (k < valid) ? noise1<MODE>(a.ns, o0 + k) : 0u;
+                }
+                float up[8];
+                uint32_t ob[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    float nb;
+                    muon_momentum<NEST>(gf[k], bf[k], a.beta, one_m_beta, nb, up[k]);   // :37-42
+                    ob[k] = sr_bf16(nb, rn[k]);                                         // :44-49
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    wb[k] = pack2(ob[2 * k], ob[2 * k + 1]);
+                    // :50 (RNE); lanes beyond `valid` hold u = 0
+                    w[k] = rne_bf16x2(2 * k < valid ? up[2 * k] : 0.0f, 2 * k + 1 < valid ? up[2 * k + 1] : 0.0f);
+                }
+                store_bf16x8<VEC>(bp, 0, valid, wb);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float lo = bf16_lo(w[k]), hi = bf16_hi(w[k]);
+            s = s + lo * lo;
+            s = s + hi * hi;
+        }
+        *reinterpret_cast<uint4 *>(&tile[i][8 * j]) = make_uint4(w[0], w[1], w[2], w[3]);
+        if (a.S && r < a.Rp && c < a.Cp) {
+            uint16_t *d = a.S + b * a.sS + r * a.ldS + c;
+            if (VEC) {
+                *reinterpret_cast<uint4 *>(d) = make_uint4(w[0], w[1], w[2], w[3]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) d[k] = (uint16_t)(w[k >> 1] >> (16 * (k & 1)));
+            }
+        }
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int wdt = 128; wdt > 0; wdt >>= 1) {
+        if (threadIdx.x < wdt) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + wdt];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) a.tpart[b * a.ntiles + (int64_t)blockIdx.y * a.ntx + blockIdx.x] = red[0];
+    if (!a.T) return;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int cc = i0 + 32 * h;            // T row (u column) within the tile
+        const int64_t c = c0 + cc, r = r0 + 8 * j;
+        if (c < a.Cp && r < a.Rp) {
+            uint32_t o[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                o[k] = (uint32_t)tile[8 * j + 2 * k][cc] | ((uint32_t)tile[8 * j + 2 * k + 1][cc] << 16);
+            uint16_t *d = a.T + b * a.sT + c * a.ldT + r;
+            if (VEC) {
+                *reinterpret_cast<uint4 *>(d) = make_uint4(o[0], o[1], o[2], o[3]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) d[k] = (uint16_t)(o[k >> 1] >> (16 * (k & 1)));
+            }
+        }
+    }
+}
+
+// Per matrix b: ||u||_F from the tile sums, the first products' factors
+// alphas[b] = s^2, alphas[batch + b] = s, and rexp[b]: 0 when x0 = u, else -e
+// (ns_rescale_kernel scales x0 by 2^-e).  ||u|| >= 2^64 (inf) gives e = 127 and
+// s = 0 (u / inf = 0, as the reference's normalisation); NaN propagates.
+__global__ __launch_bounds__(256) void ns_finalize_kernel(const float *tpart, int64_t ntiles, int64_t batch,
+                                                          float *alphas, int *rexp) {
+    __shared__ float red[256];
+    const int64_t b = blockIdx.x;
+    float s = 0.0f;
+    for (int64_t t = threadIdx.x; t < ntiles; t += 256) s = s + tpart[b * ntiles + t];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x != 0) return;
+    const float d = sqrtf(red[0]);
+    int e = 0;
+    float s0;
+    if (d == __builtin_huge_valf()) {
+        e = 127;
+        s0 = 0.0f;
+    } else {
+        if (d == d) (void)frexpf(d, &e);
+        s0 = ldexpf(1.0f / (d + 1e-7f), e);
+    }
+    const bool scaled = e > PRO_ELIM || e < -PRO_ELIM;
+    const float f = scaled ? s0 : ldexpf(s0, -e);   // exact for |e| <= PRO_ELIM: 1 / (||u|| + 1e-7)
+    alphas[b] = f * f;
+    alphas[batch + b] = f;
+    rexp[b] = scaled ? -e : 0;
+}
+
+// x0 <- x0 2^rexp[b] over matrix b's padded X0 (n8 16-byte chunks at X + b sX),
+// for the matrices the finalisation marked; the others return at once.  `bpm`
+// work-groups per matrix: work-group g serves matrix g / bpm.
+__global__ __launch_bounds__(256) void ns_rescale_kernel(uint16_t *X, int64_t sX, int64_t n8, int64_t bpm,
+                                                         const int *rexp) {
+    const int64_t b = blockIdx.x / bpm, part = blockIdx.x % bpm;
+    const int ne = rexp[b];
+    if (ne == 0) return;
+    uint4 *x = reinterpret_cast<uint4 *>(X + b * sX);
+    for (int64_t i = part * 256 + threadIdx.x; i < n8; i += bpm * 256) {
+        const uint4 v = x[i];
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = rne_bf16x2(ldexpf(bf16_lo(u[k]), ne), ldexpf(bf16_hi(u[k]), ne));
+        x[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
 static inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 struct NSLayout {
     int64_t m, n, mp, np;
     bool transposed;
-    size_t off_x[2], off_a, off_b, off_part, off_alpha, off_rho, off_r, total;
+    size_t off_x[2], off_a, off_b, off_part, off_alpha, off_rho, off_r, off_tpart, off_rexp, total;
+    int64_t ntiles;   // 64 x 64 tiles of the padded update (prologue sums of squares)
 };
 
 static NSLayout ns_layout(int64_t batch, int64_t rows, int64_t cols) {
@@ -949,6 +1099,9 @@ static NSLayout ns_layout(int64_t batch, int64_t rows, int64_t cols) {
     L.off_alpha = take((size_t)batch * 2 * 4);     // alphas of the first A and X' products
     L.off_rho = take((size_t)batch * L.mp * 4);    // residuals of A's diagonal
     L.off_r = take((size_t)batch * L.mp * 4);      // residuals of B''s diagonal
+    L.ntiles = (L.mp / 64) * (L.np / 64);
+    L.off_tpart = take((size_t)batch * L.ntiles * 4);   // tile sums of squares of the update
+    L.off_rexp = take((size_t)batch * 4);               // prologue scale exponents
     L.total = o;
     return L;
 }
@@ -1168,12 +1321,82 @@ struct NSApply {
     const uint16_t *inject;
 };
 
+// The Muon momentum step that produces the update inside the prologue
+// (msr_muon_fused_step): gradients, the momentum of the call's matrix 0 and the
+// index of that matrix in its momentum stack (the noise counter's base).
+struct NSPrepare {
+    const void *const *grads;
+    bool g32;
+    uint16_t *buf;
+    int64_t first;
+    float beta;
+    bool nesterov;
+    Noise ns;
+    int noise_mode;
+};
+
+// The prologue over `batch` matrices: X0 and the tile sums (see ns_prologue_kernel),
+// the first products' factors, and the rescale of out-of-range matrices.
+static int ns_prologue(const uint16_t *in, const NSPrepare *pp, int64_t batch, int64_t rows, int64_t cols,
+                       uint16_t *X0, float *tpart, float *alphas, int *rexp, const NSLayout &L, hipStream_t s) {
+    const int64_t numel = rows * cols, xs = L.mp * L.np;
+    const int64_t Rp = L.transposed ? L.np : L.mp;
+    const int64_t Cp = L.transposed ? L.mp : L.np;
+    bool vec = (cols % 8) == 0;
+    if (pp) {
+        vec = vec && aligned(pp->buf, 16);
+        for (int64_t i = 0; i < batch && vec; ++i) vec = aligned(pp->grads[i], 16);
+    } else {
+        vec = vec && aligned(in, 16);
+    }
+    for (int64_t b0 = 0; b0 < batch; b0 += PRO_MAX) {
+        const int64_t nb = std::min<int64_t>(PRO_MAX, batch - b0);
+        PrologueArgs a = {};
+        a.rows = rows; a.cols = cols;
+        a.S = L.transposed ? nullptr : X0 + b0 * xs; a.ldS = Cp; a.sS = xs;
+        a.T = L.transposed ? X0 + b0 * xs : nullptr; a.ldT = Rp; a.sT = xs;
+        a.Rp = Rp; a.Cp = Cp;
+        a.tpart = tpart + b0 * L.ntiles;
+        a.ntx = Cp / 64; a.ntiles = L.ntiles;
+        const dim3 grid((unsigned)(Cp / 64), (unsigned)(Rp / 64), (unsigned)nb);
+        if (!pp) {
+            a.in = in + b0 * numel;
+            if (vec) hipLaunchKernelGGL((ns_prologue_kernel<SRC_COPY, NOISE_TRITON, false, false, true>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((ns_prologue_kernel<SRC_COPY, NOISE_TRITON, false, false, false>), grid, dim3(256), 0, s, a);
+        } else {
+            for (int64_t i = 0; i < nb; ++i) a.grad[i] = pp->grads[b0 + i];
+            a.buf = pp->buf + b0 * numel;
+            a.noise0 = (pp->first + b0) * numel;
+            a.beta = pp->beta;
+            a.ns = pp->ns;
+#define PRO_LAUNCH(NEST, G, V) MSR_DISPATCH_NOISE(pp->noise_mode, M, hipLaunchKernelGGL((ns_prologue_kernel<SRC_PREPARE, M, NEST, G, V>), grid, dim3(256), 0, s, a))
+            if (pp->g32) {
+                if (pp->nesterov) { if (vec) { PRO_LAUNCH(true, true, true); } else { PRO_LAUNCH(true, true, false); } }
+                else { if (vec) { PRO_LAUNCH(false, true, true); } else { PRO_LAUNCH(false, true, false); } }
+            } else {
+                if (pp->nesterov) { if (vec) { PRO_LAUNCH(true, false, true); } else { PRO_LAUNCH(true, false, false); } }
+                else { if (vec) { PRO_LAUNCH(false, false, true); } else { PRO_LAUNCH(false, false, false); } }
+            }
+#undef PRO_LAUNCH
+        }
+        int rc = check_launch("ns_prologue_kernel");
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(ns_finalize_kernel, dim3((unsigned)batch), dim3(256), 0, s, tpart, L.ntiles, batch, alphas, rexp);
+    int rc = check_launch("ns_finalize_kernel");
+    if (rc) return rc;
+    const int64_t n8 = xs / 8, bpm = std::min<int64_t>((n8 + 255) / 256, 64);
+    hipLaunchKernelGGL(ns_rescale_kernel, dim3((unsigned)(bpm * batch)), dim3(256), 0, s, X0, xs, n8, bpm, rexp);
+    return check_launch("ns_rescale_kernel");
+}
+
 // Newton-Schulz of `batch` matrices; with `ap`, the last product updates the
-// parameters instead of writing `out` (which is then unused).  Arguments are
-// validated by the callers.
+// parameters instead of writing `out` (which is then unused); with `pp`, the
+// update is made by the Muon momentum step in the prologue (`in` is unused).
+// Arguments are validated by the callers.
 static int ns_run(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows, int64_t cols, int32_t steps,
                   float a_coef, float b_coef, float c_coef, void *workspace, const NSLayout &L, hipStream_t s,
-                  const NSApply *ap) {
+                  const NSApply *ap, const NSPrepare *pp = nullptr) {
     char *ws = static_cast<char *>(workspace);
     uint16_t *X[2] = {(uint16_t *)(ws + L.off_x[0]), (uint16_t *)(ws + L.off_x[1])};
     uint16_t *A = (uint16_t *)(ws + L.off_a);
@@ -1187,44 +1410,30 @@ static int ns_run(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows
 
     // 16-byte accesses when every row of the input starts 16-byte aligned
     const bool vec = (cols % 8) == 0 && aligned(in, 16);
-    if (vec)
-        hipLaunchKernelGGL(sumsq_kernel<true>, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
-    else
-        hipLaunchKernelGGL(sumsq_kernel<false>, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
-    int rc = check_launch("sumsq_kernel");
-    if (rc) return rc;
-    // prescale: x0 = u 2^-e and the first products' alphas (steps >= 1); else the
-    // reference's bf16 normalisation (steps == 0: the output is X0 itself)
-    auto normalize = [&](bool prescale, dim3 grid, uint16_t *S, int64_t ldS, int64_t sS, uint16_t *T, int64_t ldT,
-                         int64_t sT, int64_t Rp, int64_t Cp) {
-        const bool v = vec && aligned(S, 16) && (!T || aligned(T, 16)) && ldS % 8 == 0 && sS % 8 == 0 &&
-                       ldT % 8 == 0 && sT % 8 == 0 && Rp % 8 == 0 && Cp % 8 == 0;
-        if (v && prescale)
-            hipLaunchKernelGGL(normalize_vec_kernel<true>, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, T,
-                               ldT, sT, Rp, Cp, alphas);
-        else if (v)
-            hipLaunchKernelGGL(normalize_vec_kernel<false>, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, T,
-                               ldT, sT, Rp, Cp, alphas);
-        else if (prescale)
-            hipLaunchKernelGGL(normalize_kernel<true>, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, T, ldT,
-                               sT, Rp, Cp, alphas);
+    int rc = MSR_OK;
+    // steps == 0: the output is the reference's bf16 normalisation of the input
+    auto normalize = [&](dim3 grid, uint16_t *S, int64_t ldS, int64_t sS, int64_t Rp, int64_t Cp) {
+        const bool v = vec && aligned(S, 16) && ldS % 8 == 0 && sS % 8 == 0 && Rp % 8 == 0 && Cp % 8 == 0;
+        if (v)
+            hipLaunchKernelGGL(normalize_vec_kernel, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, nullptr,
+                               0, 0, Rp, Cp);
         else
-            hipLaunchKernelGGL(normalize_kernel<false>, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, T,
-                               ldT, sT, Rp, Cp, alphas);
+            hipLaunchKernelGGL(normalize_kernel, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, nullptr, 0,
+                               0, Rp, Cp);
         return check_launch("normalize_kernel");
     };
 
-    // Padded extents of the input layout: wide -> X = x0 (mp x np); tall -> X = x0^T, x0 is (np x mp).
-    const int64_t Rp = L.transposed ? L.np : L.mp;
-    const int64_t Cp = L.transposed ? L.mp : L.np;
     if (steps == 0) {
-        return normalize(false, dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch),
-                         out, cols, numel, nullptr, 0, 0, rows, cols);
+        if (vec)
+            hipLaunchKernelGGL(sumsq_kernel<true>, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
+        else
+            hipLaunchKernelGGL(sumsq_kernel<false>, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
+        if ((rc = check_launch("sumsq_kernel"))) return rc;
+        return normalize(dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch), out, cols,
+                         numel, rows, cols);
     }
-    uint16_t *Sx = L.transposed ? nullptr : X[0];
-    uint16_t *Tx = L.transposed ? X[0] : nullptr;
-    if ((rc = normalize(true, dim3((unsigned)(Cp / 64), (unsigned)(Rp / 64), (unsigned)batch), Sx, Cp, xs, Tx, Rp,
-                        xs, Rp, Cp)))
+    if ((rc = ns_prologue(in, pp, batch, rows, cols, X[0], (float *)(ws + L.off_tpart), alphas,
+                          (int *)(ws + L.off_rexp), L, s)))
         return rc;
 
     const int mp = (int)L.mp, np = (int)L.np;
@@ -1376,6 +1585,75 @@ int msr_muon_ns_apply(const uint16_t *upd, uint16_t *const *params, const uint32
     // `out` only marks the output layout for the last product: the store writes params[b]
     return ns_run(upd, const_cast<uint16_t *>(upd), batch, rows, cols, steps, a_coef, b_coef, c_coef, workspace, L,
                   (hipStream_t)stream, &ap);
+}
+
+int msr_muon_fused_step(const void *const *grads, int32_t grads_f32, uint16_t *buf, int64_t first, int64_t batch,
+                        int64_t rows, int64_t cols, float beta, int32_t nesterov, uint32_t prepare_seed, int32_t steps,
+                        float a_coef, float b_coef, float c_coef, uint16_t *out, uint16_t *const *params,
+                        const uint32_t *apply_seeds, float lr, float weight_decay, float scale, int32_t noise_mode,
+                        const uint16_t *inject_prepare, const uint16_t *inject_apply, void *workspace,
+                        size_t workspace_bytes, msr_stream_t stream) {
+    if (!grads || !buf || first < 0 || batch < 0 || rows <= 0 || cols <= 0 || steps < 1 ||
+        (batch > 0 && !params && !out) || (params && !apply_seeds)) {
+        set_error("msr_muon_fused_step: bad arguments (steps must be >= 1; params with seeds, or out)");
+        return MSR_ERR_ARG;
+    }
+    if (noise_mode < 0 || noise_mode > 2 ||
+        (noise_mode == NOISE_INJECT && (!inject_prepare || (params && !inject_apply)))) {
+        set_error("msr_muon_fused_step: bad noise_mode %d", (int)noise_mode);
+        return MSR_ERR_ARG;
+    }
+    if (batch == 0) return MSR_OK;
+    const NSLayout L = ns_layout(batch, rows, cols);
+    if (!workspace || workspace_bytes < L.total) {
+        set_error("msr_muon_fused_step: workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
+        return MSR_ERR_WORKSPACE;
+    }
+    if (L.mp > (1 << 30) || L.np > (1 << 30)) { set_error("msr_muon_fused_step: matrix too large"); return MSR_ERR_ARG; }
+    {
+        // the momentum and the parameters (or the output) are written while the gradients,
+        // the momentum and the workspace are read: none may share memory with another, except
+        // that gradients may repeat
+        const size_t gb = (grads_f32 ? 4 : 2) * (size_t)rows * (size_t)cols, pb = 2 * (size_t)rows * (size_t)cols;
+        const size_t bb = pb * (size_t)batch;
+        auto touch = [](const void *x, size_t nx, const void *y, size_t ny) {
+            return (uintptr_t)x < (uintptr_t)y + ny && (uintptr_t)y < (uintptr_t)x + nx;
+        };
+        if (touch(buf, bb, workspace, L.total) || (out && (touch(out, bb, workspace, L.total) || touch(out, bb, buf, bb)))) {
+            set_error("msr_muon_fused_step: the momentum, the output and the workspace must not overlap");
+            return MSR_ERR_OVERLAP;
+        }
+        for (int64_t i = 0; i < batch; ++i) {
+            if (!grads[i]) { set_error("msr_muon_fused_step: null gradient pointer %lld", (long long)i); return MSR_ERR_ARG; }
+            if (touch(grads[i], gb, buf, bb) || touch(grads[i], gb, workspace, L.total) || (out && touch(grads[i], gb, out, bb))) {
+                set_error("msr_muon_fused_step: gradient %lld overlaps the momentum, the output or the workspace", (long long)i);
+                return MSR_ERR_OVERLAP;
+            }
+        }
+        if (params) {
+            for (int64_t i = 0; i < batch; ++i) {
+                if (!params[i]) { set_error("msr_muon_fused_step: null parameter pointer %lld", (long long)i); return MSR_ERR_ARG; }
+                bool race = touch(params[i], pb, buf, bb) || touch(params[i], pb, workspace, L.total);
+                for (int64_t j = 0; j < batch && !race; ++j) race = touch(params[i], pb, grads[j], gb);
+                for (int64_t j = 0; j < i && !race; ++j) race = touch(params[i], pb, params[j], pb);
+                if (race) {
+                    set_error("msr_muon_fused_step: parameter %lld overlaps another operand", (long long)i);
+                    return MSR_ERR_OVERLAP;
+                }
+            }
+        }
+    }
+    Noise pns;
+    pns.key = seed_key(prepare_seed, 0);
+    pns.inject = inject_prepare;   // indexed by the element offset in the momentum stack
+    NSPrepare pp{grads, grads_f32 != 0, buf, first, beta, nesterov != 0, pns, (int)noise_mode};
+    if (!params)
+        return ns_run(nullptr, out, batch, rows, cols, steps, a_coef, b_coef, c_coef, workspace, L, (hipStream_t)stream,
+                      nullptr, &pp);
+    NSApply ap{params, apply_seeds, lr, weight_decay, scale, (int)noise_mode, inject_apply};
+    // the last product's store writes params[b]: its `out` only marks the output layout (never accessed)
+    return ns_run(nullptr, static_cast<uint16_t *>(workspace), batch, rows, cols, steps, a_coef, b_coef, c_coef,
+                  workspace, L, (hipStream_t)stream, &ap, &pp);
 }
 
 }  // extern "C"

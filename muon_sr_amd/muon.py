@@ -6,12 +6,19 @@ constructor signatures, param-group keys, state keys (``step``,
 ``momentum_buffer``; ``ema``/``ema_squared`` for AdamW groups), seeds,
 shape-group order and checkpoint behaviour.
 
-One Muon step of a shape group runs two library calls:
-  prepare   momentum lerp + nesterov, SR store of the momentum stack, RNE bf16
-            update (grads read through a pointer table: no stack copy);
+One Muon step of a chunk of 2-D matrices of one shape is one library call
+(msr_muon_fused_step):
+  prologue  momentum lerp + nesterov, SR store of the momentum stack, RNE bf16
+            update written straight into Newton-Schulz's first iterate with its
+            sum of squares (grads read through a pointer table: no stack copy,
+            no update stack);
   NS+apply  batched Newton-Schulz on bf16 MFMA whose last product applies
-            p <- SR(p*(1-lr*wd) - lr*scale*update) to every matrix of a chunk
-            (msr_muon_ns_apply: the NS output is never written).
+            p <- SR(p*(1-lr*wd) - lr*scale*update) to every wide matrix of the
+            chunk (the NS output is never written; tall matrices get it and one
+            apply launch).
+Tensors of more than 2 dims and ns_steps = 0 run prepare, NS and apply as
+separate calls (msr_muon_prepare, msr_newton_schulz / msr_muon_ns_apply,
+msr_muon_apply); the results are the same bit for bit.
 
 Extension (additive, off by default): an AdamW group of the hybrid optimizer
 with ``optim_bits=8`` runs the blockwise 8-bit AdamW of TritonAdamW8bit
@@ -148,6 +155,38 @@ def _ns_apply(upd_stack, params, lr, weight_decay, scale, seeds, ns_steps):
     _lib.check(rc, "msr_muon_ns_apply")
 
 
+def _fused_step(grads, buf, first, params, beta, nesterov, prepare_seed, ns_steps, lr, weight_decay, scale,
+                apply_seeds):
+    """The whole Muon step of `len(grads)` 2-D matrices of one shape in one library call
+    (msr_muon_fused_step): the momentum step of rows first.. of the momentum stack whose
+    row `first` starts at `buf` (seed `prepare_seed` over the stack's element offsets,
+    muon_sr/triton_muon_sr.py:18-50, 150-159) makes the update inside the Newton-Schulz
+    prologue, and the last product applies it to wide matrices' parameters
+    (muon_sr/triton_muon_sr.py:53-80, 160-169).  Tall matrices get the NS output and
+    one apply launch (their last product stores transposed, where the fused apply
+    measured slower).  Equal, bit for bit, to prepare, NS and apply run separately."""
+    L = _lib.lib()
+    k = len(grads)
+    rows, cols = params[0].shape
+    nbytes = _lib.ctypes.c_size_t(0)
+    _lib.check(L.msr_ns_workspace_bytes(k, rows, cols, _lib.ctypes.byref(nbytes)), "msr_ns_workspace_bytes")
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=buf.device)
+    a, b, c = NS_COEFFS
+    gtab = _lib.ptr_array([g.data_ptr() for g in grads])
+    f32 = int(grads[0].dtype == torch.float32)
+    wide = rows <= cols
+    out = None if wide else torch.empty(k, rows, cols, dtype=torch.bfloat16, device=buf.device)
+    ptab = _lib.ptr_array([p.data_ptr() for p in params]) if wide else None
+    stab = _lib.ptr_array(apply_seeds, _lib.ctypes.c_uint32) if wide else None
+    rc = L.msr_muon_fused_step(gtab, f32, buf.data_ptr(), first, k, rows, cols, beta, int(bool(nesterov)),
+                               prepare_seed, ns_steps, a, b, c, None if wide else out.data_ptr(), ptab, stab, lr,
+                               weight_decay, scale, _lib.noise_mode(), None, None, ws.data_ptr(), nbytes.value,
+                               _lib.stream_of(buf))
+    _lib.check(rc, "msr_muon_fused_step")
+    if not wide:
+        _run_apply(params, out, lr, weight_decay, scale, apply_seeds)
+
+
 def _check_param(p, name):
     _lib.require_gpu(p, name, RuntimeError)
     if not p.is_contiguous():
@@ -157,6 +196,10 @@ def _check_param(p, name):
 def _muon_step(p, grad, buf, beta, nesterov, ns_steps, lr, weight_decay, step, param_idx):
     """Single-param Muon step (muon_sr/triton_muon_sr.py:116-120)."""
     grad = _grad_operand(grad)
+    if p.dim() == 2 and ns_steps >= 1:
+        _fused_step([grad], buf, 0, [p.data], beta, nesterov, _deterministic_seed(step, param_idx, salt=0), ns_steps,
+                    lr, weight_decay, _ns_scale(p.shape), [_deterministic_seed(step, param_idx, salt=1)])
+        return
     update = torch.empty(p.shape, dtype=torch.bfloat16, device=p.device)
     _run_prepare([grad], buf, update, beta, nesterov, _deterministic_seed(step, param_idx, salt=0))
     _ns_apply(update.unsqueeze(0), [p.data], lr, weight_decay, _ns_scale(p.shape),
@@ -183,11 +226,19 @@ def _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns
                 _check_param(p, "TritonMuonSR")
             ordered = sorted(active, key=lambda q: buf_indices[id(q)])
             grads = [_bf16_contig(p.grad) for p in ordered]
+            k = max(1, NS_BATCH_NUMEL // ordered[0].numel())
+            scale = _ns_scale(shape)
+            if len(shape) == 2 and ns_steps >= 1:
+                for start in range(0, Na, k):
+                    chunk = ordered[start:start + k]
+                    seeds = [_deterministic_seed(step, shape_idx * 10000 + start + j, salt=1) for j in range(len(chunk))]
+                    _fused_step(grads[start:start + k], stacked_buf[start], start, [p.data for p in chunk], beta,
+                                nesterov, _deterministic_seed(step, shape_idx, salt=0), ns_steps, lr, weight_decay,
+                                scale, seeds)
+                continue
             work = torch.empty(Na, *shape, dtype=torch.bfloat16, device=active[0].device)
             _run_prepare(grads, stacked_buf, work, beta, nesterov, _deterministic_seed(step, shape_idx, salt=0))
             del grads
-            k = max(1, NS_BATCH_NUMEL // work[0].numel())
-            scale = _ns_scale(shape)
             for start in range(0, Na, k):
                 chunk = ordered[start:start + k]
                 seeds = [_deterministic_seed(step, shape_idx * 10000 + start + j, salt=1) for j in range(len(chunk))]

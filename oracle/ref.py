@@ -338,7 +338,7 @@ def ns_fp32(G, steps: int = 5, dtype=None):
     X = G.to(torch.float32 if dtype is None else dtype)
     transposed = X.size(-2) > X.size(-1)
     if transposed:
-        X = X.mT.contiguous()   # (a transposed bf16 right operand of a batched product is avoided on GPUs)
+        X = X.mT
     X = X / (X.norm(dim=(-2, -1), keepdim=True) + 1e-7)
     for _ in range(steps):
         A = X @ X.mT
@@ -356,7 +356,7 @@ def ns_bf16_torch(G, steps: int = 5):
     X = G.to(torch.bfloat16)
     transposed = X.size(-2) > X.size(-1)
     if transposed:
-        X = X.mT
+        X = X.mT.contiguous()   # (a transposed bf16 right operand of a batched product is avoided on GPUs)
     X = X / (X.norm(dim=(-2, -1), keepdim=True) + 1e-7)
     for _ in range(steps):
         A = X @ X.mT.contiguous()

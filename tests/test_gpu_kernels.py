@@ -809,3 +809,100 @@ def test_muon_ns_apply_equals_ns_then_apply(L, batch, rows, cols, mode):
     for o in offs:
         mask[o:o + numel] = False
     assert torch.equal(store[mask].view(torch.int16), before[mask].view(torch.int16))
+
+
+@pytest.mark.parametrize("batch,rows,cols,first,f32,nest", [
+    (3, 256, 512, 0, False, True), (2, 640, 256, 1, False, True), (3, 100, 60, 2, False, True),
+    (130, 64, 128, 0, False, True), (2, 61, 99, 0, True, False), (1, 96, 96, 0, True, True),
+    (4, 72, 40, 3, False, False)])
+@pytest.mark.parametrize("mode", [O.NOISE_TRITON, O.NOISE_PHILOX8, O.NOISE_INJECT])
+@pytest.mark.parametrize("fused_apply", [True, False])
+def test_muon_fused_step_equals_separate_calls(L, batch, rows, cols, first, f32, nest, mode, fused_apply):
+    """msr_muon_fused_step (the momentum step made inside the Newton-Schulz prologue, and
+    the apply in the last product's store or, with `out`, the NS output) equals
+    msr_muon_prepare over the momentum stack, then msr_newton_schulz, then msr_muon_apply,
+    bit for bit: momentum rows, parameters or NS output.  Wide, tall, padded and
+    non-multiple-of-8 shapes, a chunk that starts inside its stack (`first`: the noise
+    offsets continue the stack's), fp32 gradients, nesterov off, more matrices than one
+    prologue and one apply launch take (96, 128), all three noise streams."""
+    import ctypes
+    from muon_sr_amd.muon import newton_schulz, NS_COEFFS
+    a, b, c = NS_COEFFS
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(batch * rows + cols + 7 * mode + first)
+    numel = rows * cols
+    total = first + batch                      # the momentum stack holds `total` matrices
+    grads = [(torch.randn(rows, cols, device=DEV, generator=gen) * 1e-3) for _ in range(batch)]
+    grads = [g if f32 else g.to(torch.bfloat16) for g in grads]
+    stack0 = (torch.randn(total, rows, cols, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16)
+    params0 = (torch.randn(batch, rows, cols, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+    inj_p = torch.randint(0, 65536, (total * numel,), device=DEV, generator=gen, dtype=torch.int32).to(torch.int16) \
+        if mode == O.NOISE_INJECT else None
+    inj_a = torch.randint(0, 65536, (batch * numel,), device=DEV, generator=gen, dtype=torch.int32).to(torch.int16) \
+        if mode == O.NOISE_INJECT else None
+    beta, pseed = 0.95, 0x2545F491
+    seeds = [(0x9E3779B9 * (i + 3)) & 0xFFFFFFFF for i in range(batch)]
+    lr, wd, scale = 0.02, 0.01, max(1.0, rows / cols) ** 0.5
+    # separate calls: prepare over rows first.. of the stack (noise offsets from the stack's start)
+    stack_ref = stack0.clone()
+    work = torch.empty(batch, rows, cols, dtype=torch.bfloat16, device=DEV)
+    gtab = ptr_array([g.data_ptr() for g in grads])
+    # msr_muon_prepare numbers its noise from its own first row: seed and offsets of rows first..
+    # are those of the whole stack only when first == 0, so the reference runs it over the whole
+    # stack with the chunk's gradients in rows first.. and zeros before
+    if first:
+        pad = [torch.zeros(rows, cols, dtype=grads[0].dtype, device=DEV) for _ in range(first)]
+        full = pad + grads
+        work_full = torch.empty(total, rows, cols, dtype=torch.bfloat16, device=DEV)
+        check(L, L.msr_muon_prepare(ptr_array([g.data_ptr() for g in full]), int(f32), stack_ref.data_ptr(),
+                                    work_full.data_ptr(), numel, total, beta, int(nest), pseed, mode, ptr(inj_p),
+                                    stream()), "msr_muon_prepare")
+        work = work_full[first:].contiguous()
+        stack_ref[:first] = stack0[:first]
+    else:
+        check(L, L.msr_muon_prepare(gtab, int(f32), stack_ref.data_ptr(), work.data_ptr(), numel, batch, beta,
+                                    int(nest), pseed, mode, ptr(inj_p), stream()), "msr_muon_prepare")
+    X = newton_schulz(work)
+    p_ref = params0.clone()
+    seeds_c = ptr_array(seeds, ctypes.c_uint32)
+    check(L, L.msr_muon_apply(ptr_array([p_ref[i].data_ptr() for i in range(batch)]), X.data_ptr(), numel, batch, lr, wd,
+                              scale, seeds_c, mode, ptr(inj_a), stream()), "msr_muon_apply")
+    # the fused call
+    stack = stack0.clone()
+    prm = params0.clone()
+    nb = ctypes.c_size_t(0)
+    check(L, L.msr_ns_workspace_bytes(batch, rows, cols, ctypes.byref(nb)), "ws")
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    out = None if fused_apply else torch.empty(batch, rows, cols, dtype=torch.bfloat16, device=DEV)
+    check(L, L.msr_muon_fused_step(gtab, int(f32), stack[first].data_ptr(), first, batch, rows, cols, beta, int(nest),
+                                   pseed, 5, a, b, c, None if fused_apply else out.data_ptr(),
+                                   ptr_array([prm[i].data_ptr() for i in range(batch)]) if fused_apply else None,
+                                   seeds_c if fused_apply else None, lr, wd, scale, mode, ptr(inj_p),
+                                   ptr(inj_a) if fused_apply else None, ws.data_ptr(), nb.value, stream()),
+          "msr_muon_fused_step")
+    torch.cuda.synchronize()
+    assert torch.equal(stack.view(torch.int16), stack_ref.view(torch.int16))   # rows before `first` untouched
+    if fused_apply:
+        assert torch.equal(prm.view(torch.int16), p_ref.view(torch.int16))
+    else:
+        assert torch.equal(out.view(torch.int16), X.view(torch.int16))
+        assert torch.equal(prm.view(torch.int16), params0.view(torch.int16))
+
+
+@pytest.mark.parametrize("shape", [(2, 128, 256), (2, 256, 96)])
+@pytest.mark.parametrize("e", [-40, -20, -17, -16, -4, 0, 16, 17, 40])
+def test_newton_schulz_prologue_scales(L, shape, e):
+    """The prologue keeps X0 = u when the exponent e of ||u||_F has |e| <= 16 and rescales
+    it by 2^-e beyond (products of unscaled tiny or huge values would leave fp32's normal
+    range).  For ||u||_F around 2^e, e from -40 to 40 on both sides of the switch, the output
+    stays within the Newton-Schulz bound of the exact iteration of the same input (with its
+    1e-7, which dominates the smallest norms)."""
+    from muon_sr_amd.muon import newton_schulz
+    g = torch.Generator().manual_seed(11)
+    G = torch.randn(*shape, generator=g)
+    G = G / G[0].norm()
+    u = (G * 2.0 ** e).to(torch.bfloat16)
+    X = newton_schulz(u.to(DEV)).float().cpu()
+    ref = O.ns_fp32(u)
+    assert torch.isfinite(X).all()
+    assert rel_fro(X, ref) < 1e-2, rel_fro(X, ref)

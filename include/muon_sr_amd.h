@@ -198,8 +198,8 @@ int msr_muon_apply(uint16_t *const *params, const uint16_t *upd, int64_t numel_e
  *   X = G/(||G||_F + 1e-7);  repeat: A = X X^T; B = b A + c A A; X = a X + B X,
  * evaluated as B' = c A A + b A + a I, X = B' X: products accumulate in fp32,
  * A, B' and X are stored in bf16 between GEMMs.  The normalised input is not
- * rounded (G itself, or G scaled by a power of two when ||G||_F is below 2^-16
- * or above 2^17, is the first iterate, and 1/(||G||_F + 1e-7) goes into the
+ * rounded (G itself, or G scaled by a power of two when ||G||_F is below 2^-17
+ * or at least 2^16, is the first iterate, and 1/(||G||_F + 1e-7) goes into the
  * first products' scale factors), and the bf16 rounding residuals of the
  * diagonals of A and B' are carried in fp32 into the next product.  Within
  * 1e-2 relative Frobenius of the exact iteration on Gaussian inputs.

@@ -889,6 +889,59 @@ def test_muon_fused_step_equals_separate_calls(L, batch, rows, cols, first, f32,
         assert torch.equal(prm.view(torch.int16), params0.view(torch.int16))
 
 
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (2048, 2048),
+                                       (5632, 2048), (2048, 5632)])
+def test_muon_fused_step_at_config_shapes(L, rows, cols):
+    """At the Llama-3-8B (config 5) and config-4 shapes, two matrices of a chunk that starts at
+    row 1 of its momentum stack: msr_muon_fused_step equals msr_muon_prepare + msr_newton_schulz
+    + msr_muon_apply bit for bit (momentum and parameters; tall shapes through the NS output and
+    one apply launch, as the classes run them), in the reference's noise stream."""
+    import ctypes
+    from muon_sr_amd.muon import newton_schulz, NS_COEFFS
+    a, b, c = NS_COEFFS
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(rows + cols)
+    batch, first, total = 2, 1, 3
+    numel = rows * cols
+    mode = O.NOISE_TRITON
+    grads = [(torch.randn(rows, cols, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16) for _ in range(batch)]
+    stack0 = (torch.randn(total, rows, cols, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16)
+    params0 = (torch.randn(batch, rows, cols, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+    beta, pseed, lr, wd, scale = 0.95, 0x1234567, 0.02, 0.01, max(1.0, rows / cols) ** 0.5
+    seeds = [(0x85EBCA6B * (i + 1)) & 0xFFFFFFFF for i in range(batch)]
+    seeds_c = ptr_array(seeds, ctypes.c_uint32)
+    # separate calls over the whole stack (row 0 gets a zero gradient and is restored)
+    full = [torch.zeros(rows, cols, dtype=torch.bfloat16, device=DEV)] + grads
+    stack_ref = stack0.clone()
+    work = torch.empty(total, rows, cols, dtype=torch.bfloat16, device=DEV)
+    check(L, L.msr_muon_prepare(ptr_array([g.data_ptr() for g in full]), 0, stack_ref.data_ptr(), work.data_ptr(),
+                                numel, total, beta, 1, pseed, mode, None, stream()), "msr_muon_prepare")
+    stack_ref[0] = stack0[0]
+    X = newton_schulz(work[first:])
+    p_ref = params0.clone()
+    check(L, L.msr_muon_apply(ptr_array([p_ref[i].data_ptr() for i in range(batch)]), X.data_ptr(), numel, batch, lr,
+                              wd, scale, seeds_c, mode, None, stream()), "msr_muon_apply")
+    del work, X
+    # the fused call, as the classes make it
+    wide = rows <= cols
+    stack, prm = stack0.clone(), params0.clone()
+    nb = ctypes.c_size_t(0)
+    check(L, L.msr_ns_workspace_bytes(batch, rows, cols, ctypes.byref(nb)), "ws")
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    out = None if wide else torch.empty(batch, rows, cols, dtype=torch.bfloat16, device=DEV)
+    ptab = ptr_array([prm[i].data_ptr() for i in range(batch)])
+    check(L, L.msr_muon_fused_step(ptr_array([g.data_ptr() for g in grads]), 0, stack[first].data_ptr(), first, batch,
+                                   rows, cols, beta, 1, pseed, 5, a, b, c, None if wide else out.data_ptr(),
+                                   ptab if wide else None, seeds_c if wide else None, lr, wd, scale, mode, None, None,
+                                   ws.data_ptr(), nb.value, stream()), "msr_muon_fused_step")
+    if not wide:
+        check(L, L.msr_muon_apply(ptab, out.data_ptr(), numel, batch, lr, wd, scale, seeds_c, mode, None, stream()),
+              "msr_muon_apply")
+    torch.cuda.synchronize()
+    assert torch.equal(stack.view(torch.int16), stack_ref.view(torch.int16))
+    assert torch.equal(prm.view(torch.int16), p_ref.view(torch.int16))
+
+
 @pytest.mark.parametrize("shape", [(2, 128, 256), (2, 256, 96)])
 @pytest.mark.parametrize("e", [-40, -20, -17, -16, -4, 0, 16, 17, 40])
 def test_newton_schulz_prologue_scales(L, shape, e):

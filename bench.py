@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import statistics
 import os
 import platform
 import sys
@@ -436,6 +437,41 @@ def bench_muon(shapes, steps_timed, warmup, label):
     return out
 
 
+def bench_gemm_nt(reps=10):
+    """The NS GEMM kernel on its own (diagnostic, not a default config): msr_gemm_nt, a batch of 64
+    products 2048 x 2048 x 2048 (both operands K-contiguous, 4096 tiles of 256 x 256)."""
+    import torch
+    from muon_sr_amd import _lib
+    L = _lib.lib()
+    M = N = K = 2048
+    batch = 64
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(10)
+    P = torch.randn(batch, M, K, device="cuda:0", generator=gen).to(torch.bfloat16)
+    Q = torch.randn(batch, N, K, device="cuda:0", generator=gen).to(torch.bfloat16)
+    D = torch.empty(batch, M, N, device="cuda:0", dtype=torch.bfloat16)
+    s = torch.cuda.current_stream().cuda_stream
+
+    def run():
+        _lib.check(L.msr_gemm_nt(P.data_ptr(), K, M * K, Q.data_ptr(), K, N * K, None, 0, 0, D.data_ptr(), N, M * N,
+                                 M, N, K, batch, 1.0, 0.0, 0.0, s), "msr_gemm_nt")
+    for _ in range(3):
+        run()
+    evs = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run()
+        e1.record()
+        evs.append((e0, e1))
+    sync()
+    ms = statistics.median(a.elapsed_time(b) for a, b in evs)
+    fl = 2.0 * M * N * K * batch
+    del P, Q, D
+    torch.cuda.empty_cache()
+    return dict(batch=batch, m=M, n=N, k=K, ms=ms, tflops=fl / (ms * 1e9))
+
+
 def config4_shapes():
     return [(2048, 2048)] * 64 + [(5632, 2048)] * 32 + [(2048, 5632)] * 16
 
@@ -660,6 +696,10 @@ def main():
         r = bench_muon(config4_shapes(), steps_timed=3, warmup=1, label="config4")
         log(f"muon config4: {r}")
         configs["muon_ns_16L_d2048"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
+    if "gemm" in todo:
+        r = bench_gemm_nt()
+        log(f"gemm_nt: {r}")
+        configs["gemm_nt_64x2048^3"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
     if "centralize" in todo:
         r = bench_centralize()
         log(f"centralize: {r}")

@@ -616,6 +616,29 @@ def bench_wgrad(reps=5, tokens=8192):
     return out
 
 
+def device_copy_gbps(reps=20):
+    """A reference streaming rate measured in the same run: a 2 GiB -> 2 GiB device copy
+    (torch copy_, i.e. the runtime's device-to-device copy), median of `reps` launches."""
+    import torch
+    n = 1 << 29
+    a = torch.ones(n, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    evs = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        b.copy_(a)
+        e1.record()
+        evs.append((e0, e1))
+    sync()
+    ms = statistics.median(x.elapsed_time(y) for x, y in evs)
+    del a, b
+    torch.cuda.empty_cache()
+    return 2.0 * 4 * n / (ms * 1e6)
+
+
 def copy_calibration():
     """A plain device copy of known size (2^28 fp32: 1 GiB read + 1 GiB written per
     launch).  Profiled with FETCH_SIZE / WRITE_SIZE, it gives the factor that turns
@@ -674,6 +697,8 @@ def main():
 
     r8 = bench_adamw8bit(args.steps, args.warmup)
     log(f"adamw8bit: {r8}")
+    copy_gbps = device_copy_gbps()
+    log(f"device copy 2 GiB -> 2 GiB: {copy_gbps:.0f} GB/s")
     configs = {"adamw8bit_2^28": {k: round(v, 4) for k, v in r8.items()}}
     other = "triton" if args.noise == "philox8" else "philox8"
     if "adamw8bit" in todo:   # the same step with the other noise stream (triton: the reference's bits)
@@ -745,7 +770,10 @@ def main():
                                        "counter run, not measured in this run)",
                      "kernel": "adamw8bit_fast_kernel", "kernel_ms": round(r8["kernel_ms"], 4),
                      "kernel_ms_stat": "median of the timed launches (HIP events on the launch stream)",
-                     "bytes_per_launch": r8["bytes_per_step"]},
+                     "bytes_per_launch": r8["bytes_per_step"],
+                     # context, not the peak: the runtime's own device copy (half reads, half writes),
+                     # measured in this run
+                     "device_copy_gbps_this_run": round(copy_gbps, 1)},
         "cpu_baseline": cpu,
         "configs": configs,
     }

@@ -440,8 +440,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     using K1_ = std::integral_constant<int, 1>;
     using K2_ = std::integral_constant<int, 2>;
     using K3_ = std::integral_constant<int, 3>;
-    auto slab = [&](auto PK, auto QK, int stage, int knext, bool pkn, bool qkn, auto DG, bool dg) {
-        dma(pkn, qkn, stage ^ 1, knext);
+    auto slab = [&](auto PK, auto QK, int stage, int knext, bool pkn, bool qkn, auto DG, bool dg, bool load) {
+        if (load) dma(pkn, qkn, stage ^ 1, knext);   // wave-uniform: no load after the last slab of K
         __builtin_amdgcn_sched_barrier(0);
         frags(PK, QK, stage, 1, fa[1], fb[1]);
         mm(0);
@@ -475,7 +475,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     // slabs) and reads its own first fragments, so no fragment registers live
     // across ranges and the accumulators keep their registers.  The last slab
     // of a range loads the first slab of the next one (selected, not
-    // branched), or itself again at the end of K.
+    // branched); the last slab of K loads nothing (its first-fragment reads
+    // of the other stage, in the loop's layouts, are then unused).
     const int KT = a.K / BK, ktP = kP / BK, ktQ = kQ / BK;
     // DG: the range is the diagonal block [m0, m0 + 256) of X' = B' X + r X (EPI_X), whose
     // slab pair (kt - kt0) / 2 holds the rows of waves with wm = (kt - kt0) / 2.
@@ -488,9 +489,9 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         for (int kt = kt0; kt < kt1; kt += 2) {
             const bool more = kt + 2 < kt1;
             const bool dg = decltype(DG)::value && ((kt - kt0) >> 1) == wm;
-            slab(PK, QK, 0, (kt + 1) * BK, PK, QK, DG, dg);
+            slab(PK, QK, 0, (kt + 1) * BK, PK, QK, DG, dg, true);
             slab(PK, QK, 1, more ? (kt + 2) * BK : kafter, more ? decltype(PK)::value : pka,
-                 more ? decltype(QK)::value : qka, DG, dg);
+                 more ? decltype(QK)::value : qka, DG, dg, more || !end);
         }
     };
     dma(0 < ktP, 0 < ktQ, 0, 0);

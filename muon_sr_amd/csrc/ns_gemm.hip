@@ -26,8 +26,12 @@
 // described at the loads).  Each K substep is one
 // scheduling region in which the MFMAs are interleaved with the next
 // substep's fragment reads; the next slab's loads are all issued at the start
-// of the slab.
+// of the slab.  Work-groups are persistent, one per CU: each walks its share
+// of the tiles, and a tile's epilogue (each wave staging its own sub-tile
+// through LDS, no work-group barrier) overlaps the loads of the next tile's
+// first slab, and its stores the next tile's first MFMAs.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "common.hpp"
@@ -70,7 +74,8 @@ struct GemmArgs {
     int d_vec;         // D rows allow 16-byte stores (set by launch_gemm)
     int dt_vec;        // DT rows allow 16-byte stores (set by launch_gemm)
     int tiles;         // tiles per matrix
-    int per_xcd;       // 1-D grid over a multiple of 8 matrices, whole matrices per XCD
+    int total;         // virtual work-groups (tiles) of the launch
+    int per_xcd;       // tile order over a multiple of 8 matrices, whole matrices per XCD
     int gm;            // operand layouts by K range (GM_*)
     int sracc;         // 0, or 1 + the noise mode of the SR-accumulating store (D = acc)
     int zero_init;     // SR-accumulating store: acc reads as zero
@@ -149,6 +154,7 @@ __device__ __forceinline__ void apply_chunk(const ApplyTab &ap, uint16_t *P, con
 constexpr int NXCD = 8;
 constexpr int GROUP_M = 4;
 constexpr int PER_XCD_TILES = 64;
+constexpr int PERSIST_MAX = 32;   // tiles per persistent work-group, at most
 
 __device__ __forceinline__ int xcd_remap(int w, int total) {
     const int per = total / NXCD;          // full rounds
@@ -190,16 +196,50 @@ __device__ __forceinline__ void decode_tile(const GemmArgs &a, int t, int &ti, i
     }
 }
 
+// Virtual work-group v -> (matrix bz, tile origin m0, n0), per the order above.
+__device__ __forceinline__ void locate_tile(const GemmArgs &a, int v, int64_t &bz, int &m0, int &n0) {
+    int ti, tj;
+    if (a.per_xcd) {
+        const int slot = v / NXCD;
+        bz = (int64_t)(v % NXCD) + (int64_t)NXCD * (slot / a.tiles);
+        decode_tile(a, slot % a.tiles, ti, tj);
+    } else {
+        bz = v / a.tiles;
+        decode_tile(a, xcd_remap(v % a.tiles, a.tiles), ti, tj);
+    }
+    m0 = ti * BM;
+    n0 = tj * BN;
+}
+
+// Work-group barrier that orders LDS accesses only: this wave's global stores
+// stay in flight across it.
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Wait until at most N vector memory operations of this wave are outstanding
+// (s_waitcnt: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at their maxima).
+// Vector memory operations complete in issue order, so every operation issued
+// before the last N has completed.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // LDS: four variables of 33 KiB, one per slab: P stage 0, P stage 1, Q stage
 // 0, Q stage 1 (32 KiB used each).  Separate variables tell the compiler that
 // the fragment reads of one stage do not alias the direct-to-LDS loads into
 // the other stage (it would otherwise wait for those loads before the reads).
-// After the K loop the same memory stages the 256 x 256 bf16 output tile with
-// a row pitch of SPITCH elements (528 B: 16-byte aligned rows; the 8-byte
-// writes of 32 consecutive rows hit each bank at most twice), rows 64 v ..
-// 64 v + 63 in variable v.
+// After the K loop the stage-1 variables hold the epilogue's staging (stage 0
+// receives the next tile's first slab meanwhile): each wave owns EST_BYTES,
+// 32 rows of its 64-column sub-tile with a row pitch of EPITCH elements (144 B:
+// 16-byte aligned rows; the 8-byte writes of 32 consecutive rows hit each
+// bank at most twice), waves 0-3 in P stage 1 and waves 4-7 in Q stage 1.
 constexpr int SPITCH = 264;
 constexpr int SLAB_BYTES = 64 * SPITCH * 2;
 __shared__ __attribute__((aligned(1024))) char lds_p0[SLAB_BYTES];
@@ -209,11 +249,9 @@ __shared__ __attribute__((aligned(1024))) char lds_q1[SLAB_BYTES];
 
 __device__ __forceinline__ char *lds_p(int stage) { return stage ? lds_p1 : lds_p0; }
 __device__ __forceinline__ char *lds_q(int stage) { return stage ? lds_q1 : lds_q0; }
-__device__ __forceinline__ uint16_t *stg_row(int r) {
-    const int v = r >> 6, o = (r & 63) * (SPITCH * 2);
-    char *b = v == 0 ? lds_p0 : v == 1 ? lds_p1 : v == 2 ? lds_q0 : lds_q1;
-    return reinterpret_cast<uint16_t *>(b + o);
-}
+constexpr int EPITCH = 72;
+constexpr int EST_BYTES = 32 * EPITCH * 2;
+static_assert(4 * EST_BYTES <= SLAB_BYTES, "epilogue staging fits the stage-1 variables");
 
 // Operand layouts of a product, by K range.  A slab of an operand is read
 // either row-major (its rows are the tile's 256 rows, K-contiguous: "R") or
@@ -249,24 +287,18 @@ enum : int { EPI_NONE = 0, EPI_A = 1, EPI_B = 2, EPI_X = 3 };
 // rounding (noise mode SRACC), as msr_sr_accum does with the RNE bf16 product.
 // APPLY >= 0 (with OUT_D or OUT_DT): the store applies the Muon update to the
 // parameters of a.ap with noise mode APPLY instead of writing D / DT.
-template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, int GM, int SRACC = -1, int EPI = EPI_NONE, int APPLY = -1>
+// FULL: every tile of the launch is in range (Mv == M, Nv == N) with 16-byte
+// rows of D / DT (or SRACC >= 0, whose stores are never bounded), so its
+// stores are unconditional.
+template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, int GM, int SRACC = -1, int EPI = EPI_NONE, int APPLY = -1,
+          bool FULL = false>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
-    int ti, tj;
-    int64_t bz;
-    if (a.per_xcd) {
-        const int slot = (int)(blockIdx.x / NXCD);
-        bz = (int64_t)(blockIdx.x % NXCD) + (int64_t)NXCD * (slot / a.tiles);
-        decode_tile(a, slot % a.tiles, ti, tj);
-    } else {
-        decode_tile(a, xcd_remap(blockIdx.x, gridDim.x), ti, tj);
-        bz = blockIdx.y;
-    }
-    const int m0 = ti * BM, n0 = tj * BN;
     constexpr bool HAS_KK = GM == GM_TRI_P || GM == GM_TRI_PQ || GM == GM_KK;
     constexpr bool HAS_RK = GM == GM_RK || GM == GM_TRI_P || GM == GM_TRI_PQ;
     constexpr bool HAS_RR = GM == GM_RR || GM == GM_TRI_PQ;
-    const int kP = GM == GM_KK ? a.K : HAS_KK ? m0 : 0;
-    const int kQ = GM == GM_RR ? 0 : GM == GM_TRI_PQ ? n0 : a.K;
+    // K ranges of the tile at (m0, n0): P is read K-major for k < kP, Q for k < kQ
+    auto kp_of = [&](int tm0) { return GM == GM_KK ? a.K : HAS_KK ? tm0 : 0; };
+    auto kq_of = [&](int tn0) { return GM == GM_RR ? 0 : GM == GM_TRI_PQ ? tn0 : a.K; };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -284,23 +316,36 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     //  * K-major slab (64 rows x 512 B): chunk c of row k is stored at c ^ 4
     //    (k & 3), so the four rows of one transposing read fall in different
     //    banks; block 8 i + w = rows 16 i + 2 w + l / 32, physical chunk l % 32.
-    // Per-lane byte offsets are fixed; the row block (i) and the K slab go into
-    // the scalar offset.
+    // Per-lane byte offsets are fixed per tile; the row block (i) and the K
+    // slab go into the scalar offset.
     const int lrow = lane >> 3;
     const int lchunk = (lane & 7) ^ (4 * (wave & 1) + (lane >> 4));
     const int kr = 2 * wave + (lane >> 5);
     const int kc = (lane & 31) ^ (4 * (kr & 3));
-    const __amdgpu_buffer_rsrc_t rP = __builtin_amdgcn_make_buffer_rsrc((void *)(a.P + bz * a.sP), (short)0, 0x7fffffff, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rQ = __builtin_amdgcn_make_buffer_rsrc((void *)(a.Q + bz * a.sQ), (short)0, 0x7fffffff, 0x00020000);
-    const uint32_t voP_r = (uint32_t)(((int64_t)(m0 + wave * 8 + lrow) * a.ldp + lchunk * 8) * 2);
-    const uint32_t voQ_r = (uint32_t)(((int64_t)(n0 + wave * 8 + lrow) * a.ldq + lchunk * 8) * 2);
-    const uint32_t voP_k = (uint32_t)(((int64_t)kr * a.ldp + m0 + 8 * kc) * 2);
-    const uint32_t voQ_k = (uint32_t)(((int64_t)kr * a.ldq + n0 + 8 * kc) * 2);
     const uint32_t ldbP = (uint32_t)(a.ldp * 2), ldbQ = (uint32_t)(a.ldq * 2);
-    // Load j (0..7) of a slab: P block j/2 for even j, Q block j/2 for odd j,
-    // each in the layout of the slab's K range (pk, qk: wave-uniform).
-    auto dma = [&](bool pk, bool qk, int stage, int k0) {
-        const uint32_t vp = pk ? voP_k : voP_r, vq = qk ? voQ_k : voQ_r;
+    // A tile's operands: its matrices and the lane's byte offsets in their
+    // row-major (pr, qr) and K-major (pk, qk) slabs at k = 0.
+    struct TileOps {
+        const uint16_t *P, *Q;
+        uint32_t pr, qr, pk, qk;
+    };
+    auto tile_ops = [&](int64_t tbz, int tm0, int tn0) {
+        TileOps o;
+        o.P = a.P + tbz * a.sP;
+        o.Q = a.Q + tbz * a.sQ;
+        o.pr = (uint32_t)(((int64_t)(tm0 + wave * 8 + lrow) * a.ldp + lchunk * 8) * 2);
+        o.qr = (uint32_t)(((int64_t)(tn0 + wave * 8 + lrow) * a.ldq + lchunk * 8) * 2);
+        o.pk = (uint32_t)(((int64_t)kr * a.ldp + tm0 + 8 * kc) * 2);
+        o.qk = (uint32_t)(((int64_t)kr * a.ldq + tn0 + 8 * kc) * 2);
+        return o;
+    };
+    // Load j (0..7) of the slab at k0 of tile o into `stage`: P block j/2 for
+    // even j, Q block j/2 for odd j, each in the layout of the slab's K range
+    // (pk, qk: wave-uniform).
+    auto dma = [&](const TileOps &o, bool pk, bool qk, int stage, int k0) {
+        const __amdgpu_buffer_rsrc_t rP = __builtin_amdgcn_make_buffer_rsrc((void *)o.P, (short)0, 0x7fffffff, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rQ = __builtin_amdgcn_make_buffer_rsrc((void *)o.Q, (short)0, 0x7fffffff, 0x00020000);
+        const uint32_t vp = pk ? o.pk : o.pr, vq = qk ? o.qk : o.qr;
         const uint32_t ip = pk ? 16 * ldbP : 64 * ldbP, iq = qk ? 16 * ldbQ : 64 * ldbQ;
         const uint32_t kp = pk ? k0 * ldbP : k0 * 2, kq = qk ? k0 * ldbQ : k0 * 2;
 #pragma unroll
@@ -357,207 +402,263 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         }
     };
 
-    f32x16_t acc[4][2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
-    bf16x8_t fa[2][4], fb[2][2];
-    auto mm = [&](int b) {
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
-                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], fa[b][mi], acc[mi][ni], 0, 0, 0);
-    };
-    // EPI_X: the term r[m] X[m][n] of X' = B' X + r X enters the accumulators as the product
-    // of X with the diagonal matrix bf16(r), over the K block k in [m0, m0 + 256) that holds
-    // the tile's own rows of X (the first 4 slabs of the RK range).  Wave (wm, wn) owns rows
-    // 128 wm .. 128 wm + 127 of the tile, which are slabs 2 wm and 2 wm + 1 of that block: in
-    // slab 2 wm + st, substep ks, the diagonal crosses the 32-row block mi = 2 st + ks / 2,
-    // and lane l's fragment (row r32, k = 8 khalf + e) holds it at e = r32 - 16 (ks & 1) -
-    // 8 khalf.  That is 16 extra MFMAs per wave and no extra memory traffic.
-    uint32_t rb16[4] = {0u, 0u, 0u, 0u};   // bf16(r) at rows 128 wm + 32 mi + r32
-    if constexpr (EPI == EPI_X) {
-        const float *rv = a.rvec + bz * a.sv + m0 + wm * 128 + r32;
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi) rb16[mi] = rne_bf16(rv[32 * mi]);
-    }
-    auto mmdiag = [&](int b, auto ST, auto KS) {
-        constexpr int ks = decltype(KS)::value;
-        constexpr int mi = 2 * decltype(ST)::value + (ks >> 1);
-        const int e = r32 - 16 * (ks & 1) - 8 * khalf;
-        const uint32_t v = (unsigned)e < 8u ? rb16[mi] << (16 * (e & 1)) : 0u;
-        const int w = e >> 1;
-        const u32x4_t words = {w == 0 ? v : 0u, w == 1 ? v : 0u, w == 2 ? v : 0u, w == 3 ? v : 0u};
-        const bf16x8_t rf = __builtin_bit_cast(bf16x8_t, words);
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], rf, acc[mi][ni], 0, 0, 0);
-    };
-    // dg: this wave's rows meet the slab pair of the diagonal block being computed
-    auto diag = [&](auto DG, bool dg, int b, int stage, auto KS) {
-        if constexpr (decltype(DG)::value) {
-            if (dg) {
-                if (stage == 0) mmdiag(b, std::integral_constant<int, 0>{}, KS);
-                else mmdiag(b, std::integral_constant<int, 1>{}, KS);
-            }
+    // Persistent work-groups: work-group g computes the tiles of virtual
+    // work-groups g, g + G, g + 2 G, ... (G = gridDim.x, a multiple of 8 when
+    // the grid is smaller than the launch, so each runs on the XCD that the
+    // tile order assumes).  The first slab of a work-group's next tile streams
+    // into stage 0 while the epilogue of its current tile runs.
+    int v = blockIdx.x;
+    int64_t bz;
+    int m0, n0;
+    locate_tile(a, v, bz, m0, n0);
+    dma(tile_ops(bz, m0, n0), 0 < kp_of(m0), 0 < kq_of(n0), 0, 0);
+    // EPI_X: the fp32 residuals r of the tile's rows 128 wm + 32 mi + r32, loaded
+    // a tile ahead (with the tile's first slab) so that no load waits at its start
+    float rf0 = 0.0f, rf1 = 0.0f, rf2 = 0.0f, rf3 = 0.0f;
+    auto load_r = [&](int64_t tbz, int tm0) __attribute__((always_inline)) {
+        if constexpr (EPI == EPI_X) {
+            const float *rv = a.rvec + tbz * a.sv + tm0 + wm * 128 + r32;
+            rf0 = rv[0];
+            rf1 = rv[32];
+            rf2 = rv[64];
+            rf3 = rv[96];
         }
     };
-    // Each substep is one scheduling region: its 8 MFMAs interleaved with the
-    // fragment reads of the next substep (6 row-major, 8 or 12 with K-major
-    // operands: 4 reads per row-major P, 8 per K-major P, 2 or 4 for Q).
-    auto pattern = [&](auto PK, auto QK) {
-        constexpr int NDS = (decltype(PK)::value ? 8 : 4) + (decltype(QK)::value ? 4 : 2);
-        if constexpr (NDS == 6) {
-#pragma unroll
-            for (int x = 0; x < 6; ++x) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                if (x == 0 || x == 2) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            }
-        } else {
-#pragma unroll
-            for (int x = 0; x < 8; ++x) {
-                if (NDS == 12 && (x & 1) == 0) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-                else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            }
-        }
-    };
-    // One K slab from `stage` (layouts PK, QK) while slab `knext` (layouts
-    // pkn, qkn) streams into the other stage.  All 8 global->LDS loads of the
-    // next slab are issued before the slab's first MFMA: the operands arrive
-    // through L2 with a latency tail (misses to the Infinity Cache / HBM), and
-    // the wait at the end of the slab then has the whole slab to cover it
-    // (measured +3..19% over spreading the loads across the substeps).  The
-    // last substep's MFMAs overlap the next slab's first fragment reads, in
-    // this slab's layouts; after the last slab of a K range these are unused.
-    using K0_ = std::integral_constant<int, 0>;
-    using K1_ = std::integral_constant<int, 1>;
-    using K2_ = std::integral_constant<int, 2>;
-    using K3_ = std::integral_constant<int, 3>;
-    auto slab = [&](auto PK, auto QK, int stage, int knext, bool pkn, bool qkn, auto DG, bool dg, bool load) {
-        if (load) dma(pkn, qkn, stage ^ 1, knext);   // wave-uniform: no load after the last slab of K
-        __builtin_amdgcn_sched_barrier(0);
-        frags(PK, QK, stage, 1, fa[1], fb[1]);
-        mm(0);
-        diag(DG, dg, 0, stage, K0_{});
-        pattern(PK, QK);
-        __builtin_amdgcn_sched_barrier(0);
-        frags(PK, QK, stage, 2, fa[0], fb[0]);
-        mm(1);
-        diag(DG, dg, 1, stage, K1_{});
-        pattern(PK, QK);
-        __builtin_amdgcn_sched_barrier(0);
-        frags(PK, QK, stage, 3, fa[1], fb[1]);
-        mm(0);
-        diag(DG, dg, 0, stage, K2_{});
-        pattern(PK, QK);
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(0);   // own loads of the next slab landed, own reads of this stage done
-        __syncthreads();                 // everyone's
-        frags(PK, QK, stage ^ 1, 0, fa[0], fb[0]);
-        mm(1);
-        diag(DG, dg, 1, stage, K3_{});
-        pattern(PK, QK);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    using T_ = std::true_type;
-    using F_ = std::false_type;
-
-    // The K ranges [0, kP) (KK), [kP, kQ) (RK) and [kQ, K) (RR) run as
-    // separate loops with uniform bodies, one after the other.  Each range
-    // starts in stage 0 with its first slab landed (ranges are multiples of 4
-    // slabs) and reads its own first fragments, so no fragment registers live
-    // across ranges and the accumulators keep their registers.  The last slab
-    // of a range loads the first slab of the next one (selected, not
-    // branched); the last slab of K loads nothing (its first-fragment reads
-    // of the other stage, in the loop's layouts, are then unused).
-    const int KT = a.K / BK, ktP = kP / BK, ktQ = kQ / BK;
-    // DG: the range is the diagonal block [m0, m0 + 256) of X' = B' X + r X (EPI_X), whose
-    // slab pair (kt - kt0) / 2 holds the rows of waves with wm = (kt - kt0) / 2.
-    auto range = [&](auto PK, auto QK, int kt0, int kt1, auto DG) {
-        const bool end = kt1 >= KT;
-        const int kafter = end ? (kt1 - 1) * BK : kt1 * BK;
-        const bool pka = end ? decltype(PK)::value : kt1 < ktP, qka = end ? decltype(QK)::value : kt1 < ktQ;
-        frags(PK, QK, 0, 0, fa[0], fb[0]);
-#pragma clang loop unroll(disable)
-        for (int kt = kt0; kt < kt1; kt += 2) {
-            const bool more = kt + 2 < kt1;
-            const bool dg = decltype(DG)::value && ((kt - kt0) >> 1) == wm;
-            slab(PK, QK, 0, (kt + 1) * BK, PK, QK, DG, dg, true);
-            slab(PK, QK, 1, more ? (kt + 2) * BK : kafter, more ? decltype(PK)::value : pka,
-                 more ? decltype(QK)::value : qka, DG, dg, more || !end);
-        }
-    };
-    dma(0 < ktP, 0 < ktQ, 0, 0);
+    load_r(bz, m0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if constexpr (HAS_KK) {
-        if (0 < ktP) range(T_{}, T_{}, 0, ktP, F_{});
-    }
-    if constexpr (EPI == EPI_X) {   // GM_TRI_P: the RK range starts at k = m0 (ktP + 4 <= ktQ)
-        range(F_{}, T_{}, ktP, ktP + 4, T_{});
-        if (ktP + 4 < ktQ) range(F_{}, T_{}, ktP + 4, ktQ, F_{});
-    } else if constexpr (HAS_RK) {
-        if (ktP < ktQ) range(F_{}, T_{}, ktP, ktQ, F_{});
-    }
-    if constexpr (HAS_RR) {
-        if (ktQ < KT) range(F_{}, F_{}, ktQ, KT, F_{});
-    }
+    for (;;) {
+        const TileOps ot = tile_ops(bz, m0, n0);
+        const int kP = kp_of(m0), kQ = kq_of(n0);
+        f32x16_t acc[4][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // ---------------- epilogue ----------------
-    // The output tile is staged through LDS as bf16 (row pitch SPITCH) so that
-    // global traffic is 16-byte row chunks: C is loaded that way, D is stored
-    // that way, and the transposed copy (DT) is gathered column-wise from LDS.
-    // A symmetric product stores its upper tiles only.
-    // Lane l holds D[m = l % 32][n = 8r + 4(l / 32) + q] of each 32x32 MFMA tile.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();   // every wave is done with the operand slabs
-    const int ec = tid & 31, er = tid >> 5;   // 16-byte chunk in a row, first row (16 rows per pass)
-    if constexpr (HAS_C) {
-        const uint16_t *Cb = a.C + bz * a.sC + (int64_t)m0 * a.ldc + n0 + 8 * ec;
-#pragma unroll 4
-        for (int it = 0; it < 16; ++it) {
-            const int r = er + 16 * it;
-            *reinterpret_cast<uint4 *>(stg_row(r) + 8 * ec) =
-                *reinterpret_cast<const uint4 *>(Cb + (int64_t)r * a.ldc);
+        bf16x8_t fa[2][4], fb[2][2];
+        auto mm = [&](int b) {
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], fa[b][mi], acc[mi][ni], 0, 0, 0);
+        };
+        // EPI_X: the term r[m] X[m][n] of X' = B' X + r X enters the accumulators as the product
+        // of X with the diagonal matrix bf16(r), over the K block k in [m0, m0 + 256) that holds
+        // the tile's own rows of X (the first 4 slabs of the RK range).  Wave (wm, wn) owns rows
+        // 128 wm .. 128 wm + 127 of the tile, which are slabs 2 wm and 2 wm + 1 of that block: in
+        // slab 2 wm + st, substep ks, the diagonal crosses the 32-row block mi = 2 st + ks / 2,
+        // and lane l's fragment (row r32, k = 8 khalf + e) holds it at e = r32 - 16 (ks & 1) -
+        // 8 khalf.  That is 16 extra MFMAs per wave and no extra memory traffic.
+        uint32_t rb16[4] = {0u, 0u, 0u, 0u};   // bf16(r) at rows 128 wm + 32 mi + r32
+        if constexpr (EPI == EPI_X) {
+            const uint32_t p01 = rne_bf16x2(rf0, rf1), p23 = rne_bf16x2(rf2, rf3);
+            rb16[0] = p01 & 0xffffu;
+            rb16[1] = p01 >> 16;
+            rb16[2] = p23 & 0xffffu;
+            rb16[3] = p23 >> 16;
         }
-        __syncthreads();
-    }
-    // (alpha * acc (+ beta * C)) (+ diag where m == n), rounded to bf16 by the
-    // hardware conversion; the multiply is skipped for alpha == 1 (x * 1 == x
-    // for every non-NaN x) and the diagonal term outside diagonal tiles.
-    // The Newton-Schulz epilogues (EPI_*) are described at their enum.
-    const float alpha = a.alpha_b ? a.alpha_b[bz] : a.alpha;
-    float rowv[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // EPI_B: rho at rows m0 + wm 128 + 32 mi + r32
-    if constexpr (EPI == EPI_B) {
-        const float *rv = a.rvec + bz * a.sv + m0 + wm * 128 + r32;
+        auto mmdiag = [&](int b, auto ST, auto KS) {
+            constexpr int ks = decltype(KS)::value;
+            constexpr int mi = 2 * decltype(ST)::value + (ks >> 1);
+            const int e = r32 - 16 * (ks & 1) - 8 * khalf;
+            const uint32_t v = (unsigned)e < 8u ? rb16[mi] << (16 * (e & 1)) : 0u;
+            const int w = e >> 1;
+            const u32x4_t words = {w == 0 ? v : 0u, w == 1 ? v : 0u, w == 2 ? v : 0u, w == 3 ? v : 0u};
+            const bf16x8_t rf = __builtin_bit_cast(bf16x8_t, words);
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) rowv[mi] = rv[32 * mi];
-    }
-    // Diagonal tiles: the lane's diagonal elements, at most one per 32-row block mi, and
-    // their fp32 rounding residuals (selects in the unrolled loop, stores after it).
-    float res[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    bool has_res[4] = {false, false, false, false};
-    auto stage_out = [&](auto scaled, auto dg) {
+            for (int ni = 0; ni < 2; ++ni)
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], rf, acc[mi][ni], 0, 0, 0);
+        };
+        // dg: this wave's rows meet the slab pair of the diagonal block being computed
+        auto diag = [&](auto DG, bool dg, int b, int stage, auto KS) {
+            if constexpr (decltype(DG)::value) {
+                if (dg) {
+                    if (stage == 0) mmdiag(b, std::integral_constant<int, 0>{}, KS);
+                    else mmdiag(b, std::integral_constant<int, 1>{}, KS);
+                }
+            }
+        };
+        // Each substep is one scheduling region: its 8 MFMAs interleaved with the
+        // fragment reads of the next substep (6 row-major, 8 or 12 with K-major
+        // operands: 4 reads per row-major P, 8 per K-major P, 2 or 4 for Q).
+        auto pattern = [&](auto PK, auto QK) {
+            constexpr int NDS = (decltype(PK)::value ? 8 : 4) + (decltype(QK)::value ? 4 : 2);
+            if constexpr (NDS == 6) {
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
+                for (int x = 0; x < 6; ++x) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    if (x == 0 || x == 2) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                }
+            } else {
+#pragma unroll
+                for (int x = 0; x < 8; ++x) {
+                    if (NDS == 12 && (x & 1) == 0) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                    else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                }
+            }
+        };
+        // One K slab from `stage` (layouts PK, QK) while slab `knext` (layouts
+        // pkn, qkn) streams into the other stage.  All 8 global->LDS loads of the
+        // next slab are issued before the slab's first MFMA: the operands arrive
+        // through L2 with a latency tail (misses to the Infinity Cache / HBM), and
+        // the wait at the end of the slab then has the whole slab to cover it
+        // (measured +3..19% over spreading the loads across the substeps).  The
+        // last substep's MFMAs overlap the next slab's first fragment reads, in
+        // this slab's layouts; after the last slab of a K range these are unused.
+        using K0_ = std::integral_constant<int, 0>;
+        using K1_ = std::integral_constant<int, 1>;
+        using K2_ = std::integral_constant<int, 2>;
+        using K3_ = std::integral_constant<int, 3>;
+        auto slab = [&](auto PK, auto QK, int stage, int knext, bool pkn, bool qkn, auto DG, bool dg, bool load) {
+            if (load) dma(ot, pkn, qkn, stage ^ 1, knext);   // wave-uniform: no load after the last slab of K
+            __builtin_amdgcn_sched_barrier(0);
+            frags(PK, QK, stage, 1, fa[1], fb[1]);
+            mm(0);
+            diag(DG, dg, 0, stage, K0_{});
+            pattern(PK, QK);
+            __builtin_amdgcn_sched_barrier(0);
+            frags(PK, QK, stage, 2, fa[0], fb[0]);
+            mm(1);
+            diag(DG, dg, 1, stage, K1_{});
+            pattern(PK, QK);
+            __builtin_amdgcn_sched_barrier(0);
+            frags(PK, QK, stage, 3, fa[1], fb[1]);
+            mm(0);
+            diag(DG, dg, 0, stage, K2_{});
+            pattern(PK, QK);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0);   // own loads of the next slab landed, own reads of this stage done
+            __syncthreads();                 // everyone's
+            frags(PK, QK, stage ^ 1, 0, fa[0], fb[0]);
+            mm(1);
+            diag(DG, dg, 1, stage, K3_{});
+            pattern(PK, QK);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+
+        // The K ranges [0, kP) (KK), [kP, kQ) (RK) and [kQ, K) (RR) run as
+        // separate loops with uniform bodies, one after the other.  Each range
+        // starts in stage 0 with its first slab landed (ranges are multiples of 4
+        // slabs) and reads its own first fragments, so no fragment registers live
+        // across ranges and the accumulators keep their registers.  The last slab
+        // of a range loads the first slab of the next one (selected, not
+        // branched); the last slab of K loads nothing (its first-fragment reads
+        // of the other stage, in the loop's layouts, are then unused).
+        const int KT = a.K / BK, ktP = kP / BK, ktQ = kQ / BK;
+        // DG: the range is the diagonal block [m0, m0 + 256) of X' = B' X + r X (EPI_X), whose
+        // slab pair (kt - kt0) / 2 holds the rows of waves with wm = (kt - kt0) / 2.
+        auto range = [&](auto PK, auto QK, int kt0, int kt1, auto DG) {
+            const bool end = kt1 >= KT;
+            const int kafter = end ? (kt1 - 1) * BK : kt1 * BK;
+            const bool pka = end ? decltype(PK)::value : kt1 < ktP, qka = end ? decltype(QK)::value : kt1 < ktQ;
+            frags(PK, QK, 0, 0, fa[0], fb[0]);
+#pragma clang loop unroll(disable)
+            for (int kt = kt0; kt < kt1; kt += 2) {
+                const bool more = kt + 2 < kt1;
+                const bool dg = decltype(DG)::value && ((kt - kt0) >> 1) == wm;
+                slab(PK, QK, 0, (kt + 1) * BK, PK, QK, DG, dg, true);
+                slab(PK, QK, 1, more ? (kt + 2) * BK : kafter, more ? decltype(PK)::value : pka,
+                     more ? decltype(QK)::value : qka, DG, dg, more || !end);
+            }
+        };
+        if constexpr (HAS_KK) {
+            if (0 < ktP) range(T_{}, T_{}, 0, ktP, F_{});
+        }
+        if constexpr (EPI == EPI_X) {   // GM_TRI_P: the RK range starts at k = m0 (ktP + 4 <= ktQ)
+            range(F_{}, T_{}, ktP, ktP + 4, T_{});
+            if (ktP + 4 < ktQ) range(F_{}, T_{}, ktP + 4, ktQ, F_{});
+        } else if constexpr (HAS_RK) {
+            if (ktP < ktQ) range(F_{}, T_{}, ktP, ktQ, F_{});
+        }
+        if constexpr (HAS_RR) {
+            if (ktQ < KT) range(F_{}, F_{}, ktQ, KT, F_{});
+        }
+
+        // ---------------- epilogue ----------------
+        // Each wave stages its own 128 x 64 sub-tile through its private LDS
+        // region, one 32-row block mi at a time.  LDS accesses of one wave
+        // execute in order, so the epilogue needs no work-group barrier.  Global
+        // traffic is 16-byte chunks of whole 128-byte row segments: C is loaded
+        // that way, D is stored that way, and the transposed copy (DT) is
+        // gathered column-wise.  A symmetric product stores its upper tiles only.
+        // Lane l holds D[m = l % 32][n = 8r + 4(l / 32) + q] of each 32x32 MFMA tile.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();   // every wave is done with the operand slabs
+        const int vn = v + (int)gridDim.x;
+        const bool next = vn < a.total;
+        // The epilogue's lane indices, from an opaque copy of the thread index:
+        // its addresses are then formed here instead of being hoisted out of
+        // the tile loop, where they would stay live through the K loop.
+        int e_tid = tid;
+        asm volatile("" : "+v"(e_tid));
+        const int e_lane = e_tid & 63;
+        const int e_r32 = e_lane & 31, e_khalf = e_lane >> 5;
+        const int crow = e_lane >> 3, cchk = e_lane & 7;     // chunk accesses: rows crow + 8 i, 16-byte chunk cchk
+        const int wm0 = m0 + 128 * wm, wn0 = n0 + 64 * wn;   // the wave's sub-tile
+        char *const wst = (wave < 4 ? lds_p1 : lds_q1) + (wave & 3) * EST_BYTES;
+        auto est = [&](int row) __attribute__((always_inline)) { return reinterpret_cast<uint16_t *>(wst + row * (EPITCH * 2)); };
+        // (alpha * acc (+ beta * C)) (+ diag where m == n), rounded to bf16 by the
+        // hardware conversion; the multiply is skipped for alpha == 1 (x * 1 == x
+        // for every non-NaN x) and the diagonal term outside diagonal tiles.
+        // The Newton-Schulz epilogues (EPI_*) are described at their enum.
+        const float alpha = a.alpha_b ? a.alpha_b[bz] : a.alpha;
+        float rho0 = 0.0f, rho1 = 0.0f, rho2 = 0.0f, rho3 = 0.0f;   // EPI_B: rho at rows wm0 + 32 mi + e_r32
+        if constexpr (EPI == EPI_B) {
+            const float *rv = a.rvec + bz * a.sv + wm0 + e_r32;
+            rho0 = rv[0];
+            rho1 = rv[32];
+            rho2 = rv[64];
+            rho3 = rv[96];
+        }
+        // The next tile's first slab into stage 0
+        int64_t nbz = bz;
+        int nm0 = m0, nn0 = n0;
+        if (next) {
+            locate_tile(a, vn, nbz, nm0, nn0);
+            dma(tile_ops(nbz, nm0, nn0), 0 < kp_of(nm0), 0 < kq_of(nn0), 0, 0);
+            load_r(nbz, nm0);
+        }
+        // Diagonal tiles: the lane's diagonal element of each 32-row block mi (at most
+        // one) and its fp32 rounding residual (selects in the unrolled loop, a store
+        // after the block).
+        const bool dtile = m0 == n0 && (a.diag != 0.0f || EPI == EPI_A || EPI == EPI_B);
+        auto block = [&](auto MI, auto SC, auto DG, auto FL) __attribute__((always_inline)) {
+            constexpr int mi = decltype(MI)::value;
+            constexpr bool fl = decltype(FL)::value;
+            if constexpr (HAS_C) {   // this block of C into the staging
+                const uint16_t *Cb = a.C + bz * a.sC + (int64_t)(wm0 + 32 * mi + crow) * a.ldc + wn0 + 8 * cchk;
+                const int64_t l8 = 8 * a.ldc;
+                const uint4 c0 = *reinterpret_cast<const uint4 *>(Cb);
+                const uint4 c1 = *reinterpret_cast<const uint4 *>(Cb + l8);
+                const uint4 c2 = *reinterpret_cast<const uint4 *>(Cb + 2 * l8);
+                const uint4 c3 = *reinterpret_cast<const uint4 *>(Cb + 3 * l8);
+                *reinterpret_cast<uint4 *>(est(crow) + 8 * cchk) = c0;
+                *reinterpret_cast<uint4 *>(est(crow + 8) + 8 * cchk) = c1;
+                *reinterpret_cast<uint4 *>(est(crow + 16) + 8 * cchk) = c2;
+                *reinterpret_cast<uint4 *>(est(crow + 24) + 8 * cchk) = c3;
+            }
+            const float rho = mi == 0 ? rho0 : mi == 1 ? rho1 : mi == 2 ? rho2 : rho3;
+            float res_mi = 0.0f;
+            bool has_mi = false;
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int ml = wm * 128 + mi * 32 + r32;
-                    const int nl = wn * 64 + ni * 32 + 8 * r + 4 * khalf;
-                    uint2 *sp = reinterpret_cast<uint2 *>(stg_row(ml) + nl);
+                    const int ml = wm * 128 + mi * 32 + e_r32;                  // tile row
+                    const int nl = wn * 64 + ni * 32 + 8 * r + 4 * e_khalf;     // tile column
+                    uint2 *sp = reinterpret_cast<uint2 *>(est(e_r32) + ni * 32 + 8 * r + 4 * e_khalf);
                     float v[4] = {acc[mi][ni][4 * r], acc[mi][ni][4 * r + 1], acc[mi][ni][4 * r + 2],
                                   acc[mi][ni][4 * r + 3]};
                     float cv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                    if constexpr (decltype(scaled)::value) {
+                    if constexpr (decltype(SC)::value) {
 #pragma unroll
                         for (int q = 0; q < 4; ++q) v[q] = alpha * v[q];
                     }
@@ -570,153 +671,189 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
 #pragma unroll
                         for (int q = 0; q < 4; ++q) v[q] = v[q] + a.beta * cv[q];
                     }
-                    if constexpr (decltype(dg)::value) {   // m0 == n0 here
+                    if constexpr (decltype(DG)::value) {   // m0 == n0 here
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
                             const bool on = ml == nl + q;
                             if constexpr (EPI == EPI_B)
-                                v[q] = on ? v[q] + (a.diag + rowv[mi] * (a.beta + 2.0f * alpha * cv[q])) : v[q];
+                                v[q] = on ? v[q] + (a.diag + rho * (a.beta + 2.0f * alpha * cv[q])) : v[q];
                             else if constexpr (EPI != EPI_A)
                                 v[q] = on ? v[q] + a.diag : v[q];
                         }
                     }
                     const uint2 w = make_uint2(rne_bf16x2(v[0], v[1]), rne_bf16x2(v[2], v[3]));
                     *sp = w;
-                    if constexpr (decltype(dg)::value && (EPI == EPI_A || EPI == EPI_B)) {
+                    if constexpr (decltype(DG)::value && (EPI == EPI_A || EPI == EPI_B)) {
                         const float rq[4] = {bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)};
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
                             const bool on = ml == nl + q;
-                            res[mi] = on ? v[q] - rq[q] : res[mi];
-                            has_res[mi] = has_res[mi] || on;
+                            res_mi = on ? v[q] - rq[q] : res_mi;
+                            has_mi = has_mi || on;
                         }
                     }
                 }
             }
-        }
-    };
-    if (ti == tj && (a.diag != 0.0f || EPI == EPI_A || EPI == EPI_B)) {
-        if (alpha == 1.0f) stage_out(std::false_type{}, std::true_type{});
-        else stage_out(std::true_type{}, std::true_type{});
-        if constexpr (EPI == EPI_A || EPI == EPI_B) {
-            float *resid = a.resid + bz * a.sv + m0 + wm * 128 + r32;
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-                if (has_res[mi]) resid[32 * mi] = res[mi];
-        }
-    } else {
-        if (alpha == 1.0f) stage_out(std::false_type{}, std::false_type{});
-        else stage_out(std::true_type{}, std::false_type{});
-    }
-    __syncthreads();
-    if constexpr (SRACC >= 0) {
-        // acc <- SR(f32(acc) + f32(tile)), 8 elements (one noise8 group) per access
-        uint16_t *Db = a.D + bz * a.sD;
-#pragma unroll 4
-        for (int it = 0; it < 16; ++it) {
-            const int r = er + 16 * it;
-            const int64_t o0 = (int64_t)(m0 + r) * a.ldd + n0 + 8 * ec;
-            const uint4 w = *reinterpret_cast<const uint4 *>(stg_row(r) + 8 * ec);
-            uint4 c = make_uint4(0u, 0u, 0u, 0u);
-            if (!a.zero_init) c = *reinterpret_cast<const uint4 *>(Db + o0);
-            const uint32_t gw[4] = {w.x, w.y, w.z, w.w}, cw[4] = {c.x, c.y, c.z, c.w};
-            uint32_t rn[8], o[4];
-            noise8<SRACC>(a.ns, o0, 8, rn);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                o[j] = pack2(sr_bf16(bf16_lo(cw[j]) + bf16_lo(gw[j]), rn[2 * j]),
-                             sr_bf16(bf16_hi(cw[j]) + bf16_hi(gw[j]), rn[2 * j + 1]));
-            *reinterpret_cast<uint4 *>(Db + o0) = make_uint4(o[0], o[1], o[2], o[3]);
-        }
-    } else if constexpr (OUT_D && APPLY >= 0) {
-        uint16_t *Pp = a.ap.p[bz];
-        Noise ns;
-        ns.key = seed_key(a.ap.seed[bz], 0);
-        ns.inject = a.ap.inject ? a.ap.inject + bz * a.ap.numel : nullptr;
-        const int n = n0 + 8 * ec;
-#pragma unroll 2
-        for (int it = 0; it < 16; ++it) {
-            const int r = er + 16 * it;
-            const int m = m0 + r;
-            if (m >= a.Mv || n >= a.Nv) continue;
-            const uint4 w = *reinterpret_cast<const uint4 *>(stg_row(r) + 8 * ec);
-            const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-            const int64_t off = (int64_t)m * a.ldd + n;
-            const int valid = min(8, a.Nv - n);
-            apply_chunk<APPLY>(a.ap, Pp, ns, off, valid, a.d_vec != 0, u, apply_load(Pp, off, valid, a.d_vec != 0));
-        }
-    } else if constexpr (OUT_D) {
-        uint16_t *Db = a.D + bz * a.sD;
-#pragma unroll 4
-        for (int it = 0; it < 16; ++it) {
-            const int r = er + 16 * it;
-            const int m = m0 + r, n = n0 + 8 * ec;
-            if (m >= a.Mv) continue;
-            const uint4 w = *reinterpret_cast<const uint4 *>(stg_row(r) + 8 * ec);
-            uint16_t *dp = Db + (int64_t)m * a.ldd + n;
-            if (a.d_vec && n + 8 <= a.Nv) {
-                st_nt4(dp, u32x4_t{w.x, w.y, w.z, w.w});   // streaming store: measured 0.4-1.6 % faster NS
-            } else {
-                const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (n + j < a.Nv) dp[j] = (uint16_t)(u[j >> 1] >> (16 * (j & 1)));
+            if constexpr (decltype(DG)::value && (EPI == EPI_A || EPI == EPI_B)) {
+                if (has_mi) a.resid[bz * a.sv + wm0 + 32 * mi + e_r32] = res_mi;
             }
-        }
-    }
-    // Transposed copy: T[n][m] = tile[m][n].  Lanes of a wave take 64
-    // consecutive n (a conflict-free LDS row read per element) and each stores
-    // 8 consecutive m (16 bytes) of its row n.
-    if constexpr (OUT_DT && APPLY >= 0) {
-        uint16_t *Pp = a.ap.p[bz];
-        Noise ns;
-        ns.key = seed_key(a.ap.seed[bz], 0);
-        ns.inject = a.ap.inject ? a.ap.inject + bz * a.ap.numel : nullptr;
-        const int nl = tid & 255;
-        const int n = n0 + nl;
-        const int c0 = (tid >> 8) * 16;
-        u32x4_t pw[16];
+            // block mi of the output: rows wm0 + 32 mi + crow + 8 i, columns wn0 + 8 cchk
+            const int bm0 = wm0 + 32 * mi;
+            if constexpr (SRACC >= 0) {
+                // acc <- SR(f32(acc) + f32(tile)), 8 elements (one noise8 group) per access
+                uint16_t *Db = a.D + bz * a.sD;
+                uint4 c[4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int m = m0 + 8 * (c0 + i);
-            pw[i] = (n < a.Nv && m < a.Mv) ? apply_load(Pp, (int64_t)n * a.lddt + m, min(8, a.Mv - m), a.dt_vec != 0)
-                                           : u32x4_t{0u, 0u, 0u, 0u};
-        }
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t o0 = (int64_t)(bm0 + crow + 8 * i) * a.ldd + wn0 + 8 * cchk;
+                    c[i] = a.zero_init ? make_uint4(0u, 0u, 0u, 0u) : *reinterpret_cast<const uint4 *>(Db + o0);
+                }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int c = c0 + i;
-            uint32_t u[4];
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t o0 = (int64_t)(bm0 + crow + 8 * i) * a.ldd + wn0 + 8 * cchk;
+                    const uint4 w = *reinterpret_cast<const uint4 *>(est(crow + 8 * i) + 8 * cchk);
+                    const uint32_t gw[4] = {w.x, w.y, w.z, w.w}, cw[4] = {c[i].x, c[i].y, c[i].z, c[i].w};
+                    uint32_t rn[8], o[4];
+                    noise8<SRACC>(a.ns, o0, 8, rn);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                u[j] = (uint32_t)stg_row(8 * c + 2 * j)[nl] | ((uint32_t)stg_row(8 * c + 2 * j + 1)[nl] << 16);
-            const int m = m0 + 8 * c;
-            if (n >= a.Nv || m >= a.Mv) continue;
-            apply_chunk<APPLY>(a.ap, Pp, ns, (int64_t)n * a.lddt + m, min(8, a.Mv - m), a.dt_vec != 0, u, pw[i]);
-        }
-    } else if constexpr (OUT_DT) {
-        uint16_t *Tb = a.DT + bz * a.sDT;
-        const int64_t ldt = a.lddt;
-        const int tm0 = m0, tn0 = n0, tMv = a.Mv, tNv = a.Nv;
-        const bool tvec = a.dt_vec;
-        const int nl = tid & 255;                 // tile column = output row
-        const int n = tn0 + nl;
-#pragma unroll 4
-        for (int c = (tid >> 8) * 16; c < (tid >> 8) * 16 + 16; ++c) {   // 8-row chunk of the tile = 8 output columns
-            uint32_t u[4];
+                    for (int j = 0; j < 4; ++j)
+                        o[j] = pack2(sr_bf16(bf16_lo(cw[j]) + bf16_lo(gw[j]), rn[2 * j]),
+                                     sr_bf16(bf16_hi(cw[j]) + bf16_hi(gw[j]), rn[2 * j + 1]));
+                    *reinterpret_cast<uint4 *>(Db + o0) = make_uint4(o[0], o[1], o[2], o[3]);
+                }
+            } else if constexpr (OUT_D && APPLY >= 0) {
+                uint16_t *Pp = a.ap.p[bz];
+                Noise ns;
+                ns.key = seed_key(a.ap.seed[bz], 0);
+                ns.inject = a.ap.inject ? a.ap.inject + bz * a.ap.numel : nullptr;
+                const int n = wn0 + 8 * cchk;
+                const bool vec = fl || a.d_vec != 0;
+                u32x4_t pw[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                u[j] = (uint32_t)stg_row(8 * c + 2 * j)[nl] | ((uint32_t)stg_row(8 * c + 2 * j + 1)[nl] << 16);
-            const int m = tm0 + 8 * c;
-            if (n >= tNv) continue;
-            uint16_t *tp = Tb + (int64_t)n * ldt + m;
-            if (tvec && m + 8 <= tMv) {
-                *reinterpret_cast<uint4 *>(tp) = make_uint4(u[0], u[1], u[2], u[3]);
-            } else {
+                for (int i = 0; i < 4; ++i) {
+                    const int m = bm0 + crow + 8 * i;
+                    const bool in = fl || (m < a.Mv && n < a.Nv);
+                    pw[i] = in ? apply_load(Pp, (int64_t)m * a.ldd + n, fl ? 8 : min(8, a.Nv - n), vec)
+                               : u32x4_t{0u, 0u, 0u, 0u};
+                }
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (m + j < tMv) tp[j] = (uint16_t)(u[j >> 1] >> (16 * (j & 1)));
+                for (int i = 0; i < 4; ++i) {
+                    const int m = bm0 + crow + 8 * i;
+                    if (!fl && (m >= a.Mv || n >= a.Nv)) continue;
+                    const uint4 w = *reinterpret_cast<const uint4 *>(est(crow + 8 * i) + 8 * cchk);
+                    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+                    apply_chunk<APPLY>(a.ap, Pp, ns, (int64_t)m * a.ldd + n, fl ? 8 : min(8, a.Nv - n), vec, u, pw[i]);
+                }
+            } else if constexpr (OUT_D) {
+                uint16_t *Db = a.D + bz * a.sD;
+                const int n = wn0 + 8 * cchk;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int m = bm0 + crow + 8 * i;
+                    const uint4 w = *reinterpret_cast<const uint4 *>(est(crow + 8 * i) + 8 * cchk);
+                    uint16_t *dp = Db + (int64_t)m * a.ldd + n;
+                    if (fl) {
+                        st_nt4(dp, u32x4_t{w.x, w.y, w.z, w.w});   // streaming store: measured 0.4-1.6 % faster NS
+                    } else if (m < a.Mv) {
+                        if (a.d_vec && n + 8 <= a.Nv) {
+                            st_nt4(dp, u32x4_t{w.x, w.y, w.z, w.w});
+                        } else {
+                            const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                            for (int j = 0; j < 8; ++j)
+                                if (n + j < a.Nv) dp[j] = (uint16_t)(u[j >> 1] >> (16 * (j & 1)));
+                        }
+                    }
+                }
             }
-        }
+            // Transposed copy: T[n][m] = tile[m][n].  Lane l takes column wn0 + l
+            // (a conflict-free LDS row read per element) and stores 8
+            // consecutive m (16 bytes) of its row n per chunk c.
+            if constexpr (OUT_DT && APPLY >= 0) {
+                uint16_t *Pp = a.ap.p[bz];
+                Noise ns;
+                ns.key = seed_key(a.ap.seed[bz], 0);
+                ns.inject = a.ap.inject ? a.ap.inject + bz * a.ap.numel : nullptr;
+                const int n = wn0 + e_lane;
+                const bool vec = fl || a.dt_vec != 0;
+                u32x4_t pw[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int m = bm0 + 8 * c;
+                    const bool in = fl || (n < a.Nv && m < a.Mv);
+                    pw[c] = in ? apply_load(Pp, (int64_t)n * a.lddt + m, fl ? 8 : min(8, a.Mv - m), vec)
+                               : u32x4_t{0u, 0u, 0u, 0u};
+                }
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    uint32_t u[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        u[j] = (uint32_t)est(8 * c + 2 * j)[e_lane] | ((uint32_t)est(8 * c + 2 * j + 1)[e_lane] << 16);
+                    const int m = bm0 + 8 * c;
+                    if (!fl && (n >= a.Nv || m >= a.Mv)) continue;
+                    apply_chunk<APPLY>(a.ap, Pp, ns, (int64_t)n * a.lddt + m, fl ? 8 : min(8, a.Mv - m), vec, u, pw[c]);
+                }
+            } else if constexpr (OUT_DT) {
+                uint16_t *Tb = a.DT + bz * a.sDT;
+                const int n = wn0 + e_lane;                // tile column = output row
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {             // 8-row chunk of the block = 8 output columns
+                    uint32_t u[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        u[j] = (uint32_t)est(8 * c + 2 * j)[e_lane] | ((uint32_t)est(8 * c + 2 * j + 1)[e_lane] << 16);
+                    const int m = bm0 + 8 * c;
+                    uint16_t *tp = Tb + (int64_t)n * a.lddt + m;
+                    if (fl) {
+                        *reinterpret_cast<uint4 *>(tp) = make_uint4(u[0], u[1], u[2], u[3]);
+                    } else if (n < a.Nv) {
+                        if (a.dt_vec && m + 8 <= a.Mv) {
+                            *reinterpret_cast<uint4 *>(tp) = make_uint4(u[0], u[1], u[2], u[3]);
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < 8; ++j)
+                                if (m + j < a.Mv) tp[j] = (uint16_t)(u[j >> 1] >> (16 * (j & 1)));
+                        }
+                    }
+                }
+            }
+        };
+        using I0_ = std::integral_constant<int, 0>;
+        using I1_ = std::integral_constant<int, 1>;
+        using I2_ = std::integral_constant<int, 2>;
+        using I3_ = std::integral_constant<int, 3>;
+        auto blocks = [&](auto SC, auto DG, auto FL) __attribute__((always_inline)) {
+            block(I0_{}, SC, DG, FL);
+            block(I1_{}, SC, DG, FL);
+            block(I2_{}, SC, DG, FL);
+            block(I3_{}, SC, DG, FL);
+        };
+        auto epilogue = [&](auto FL) __attribute__((always_inline)) {
+            if (dtile) {
+                if (alpha == 1.0f) blocks(F_{}, T_{}, FL);
+                else blocks(T_{}, T_{}, FL);
+            } else {
+                if (alpha == 1.0f) blocks(F_{}, F_{}, FL);
+                else blocks(T_{}, F_{}, FL);
+            }
+        };
+        // The next tile's first slab was loaded before this tile's stores.  With
+        // FL the epilogue issues 16 unconditional store instructions per lane
+        // after those loads, and vector memory operations complete in order, so
+        // waiting for all but the last 16 leaves the stores in flight; otherwise
+        // wait for everything.
+        epilogue(std::integral_constant<bool, FULL>{});
+        if constexpr (FULL) wait_vm<16>();
+        else __builtin_amdgcn_s_waitcnt(0);
+        if (!next) break;
+        // Everyone's slab landed and every wave is done with its staging.  A
+        // plain barrier: a fence here would also wait for this wave's stores.
+        asm volatile("s_barrier" ::: "memory");
+        v = vn;
+        bz = nbz;
+        m0 = nm0;
+        n0 = nn0;
     }
 }
 
@@ -1107,6 +1244,19 @@ static NSLayout ns_layout(int64_t batch, int64_t rows, int64_t cols) {
     return L;
 }
 
+// Compute units of the stream's device (cached per device).
+static int cu_count(hipStream_t s, int *cus) {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    hipError_t e = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) { set_error("gemm: device of the stream: %s", hipGetErrorString(e)); return (int)e; }
+    if (dev >= 0 && dev < 64 && (*cus = cache[dev].load(std::memory_order_relaxed)) > 0) return MSR_OK;
+    e = hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess || *cus <= 0) { set_error("gemm: compute unit count: %s", hipGetErrorString(e)); return e ? (int)e : MSR_ERR_ARG; }
+    if (dev >= 0 && dev < 64) cache[dev].store(*cus, std::memory_order_relaxed);
+    return MSR_OK;
+}
+
 static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
     GemmArgs a = a0;
     // an operand read from upper-stored symmetric tiles is square
@@ -1140,16 +1290,36 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
     }
     const int64_t tiles = a.symmetric ? (int64_t)a.tiles_m * (a.tiles_m + 1) / 2 : (int64_t)a.tiles_m * a.tiles_n;
     a.tiles = (int)tiles;
-    auto launch = [&](const GemmArgs &ab, dim3 grid) {
+    // At most one work-group per CU (the LDS of one fills a CU), persistent
+    // over the tiles when each takes at most PERSIST_MAX of them; the grid is a
+    // multiple of 8 when smaller than the launch.  (Over longer runs of tiles the
+    // work-groups drift apart and the tiles in flight stop sharing operand rows
+    // in L2: one tile per work-group measured faster on the 4096 x 14336
+    // products, 56 tiles per CU.)
+    int cus = 0;
+    {
+        const int rc = cu_count(s, &cus);
+        if (rc) return rc;
+    }
+    const int64_t gmax = std::max<int64_t>(NXCD, cus / NXCD * NXCD);
+    auto launch = [&](const GemmArgs &ab, int64_t total) {
         const dim3 block(GEMM_THREADS);
+        const dim3 grid((unsigned)(total <= PERSIST_MAX * gmax ? std::min<int64_t>(total, gmax) : total));
         const bool c = ab.C != nullptr, d = ab.D != nullptr, dt = ab.DT != nullptr;
         const int gm = ab.gm;
+        // every tile in range with 16-byte output rows: unconditional stores
+        const bool full = ab.Mv == ab.M && ab.Nv == ab.N && (d ? ab.d_vec : ab.dt_vec) != 0;
         if (ab.sracc > 0) {   // weight gradient accumulated into D with SR
             if (gm != GM_KK || ab.symmetric || c || !d || dt) { set_error("gemm: unsupported SR-accumulating product"); return (int)MSR_ERR_ARG; }
-            MSR_DISPATCH_NOISE(ab.sracc - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_KK, M>), grid, block, 0, s, ab));
+            MSR_DISPATCH_NOISE(ab.sracc - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_KK, M, EPI_NONE, -1, true>), grid, block, 0, s, ab));
         } else if (ab.symmetric) {   // A = X X^T (RR), B' = c A A + b A + a I (TRI_PQ)
-            if (gm == GM_RR && !c && d && !dt && ab.resid) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false, GM_RR, -1, EPI_A>), grid, block, 0, s, ab);
-            else if (gm == GM_TRI_PQ && c && d && !dt && ab.resid && ab.rvec) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false, GM_TRI_PQ, -1, EPI_B>), grid, block, 0, s, ab);
+            if (gm == GM_RR && !c && d && !dt && ab.resid) {
+                if (full) hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false, GM_RR, -1, EPI_A, -1, true>), grid, block, 0, s, ab);
+                else hipLaunchKernelGGL((gemm_nt_kernel<true, false, true, false, GM_RR, -1, EPI_A>), grid, block, 0, s, ab);
+            } else if (gm == GM_TRI_PQ && c && d && !dt && ab.resid && ab.rvec) {
+                if (full) hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false, GM_TRI_PQ, -1, EPI_B, -1, true>), grid, block, 0, s, ab);
+                else hipLaunchKernelGGL((gemm_nt_kernel<true, true, true, false, GM_TRI_PQ, -1, EPI_B>), grid, block, 0, s, ab);
+            }
             else { set_error("gemm: unsupported symmetric product"); return (int)MSR_ERR_ARG; }
         } else if (gm == GM_TRI_P) {   // X' = B' X + r X: D = X', or DT = X'^T for the tall output
             if (!ab.rvec) { set_error("gemm: X' = B' X needs the diagonal residuals"); return (int)MSR_ERR_ARG; }
@@ -1157,15 +1327,22 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
                 if (c || d == dt) { set_error("gemm: unsupported apply epilogue"); return (int)MSR_ERR_ARG; }
                 if (d) { MSR_DISPATCH_NOISE(ab.apply1 - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P, -1, EPI_X, M>), grid, block, 0, s, ab)); }
                 else { MSR_DISPATCH_NOISE(ab.apply1 - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, false, true, GM_TRI_P, -1, EPI_X, M>), grid, block, 0, s, ab)); }
-            } else if (!c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P, -1, EPI_X>), grid, block, 0, s, ab);
-            else if (!c && !d && dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, false, true, GM_TRI_P, -1, EPI_X>), grid, block, 0, s, ab);
+            } else if (!c && d && !dt) {
+                if (full) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P, -1, EPI_X, -1, true>), grid, block, 0, s, ab);
+                else hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P, -1, EPI_X>), grid, block, 0, s, ab);
+            } else if (!c && !d && dt) {
+                if (full) hipLaunchKernelGGL((gemm_nt_kernel<false, false, false, true, GM_TRI_P, -1, EPI_X, -1, true>), grid, block, 0, s, ab);
+                else hipLaunchKernelGGL((gemm_nt_kernel<false, false, false, true, GM_TRI_P, -1, EPI_X>), grid, block, 0, s, ab);
+            }
             else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
         } else if (gm == GM_RK) {   // msr_gemm_nn
             if (c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false, GM_RK>), grid, block, 0, s, ab);
+            else if (!c && d && !dt && full) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_RK, -1, EPI_NONE, -1, true>), grid, block, 0, s, ab);
             else if (!c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_RK>), grid, block, 0, s, ab);
             else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
         } else if (gm == GM_RR) {   // msr_gemm_nt
             if (c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, true, true, false, GM_RR>), grid, block, 0, s, ab);
+            else if (!c && d && !dt && full) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_RR, -1, EPI_NONE, -1, true>), grid, block, 0, s, ab);
             else if (!c && d && !dt) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_RR>), grid, block, 0, s, ab);
             else { set_error("gemm: unsupported epilogue combination"); return (int)MSR_ERR_ARG; }
         } else {
@@ -1193,24 +1370,28 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
         }
         return ab;
     };
-    // whole matrices per XCD for the largest multiple of 8 matrices (1-D grids
-    // of at most 2^31 - 1 work-groups), the remainder per matrix (2-D grids)
-    const int64_t per_launch8 = ((int64_t(1) << 31) - 1) / (tiles * NXCD) * NXCD;
+    // whole matrices per XCD for the largest multiple of 8 matrices, the
+    // remainder spread per matrix; launches of fewer than 2^30 tiles
+    const int64_t per_launch = (int64_t(1) << 30) / tiles;
+    if (per_launch < 1) { set_error("gemm: a matrix of 2^30 tiles or more"); return MSR_ERR_ARG; }
     int64_t b0 = 0;
-    while (tiles <= PER_XCD_TILES && per_launch8 > 0 && batch - b0 >= NXCD) {
-        const int64_t nb = std::min((batch - b0) / NXCD * NXCD, per_launch8);
+    while (tiles <= PER_XCD_TILES && per_launch >= NXCD && batch - b0 >= NXCD) {
+        const int64_t nb = std::min((batch - b0) / NXCD * NXCD, per_launch / NXCD * NXCD);
         GemmArgs ab = offset(b0);
         ab.per_xcd = 1;
-        const int rc = launch(ab, dim3((unsigned)(tiles * nb)));
+        ab.total = (int)(tiles * nb);
+        const int rc = launch(ab, ab.total);
         if (rc) return rc;
         b0 += nb;
     }
-    for (; b0 < batch; b0 += 65535) {
-        const int64_t nb = (batch - b0) < 65535 ? (batch - b0) : 65535;
+    while (b0 < batch) {
+        const int64_t nb = std::min(batch - b0, per_launch);
         GemmArgs ab = offset(b0);
         ab.per_xcd = 0;
-        const int rc = launch(ab, dim3((unsigned)tiles, (unsigned)nb));
+        ab.total = (int)(tiles * nb);
+        const int rc = launch(ab, ab.total);
         if (rc) return rc;
+        b0 += nb;
     }
     return MSR_OK;
 }

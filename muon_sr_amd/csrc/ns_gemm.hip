@@ -766,44 +766,50 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
                     }
                 }
             }
-            // Transposed copy: T[n][m] = tile[m][n].  Lane l takes column wn0 + l
-            // (a conflict-free LDS row read per element) and stores 8
-            // consecutive m (16 bytes) of its row n per chunk c.
+            // Transposed copy: T[n][m] = tile[m][n].  The block's 32 rows are 32
+            // consecutive m of every output row n: lane l takes output rows
+            // n = wn0 + l / 4 + 16 i (i = 0..3) and, in each, the 8 consecutive m
+            // (16 bytes) from bm0 + 8 (l % 4), so four lanes write 64 contiguous
+            // bytes of one output row (LDS: one 2-byte read per element, at most
+            // two lanes per bank).
+            const int tq = e_lane & 3, tn = e_lane >> 2;
             if constexpr (OUT_DT && APPLY >= 0) {
                 uint16_t *Pp = a.ap.p[bz];
                 Noise ns;
                 ns.key = seed_key(a.ap.seed[bz], 0);
                 ns.inject = a.ap.inject ? a.ap.inject + bz * a.ap.numel : nullptr;
-                const int n = wn0 + e_lane;
+                const int m = bm0 + 8 * tq;
                 const bool vec = fl || a.dt_vec != 0;
                 u32x4_t pw[4];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int m = bm0 + 8 * c;
+                for (int i = 0; i < 4; ++i) {
+                    const int n = wn0 + tn + 16 * i;
                     const bool in = fl || (n < a.Nv && m < a.Mv);
-                    pw[c] = in ? apply_load(Pp, (int64_t)n * a.lddt + m, fl ? 8 : min(8, a.Mv - m), vec)
+                    pw[i] = in ? apply_load(Pp, (int64_t)n * a.lddt + m, fl ? 8 : min(8, a.Mv - m), vec)
                                : u32x4_t{0u, 0u, 0u, 0u};
                 }
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
+                for (int i = 0; i < 4; ++i) {
+                    const int nl = tn + 16 * i;
                     uint32_t u[4];
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        u[j] = (uint32_t)est(8 * c + 2 * j)[e_lane] | ((uint32_t)est(8 * c + 2 * j + 1)[e_lane] << 16);
-                    const int m = bm0 + 8 * c;
+                        u[j] = (uint32_t)est(8 * tq + 2 * j)[nl] | ((uint32_t)est(8 * tq + 2 * j + 1)[nl] << 16);
+                    const int n = wn0 + nl;
                     if (!fl && (n >= a.Nv || m >= a.Mv)) continue;
-                    apply_chunk<APPLY>(a.ap, Pp, ns, (int64_t)n * a.lddt + m, fl ? 8 : min(8, a.Mv - m), vec, u, pw[c]);
+                    apply_chunk<APPLY>(a.ap, Pp, ns, (int64_t)n * a.lddt + m, fl ? 8 : min(8, a.Mv - m), vec, u, pw[i]);
                 }
             } else if constexpr (OUT_DT) {
                 uint16_t *Tb = a.DT + bz * a.sDT;
-                const int n = wn0 + e_lane;                // tile column = output row
+                const int m = bm0 + 8 * tq;
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {             // 8-row chunk of the block = 8 output columns
+                for (int i = 0; i < 4; ++i) {
+                    const int nl = tn + 16 * i;           // tile column = output row
                     uint32_t u[4];
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        u[j] = (uint32_t)est(8 * c + 2 * j)[e_lane] | ((uint32_t)est(8 * c + 2 * j + 1)[e_lane] << 16);
-                    const int m = bm0 + 8 * c;
+                        u[j] = (uint32_t)est(8 * tq + 2 * j)[nl] | ((uint32_t)est(8 * tq + 2 * j + 1)[nl] << 16);
+                    const int n = wn0 + nl;
                     uint16_t *tp = Tb + (int64_t)n * a.lddt + m;
                     if (fl) {
                         *reinterpret_cast<uint4 *>(tp) = make_uint4(u[0], u[1], u[2], u[3]);

@@ -13,9 +13,8 @@ One Muon step of a chunk of 2-D matrices of one shape is one library call
             sum of squares (grads read through a pointer table: no stack copy,
             no update stack);
   NS+apply  batched Newton-Schulz on bf16 MFMA whose last product applies
-            p <- SR(p*(1-lr*wd) - lr*scale*update) to every wide matrix of the
-            chunk (the NS output is never written; tall matrices get it and one
-            apply launch).
+            p <- SR(p*(1-lr*wd) - lr*scale*update) to every matrix of the chunk
+            (the NS output is never written).
 Tensors of more than 2 dims and ns_steps = 0 run prepare, NS and apply as
 separate calls (msr_muon_prepare, msr_newton_schulz / msr_muon_ns_apply,
 msr_muon_apply); the results are the same bit for bit.
@@ -132,14 +131,12 @@ def _run_apply(params, upd_stack, lr, weight_decay, scale, seeds):
 def _ns_apply(upd_stack, params, lr, weight_decay, scale, seeds, ns_steps):
     """Newton-Schulz of `upd_stack` [k, *param shape] and the Muon update of the k
     parameters: the reference's _newton_schulz + _run_apply per parameter
-    (muon_sr/triton_muon_sr.py:105-120, 160-169).  For wide matrices (rows <= cols)
-    this is one library call (msr_muon_ns_apply) whose last product applies the update
-    (no NS output is written).  Tall matrices, whose last product stores transposed
-    (the fused apply measured 6-10 % slower there), parameters of more than 2 dims (NS
-    over their leading dims as a batch, one apply over the whole tensor) and
-    ns_steps = 0 (NS is then only the bf16 normalisation) run the two calls
-    separately; the results are the same bit for bit."""
-    if ns_steps < 1 or upd_stack.dim() != 3 or upd_stack.shape[1] > upd_stack.shape[2]:
+    (muon_sr/triton_muon_sr.py:105-120, 160-169).  For matrices this is one library
+    call (msr_muon_ns_apply) whose last product applies the update (no NS output is
+    written).  Parameters of more than 2 dims (NS over their leading dims as a batch,
+    one apply over the whole tensor) and ns_steps = 0 (NS is then only the bf16
+    normalisation) run the two calls separately; the results are the same bit for bit."""
+    if ns_steps < 1 or upd_stack.dim() != 3:
         _run_apply(params, newton_schulz(upd_stack, steps=ns_steps), lr, weight_decay, scale, seeds)
         return
     L = _lib.lib()
@@ -161,10 +158,9 @@ def _fused_step(grads, buf, first, params, beta, nesterov, prepare_seed, ns_step
     (msr_muon_fused_step): the momentum step of rows first.. of the momentum stack whose
     row `first` starts at `buf` (seed `prepare_seed` over the stack's element offsets,
     muon_sr/triton_muon_sr.py:18-50, 150-159) makes the update inside the Newton-Schulz
-    prologue, and the last product applies it to wide matrices' parameters
-    (muon_sr/triton_muon_sr.py:53-80, 160-169).  Tall matrices get the NS output and
-    one apply launch (their last product stores transposed, where the fused apply
-    measured slower).  Equal, bit for bit, to prepare, NS and apply run separately."""
+    prologue, and the last product applies it to the parameters
+    (muon_sr/triton_muon_sr.py:53-80, 160-169).  Equal, bit for bit, to prepare, NS
+    and apply run separately."""
     L = _lib.lib()
     k = len(grads)
     rows, cols = params[0].shape
@@ -174,17 +170,12 @@ def _fused_step(grads, buf, first, params, beta, nesterov, prepare_seed, ns_step
     a, b, c = NS_COEFFS
     gtab = _lib.ptr_array([g.data_ptr() for g in grads])
     f32 = int(grads[0].dtype == torch.float32)
-    wide = rows <= cols
-    out = None if wide else torch.empty(k, rows, cols, dtype=torch.bfloat16, device=buf.device)
-    ptab = _lib.ptr_array([p.data_ptr() for p in params]) if wide else None
-    stab = _lib.ptr_array(apply_seeds, _lib.ctypes.c_uint32) if wide else None
+    ptab = _lib.ptr_array([p.data_ptr() for p in params])
+    stab = _lib.ptr_array(apply_seeds, _lib.ctypes.c_uint32)
     rc = L.msr_muon_fused_step(gtab, f32, buf.data_ptr(), first, k, rows, cols, beta, int(bool(nesterov)),
-                               prepare_seed, ns_steps, a, b, c, None if wide else out.data_ptr(), ptab, stab, lr,
-                               weight_decay, scale, _lib.noise_mode(), None, None, ws.data_ptr(), nbytes.value,
-                               _lib.stream_of(buf))
+                               prepare_seed, ns_steps, a, b, c, None, ptab, stab, lr, weight_decay, scale,
+                               _lib.noise_mode(), None, None, ws.data_ptr(), nbytes.value, _lib.stream_of(buf))
     _lib.check(rc, "msr_muon_fused_step")
-    if not wide:
-        _run_apply(params, out, lr, weight_decay, scale, apply_seeds)
 
 
 def _check_param(p, name):

@@ -617,6 +617,41 @@ def test_gemm_nn_vs_torch_fp32(L, M, N, K, batch, alpha, beta, pad):
     assert bool((err <= tol).all()), float((err - tol).max())
 
 
+@pytest.mark.parametrize("M,N,K,batch,with_c", [
+    (512, 1024, 256, 48, False),    # 8 tiles per matrix, 384 tiles: work-groups take 1-2 tiles each
+    (512, 1024, 256, 48, True),     # the same with C (stores bounded per element)
+    (2048, 2304, 128, 8, False),    # 72 tiles per matrix (tile ranges spread over the XCDs), 576 tiles
+    (2048, 2048, 128, 136, False),  # 8704 tiles: more than 32 per CU, one tile per work-group
+])
+def test_gemm_tiles_per_work_group(L, M, N, K, batch, with_c):
+    """Launches whose work-groups walk several tiles (one work-group per CU, the next
+    tile's first slab loaded during the epilogue), and one long enough to run a tile
+    per work-group: every product equals the same product launched alone, bit for bit,
+    and torch's fp32 product within bf16 rounding."""
+    torch.manual_seed(M + N + K + batch)
+    P = torch.randn(batch, M, K, device=DEV).to(torch.bfloat16)
+    Q = torch.randn(batch, N, K, device=DEV).to(torch.bfloat16)
+    C = torch.randn(batch, M, N, device=DEV).to(torch.bfloat16) if with_c else None
+    beta = -1.25 if with_c else 0.0
+    D = torch.empty(batch, M, N, device=DEV, dtype=torch.bfloat16)
+
+    def gemm(b0, nb, out):
+        cp = C[b0].data_ptr() if with_c else None
+        check(L, L.msr_gemm_nt(P[b0].data_ptr(), K, M * K, Q[b0].data_ptr(), K, N * K, cp, N, M * N, out.data_ptr(),
+                               N, M * N, M, N, K, nb, 1.0, beta, 0.0, stream()), "gemm")
+    gemm(0, batch, D)
+    one = torch.empty(1, M, N, device=DEV, dtype=torch.bfloat16)
+    for b in sorted({0, 1, batch // 2, batch - 1}):
+        gemm(b, 1, one)
+        assert torch.equal(one[0].view(torch.int16), D[b].view(torch.int16)), b
+        ref = torch.matmul(P[b].float(), Q[b].float().t().contiguous())
+        if with_c:
+            ref = ref + beta * C[b].float()
+        err = (D[b].float() - ref).abs()
+        tol = 2.0 ** -8 * ref.abs() + 1e-5 * ref.abs().max()
+        assert bool((err <= tol).all()), (b, float((err - tol).max()))
+
+
 def test_gemm_nn_equals_nt_on_transposed_operand(L):
     """The NN product with Q equals the NT product with Q^T bit for bit: same fp32
     accumulation order and the same MFMA operand layout, only the LDS path differs."""

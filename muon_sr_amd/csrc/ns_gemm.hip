@@ -405,8 +405,10 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     // Persistent work-groups: work-group g computes the tiles of virtual
     // work-groups g, g + G, g + 2 G, ... (G = gridDim.x, a multiple of 8 when
     // the grid is smaller than the launch, so each runs on the XCD that the
-    // tile order assumes).  The first slab of a work-group's next tile streams
-    // into stage 0 while the epilogue of its current tile runs.
+    // tile order assumes; launches of more than PERSIST_MAX tiles per CU get a
+    // work-group per tile, which leaves the loop after its first).  The first
+    // slab of a work-group's next tile streams into stage 0 while the epilogue
+    // of its current tile runs.
     int v = blockIdx.x;
     int64_t bz;
     int m0, n0;

@@ -293,6 +293,8 @@ enum : int { EPI_NONE = 0, EPI_A = 1, EPI_B = 2, EPI_X = 3 };
 template <bool SYM, bool HAS_C, bool OUT_D, bool OUT_DT, int GM, int SRACC = -1, int EPI = EPI_NONE, int APPLY = -1,
           bool FULL = false>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
+    using T_ = std::true_type;
+    using F_ = std::false_type;
     constexpr bool HAS_KK = GM == GM_TRI_P || GM == GM_TRI_PQ || GM == GM_KK;
     constexpr bool HAS_RK = GM == GM_RK || GM == GM_TRI_P || GM == GM_TRI_PQ;
     constexpr bool HAS_RR = GM == GM_RR || GM == GM_TRI_PQ;
@@ -328,6 +330,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     struct TileOps {
         const uint16_t *P, *Q;
         uint32_t pr, qr, pk, qk;
+        bool qp;   // a diagonal tile of a symmetric product: its Q slabs are its P slabs
     };
     auto tile_ops = [&](int64_t tbz, int tm0, int tn0) {
         TileOps o;
@@ -337,12 +340,14 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         o.qr = (uint32_t)(((int64_t)(tn0 + wave * 8 + lrow) * a.ldq + lchunk * 8) * 2);
         o.pk = (uint32_t)(((int64_t)kr * a.ldp + tm0 + 8 * kc) * 2);
         o.qk = (uint32_t)(((int64_t)kr * a.ldq + tn0 + 8 * kc) * 2);
+        o.qp = SYM && tm0 == tn0;
         return o;
     };
     // Load j (0..7) of the slab at k0 of tile o into `stage`: P block j/2 for
     // even j, Q block j/2 for odd j, each in the layout of the slab's K range
-    // (pk, qk: wave-uniform).
-    auto dma = [&](const TileOps &o, bool pk, bool qk, int stage, int k0) {
+    // (pk, qk: wave-uniform).  QP: a diagonal tile of a symmetric product (P = Q,
+    // m0 = n0, the same K ranges) loads P only and reads its Q fragments there.
+    auto dma = [&](const TileOps &o, bool pk, bool qk, int stage, int k0, auto QP) {
         const __amdgpu_buffer_rsrc_t rP = __builtin_amdgcn_make_buffer_rsrc((void *)o.P, (short)0, 0x7fffffff, 0x00020000);
         const __amdgpu_buffer_rsrc_t rQ = __builtin_amdgcn_make_buffer_rsrc((void *)o.Q, (short)0, 0x7fffffff, 0x00020000);
         const uint32_t vp = pk ? o.pk : o.pr, vq = qk ? o.qk : o.qr;
@@ -352,11 +357,16 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         for (int j = 0; j < 8; ++j) {
             const int i = j >> 1;
             const int dst = (8 * i + wave) * 1024;
-            if (j & 1)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_void_t *)(lds_q(stage) + dst), 16, vq, i * iq + kq, 0, 0);
-            else
+            if (j & 1) {
+                if constexpr (!decltype(QP)::value)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_void_t *)(lds_q(stage) + dst), 16, vq, i * iq + kq, 0, 0);
+            } else
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rP, (lds_void_t *)(lds_p(stage) + dst), 16, vp, i * ip + kp, 0, 0);
         }
+    };
+    auto dma_first = [&](const TileOps &o, int tm0, int tn0) {   // a tile's first slab, into stage 0
+        if (o.qp) dma(o, 0 < kp_of(tm0), 0 < kq_of(tn0), 0, 0, T_{});
+        else dma(o, 0 < kp_of(tm0), 0 < kq_of(tn0), 0, 0, F_{});
     };
     // Row-major fragment reads: chunk (2 ks + khalf) ^ ((row >> 1) & 7) of row;
     // bits 1-3 of row come from r32 only, so one byte offset per (operand, ks)
@@ -389,7 +399,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(p + 2048));
         return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     };
-    auto frags = [&](auto PK, auto QK, int stage, int ks, bf16x8_t (&pa)[4], bf16x8_t (&qb)[2]) {
+    auto frags = [&](auto PK, auto QK, auto QP, int stage, int ks, bf16x8_t (&pa)[4], bf16x8_t (&qb)[2]) {
+        const char *qs = decltype(QP)::value ? lds_p(stage) : lds_q(stage);   // Q from the P slabs (dma)
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
             if constexpr (decltype(PK)::value) pa[mi] = trfrag(lds_p(stage) + offPK[mi] + ks * 8192);
@@ -397,8 +408,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         }
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) {
-            if constexpr (decltype(QK)::value) qb[ni] = trfrag(lds_q(stage) + offQK[ni] + ks * 8192);
-            else qb[ni] = *reinterpret_cast<const bf16x8_t *>(lds_q(stage) + offQ[ks] + ni * 4096);
+            if constexpr (decltype(QK)::value) qb[ni] = trfrag(qs + offQK[ni] + ks * 8192);
+            else qb[ni] = *reinterpret_cast<const bf16x8_t *>(qs + offQ[ks] + ni * 4096);
         }
     };
 
@@ -413,7 +424,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     int64_t bz;
     int m0, n0;
     locate_tile(a, v, bz, m0, n0);
-    dma(tile_ops(bz, m0, n0), 0 < kp_of(m0), 0 < kq_of(n0), 0, 0);
+    dma_first(tile_ops(bz, m0, n0), m0, n0);
     // EPI_X: the fp32 residuals r of the tile's rows 128 wm + 32 mi + r32, loaded
     // a tile ahead (with the tile's first slab) so that no load waits at its start
     float rf0 = 0.0f, rf1 = 0.0f, rf2 = 0.0f, rf3 = 0.0f;
@@ -517,35 +528,32 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         using K1_ = std::integral_constant<int, 1>;
         using K2_ = std::integral_constant<int, 2>;
         using K3_ = std::integral_constant<int, 3>;
-        auto slab = [&](auto PK, auto QK, int stage, int knext, bool pkn, bool qkn, auto DG, bool dg, bool load) {
-            if (load) dma(ot, pkn, qkn, stage ^ 1, knext);   // wave-uniform: no load after the last slab of K
+        auto slab = [&](auto PK, auto QK, auto QP, int stage, int knext, bool pkn, bool qkn, auto DG, bool dg, bool load) {
+            if (load) dma(ot, pkn, qkn, stage ^ 1, knext, QP);   // wave-uniform: no load after the last slab of K
             __builtin_amdgcn_sched_barrier(0);
-            frags(PK, QK, stage, 1, fa[1], fb[1]);
+            frags(PK, QK, QP, stage, 1, fa[1], fb[1]);
             mm(0);
             diag(DG, dg, 0, stage, K0_{});
             pattern(PK, QK);
             __builtin_amdgcn_sched_barrier(0);
-            frags(PK, QK, stage, 2, fa[0], fb[0]);
+            frags(PK, QK, QP, stage, 2, fa[0], fb[0]);
             mm(1);
             diag(DG, dg, 1, stage, K1_{});
             pattern(PK, QK);
             __builtin_amdgcn_sched_barrier(0);
-            frags(PK, QK, stage, 3, fa[1], fb[1]);
+            frags(PK, QK, QP, stage, 3, fa[1], fb[1]);
             mm(0);
             diag(DG, dg, 0, stage, K2_{});
             pattern(PK, QK);
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_waitcnt(0);   // own loads of the next slab landed, own reads of this stage done
             __syncthreads();                 // everyone's
-            frags(PK, QK, stage ^ 1, 0, fa[0], fb[0]);
+            frags(PK, QK, QP, stage ^ 1, 0, fa[0], fb[0]);
             mm(1);
             diag(DG, dg, 1, stage, K3_{});
             pattern(PK, QK);
             __builtin_amdgcn_sched_barrier(0);
         };
-        using T_ = std::true_type;
-        using F_ = std::false_type;
-
         // The K ranges [0, kP) (KK), [kP, kQ) (RK) and [kQ, K) (RR) run as
         // separate loops with uniform bodies, one after the other.  Each range
         // starts in stage 0 with its first slab landed (ranges are multiples of 4
@@ -557,31 +565,39 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         const int KT = a.K / BK, ktP = kP / BK, ktQ = kQ / BK;
         // DG: the range is the diagonal block [m0, m0 + 256) of X' = B' X + r X (EPI_X), whose
         // slab pair (kt - kt0) / 2 holds the rows of waves with wm = (kt - kt0) / 2.
-        auto range = [&](auto PK, auto QK, int kt0, int kt1, auto DG) {
+        auto range = [&](auto PK, auto QK, auto QP, int kt0, int kt1, auto DG) {
             const bool end = kt1 >= KT;
             const int kafter = end ? (kt1 - 1) * BK : kt1 * BK;
             const bool pka = end ? decltype(PK)::value : kt1 < ktP, qka = end ? decltype(QK)::value : kt1 < ktQ;
-            frags(PK, QK, 0, 0, fa[0], fb[0]);
+            frags(PK, QK, QP, 0, 0, fa[0], fb[0]);
 #pragma clang loop unroll(disable)
             for (int kt = kt0; kt < kt1; kt += 2) {
                 const bool more = kt + 2 < kt1;
                 const bool dg = decltype(DG)::value && ((kt - kt0) >> 1) == wm;
-                slab(PK, QK, 0, (kt + 1) * BK, PK, QK, DG, dg, true);
-                slab(PK, QK, 1, more ? (kt + 2) * BK : kafter, more ? decltype(PK)::value : pka,
+                slab(PK, QK, QP, 0, (kt + 1) * BK, PK, QK, DG, dg, true);
+                slab(PK, QK, QP, 1, more ? (kt + 2) * BK : kafter, more ? decltype(PK)::value : pka,
                      more ? decltype(QK)::value : qka, DG, dg, more || !end);
             }
         };
-        if constexpr (HAS_KK) {
-            if (0 < ktP) range(T_{}, T_{}, 0, ktP, F_{});
-        }
-        if constexpr (EPI == EPI_X) {   // GM_TRI_P: the RK range starts at k = m0 (ktP + 4 <= ktQ)
-            range(F_{}, T_{}, ktP, ktP + 4, T_{});
-            if (ktP + 4 < ktQ) range(F_{}, T_{}, ktP + 4, ktQ, F_{});
-        } else if constexpr (HAS_RK) {
-            if (ktP < ktQ) range(F_{}, T_{}, ktP, ktQ, F_{});
-        }
-        if constexpr (HAS_RR) {
-            if (ktQ < KT) range(F_{}, F_{}, ktQ, KT, F_{});
+        auto kloop = [&](auto QP) {
+            if constexpr (HAS_KK) {
+                if (0 < ktP) range(T_{}, T_{}, QP, 0, ktP, F_{});
+            }
+            if constexpr (EPI == EPI_X) {   // GM_TRI_P: the RK range starts at k = m0 (ktP + 4 <= ktQ)
+                range(F_{}, T_{}, QP, ktP, ktP + 4, T_{});
+                if (ktP + 4 < ktQ) range(F_{}, T_{}, QP, ktP + 4, ktQ, F_{});
+            } else if constexpr (HAS_RK) {
+                if (ktP < ktQ) range(F_{}, T_{}, QP, ktP, ktQ, F_{});
+            }
+            if constexpr (HAS_RR) {
+                if (ktQ < KT) range(F_{}, F_{}, QP, ktQ, KT, F_{});
+            }
+        };
+        if constexpr (SYM) {   // diagonal tiles read Q from the P slabs (one K loop each)
+            if (ot.qp) kloop(T_{});
+            else kloop(F_{});
+        } else {
+            kloop(F_{});
         }
 
         // ---------------- epilogue ----------------
@@ -625,7 +641,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         int nm0 = m0, nn0 = n0;
         if (next) {
             locate_tile(a, vn, nbz, nm0, nn0);
-            dma(tile_ops(nbz, nm0, nn0), 0 < kp_of(nm0), 0 < kq_of(nn0), 0, 0);
+            dma_first(tile_ops(nbz, nm0, nn0), nm0, nn0);
             load_r(nbz, nm0);
         }
         // Diagonal tiles: the lane's diagonal element of each 32-row block mi (at most

@@ -416,9 +416,9 @@ def bench_muon(shapes, steps_timed, warmup, label):
         opt.step()
     sync()
     # the fused step calls alone (per chunk: the momentum step made in the Newton-Schulz
-    # prologue, the 5 iterations and, for wide matrices, the parameter update done by the
-    # last product's store), bracketed on their stream, beside the whole step (which adds
-    # the apply launches of tall matrices and the host work)
+    # prologue, the 5 iterations and the parameter update done by the last product's
+    # store), bracketed on their stream, beside the whole step (which adds the host work
+    # between the calls)
     with LaunchTimer("msr_muon_fused_step", "msr_muon_ns_apply", "msr_newton_schulz") as lt:
         t0 = time.perf_counter()
         lt.on = True

@@ -801,13 +801,29 @@ def test_newton_schulz_batch_invariant_and_steps0(L):
     assert rel_fro(X0, exp) < 1e-2
 
 
-@pytest.mark.parametrize("batch,rows,cols", [(3, 256, 512), (2, 640, 256), (3, 100, 60), (130, 256, 256), (2, 61, 99)])
+@pytest.mark.parametrize("batch,rows,cols", [(300, 200, 300), (300, 300, 200)])
+def test_newton_schulz_many_tiles_batch_invariant(L, batch, rows, cols):
+    """Hundreds of padded matrices: the products' work-groups each walk several tiles and
+    the last product's stores are bounded (partial tiles), wide and tall (transposed
+    store).  Every matrix equals its own Newton-Schulz, bit for bit."""
+    from muon_sr_amd.muon import newton_schulz
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(batch + rows)
+    G = (torch.randn(batch, rows, cols, device=DEV, generator=gen) * 1e-2).to(torch.bfloat16)
+    full = newton_schulz(G)
+    for i in (0, 1, batch // 2, batch - 1):
+        assert torch.equal(full[i:i + 1], newton_schulz(G[i:i + 1].clone())), i
+
+
+@pytest.mark.parametrize("batch,rows,cols", [(3, 256, 512), (2, 640, 256), (3, 100, 60), (130, 256, 256), (2, 61, 99),
+                                             (150, 300, 700), (150, 700, 300)])
 @pytest.mark.parametrize("mode", [O.NOISE_TRITON, O.NOISE_PHILOX8, O.NOISE_INJECT])
 def test_muon_ns_apply_equals_ns_then_apply(L, batch, rows, cols, mode):
     """msr_muon_ns_apply (the apply done by the last Newton-Schulz product's store) equals
     msr_newton_schulz followed by msr_muon_apply bit for bit: wide, tall and padded shapes,
     columns that are no multiple of 8 (element-wise stores and noise), more than 128
-    matrices (several apply launches) and misaligned parameters."""
+    matrices (several apply launches), launches whose work-groups walk several tiles and
+    misaligned parameters."""
     import ctypes
     from muon_sr_amd.muon import newton_schulz, NS_COEFFS
     a, b, c = NS_COEFFS

@@ -211,14 +211,6 @@ __device__ __forceinline__ void locate_tile(const GemmArgs &a, int v, int64_t &b
     n0 = tj * BN;
 }
 
-// Work-group barrier that orders LDS accesses only: this wave's global stores
-// stay in flight across it.
-__device__ __forceinline__ void lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Wait until at most N vector memory operations of this wave are outstanding
 // (s_waitcnt: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at their maxima).
 // Vector memory operations complete in issue order, so every operation issued
@@ -231,8 +223,8 @@ __device__ __forceinline__ void wait_vm() {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// LDS: four variables of 33 KiB, one per slab: P stage 0, P stage 1, Q stage
-// 0, Q stage 1 (32 KiB used each).  Separate variables tell the compiler that
+// LDS: four variables of 32 KiB, one per slab: P stage 0, P stage 1, Q stage
+// 0, Q stage 1.  Separate variables tell the compiler that
 // the fragment reads of one stage do not alias the direct-to-LDS loads into
 // the other stage (it would otherwise wait for those loads before the reads).
 // After the K loop the stage-1 variables hold the epilogue's staging (stage 0
@@ -240,8 +232,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // 32 rows of its 64-column sub-tile with a row pitch of EPITCH elements (144 B:
 // 16-byte aligned rows; the 8-byte writes of 32 consecutive rows hit each
 // bank at most twice), waves 0-3 in P stage 1 and waves 4-7 in Q stage 1.
-constexpr int SPITCH = 264;
-constexpr int SLAB_BYTES = 64 * SPITCH * 2;
+constexpr int SLAB_BYTES = 256 * BK * 2;   // 256 rows x 64 k, or 64 k x 256 columns, of bf16
 __shared__ __attribute__((aligned(1024))) char lds_p0[SLAB_BYTES];
 __shared__ __attribute__((aligned(1024))) char lds_p1[SLAB_BYTES];
 __shared__ __attribute__((aligned(1024))) char lds_q0[SLAB_BYTES];

@@ -87,6 +87,7 @@ struct GemmArgs {
     int64_t sv;             // batch stride of resid and rvec
     int apply1;             // 0, or 1 + the noise mode of the fused apply store (then D / DT only mark the layout)
     ApplyTab ap;            // apply1 > 0: the parameters the D / DT store updates instead of writing
+    int *tile_ctr;          // dynamic tile order (see the kernel), or null: [0, 8) per XCD, [8] work-groups done
 };
 
 // p[off + j] <- SR(p*(1 - lr*wd) - lr*(f32(u_j)*scale)) for the j < valid bf16 values u
@@ -431,7 +432,19 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
     load_r(bz, m0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    // Dynamic tile order (a.tile_ctr, launches of more tiles than work-groups; the
+    // grid is then a multiple of 8): work-group g on XCD x = g % 8 takes slot g / 8 of
+    // that XCD's tile list (the tiles of virtual work-groups x + 8 slot) first, as in
+    // the static order, and each next slot from the XCD's counter, fetched while its
+    // current tile runs.  The tiles in flight then stay a compact run of each XCD's
+    // list however unevenly the work-groups progress.  The last work-group to finish
+    // resets the counters for the next launch on the stream.
+    const bool dyn = a.tile_ctr != nullptr;
+    const int xcd = (int)(blockIdx.x % NXCD);
+    __shared__ int s_next_slot;
+    int my_slot = 0;
     for (;;) {
+        if (dyn && tid == 0) my_slot = (int)(gridDim.x / NXCD) + atomicAdd(a.tile_ctr + xcd, 1);
         const TileOps ot = tile_ops(bz, m0, n0);
         const int kP = kp_of(m0), kQ = kq_of(n0);
         f32x16_t acc[4][2];
@@ -600,8 +613,9 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         // gathered column-wise.  A symmetric product stores its upper tiles only.
         // Lane l holds D[m = l % 32][n = 8r + 4(l / 32) + q] of each 32x32 MFMA tile.
         __builtin_amdgcn_s_waitcnt(0);
+        if (dyn && tid == 0) s_next_slot = my_slot;
         __syncthreads();   // every wave is done with the operand slabs
-        const int vn = v + (int)gridDim.x;
+        const int vn = dyn ? xcd + NXCD * __builtin_amdgcn_readfirstlane(s_next_slot) : v + (int)gridDim.x;
         const bool next = vn < a.total;
         // The epilogue's lane indices, from an opaque copy of the thread index:
         // its addresses are then formed here instead of being hoisted out of
@@ -869,6 +883,11 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         bz = nbz;
         m0 = nm0;
         n0 = nn0;
+    }
+    // every work-group has fetched its last slot when it gets here
+    if (dyn && tid == 0 && atomicAdd(a.tile_ctr + NXCD, 1) == (int)gridDim.x - 1) {
+#pragma unroll
+        for (int i = 0; i <= NXCD; ++i) a.tile_ctr[i] = 0;
     }
 }
 
@@ -1176,9 +1195,10 @@ __global__ __launch_bounds__(256) void ns_prologue_kernel(PrologueArgs a) {
 // (ns_rescale_kernel scales x0 by 2^-e).  ||u|| >= 2^64 (inf) gives e = 127 and
 // s = 0 (u / inf = 0, as the reference's normalisation); NaN propagates.
 __global__ __launch_bounds__(256) void ns_finalize_kernel(const float *tpart, int64_t ntiles, int64_t batch,
-                                                          float *alphas, int *rexp) {
+                                                          float *alphas, int *rexp, int *tile_ctr) {
     __shared__ float red[256];
     const int64_t b = blockIdx.x;
+    if (b == 0 && threadIdx.x <= NXCD) tile_ctr[threadIdx.x] = 0;   // the GEMMs' tile counters start at zero
     float s = 0.0f;
     for (int64_t t = threadIdx.x; t < ntiles; t += 256) s = s + tpart[b * ntiles + t];
     red[threadIdx.x] = s;
@@ -1229,7 +1249,7 @@ static inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * 
 struct NSLayout {
     int64_t m, n, mp, np;
     bool transposed;
-    size_t off_x[2], off_a, off_b, off_part, off_alpha, off_rho, off_r, off_tpart, off_rexp, total;
+    size_t off_x[2], off_a, off_b, off_part, off_alpha, off_rho, off_r, off_tpart, off_rexp, off_ctr, total;
     int64_t ntiles;   // 64 x 64 tiles of the padded update (prologue sums of squares)
 };
 
@@ -1255,6 +1275,7 @@ static NSLayout ns_layout(int64_t batch, int64_t rows, int64_t cols) {
     L.ntiles = (L.mp / 64) * (L.np / 64);
     L.off_tpart = take((size_t)batch * L.ntiles * 4);   // tile sums of squares of the update
     L.off_rexp = take((size_t)batch * 4);               // prologue scale exponents
+    L.off_ctr = take(16 * 4);                           // the GEMMs' dynamic tile counters
     L.total = o;
     return L;
 }
@@ -1306,20 +1327,30 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
     const int64_t tiles = a.symmetric ? (int64_t)a.tiles_m * (a.tiles_m + 1) / 2 : (int64_t)a.tiles_m * a.tiles_n;
     a.tiles = (int)tiles;
     // At most one work-group per CU (the LDS of one fills a CU), persistent
-    // over the tiles when each takes at most PERSIST_MAX of them; the grid is a
-    // multiple of 8 when smaller than the launch.  (Over longer runs of tiles the
-    // work-groups drift apart and the tiles in flight stop sharing operand rows
-    // in L2: one tile per work-group measured faster on the 4096 x 14336
-    // products, 56 tiles per CU.)
+    // over the tiles.  With tile counters (a.tile_ctr, the Newton-Schulz
+    // products) and more tiles than work-groups, each XCD's work-groups draw
+    // the XCD's tiles in order from its counter, so the tiles in flight stay
+    // neighbours in L2 however long the run.  Without counters the order is
+    // static (tile v + grid): persistent while each work-group takes at most
+    // PERSIST_MAX tiles, one tile per work-group beyond that (over longer
+    // static runs the work-groups drift apart and the tiles in flight stop
+    // sharing operand rows: one tile per work-group measured faster on the
+    // 4096 x 14336 products, 56 tiles per CU).  A grid smaller than the launch
+    // is a multiple of 8.
     int cus = 0;
     {
         const int rc = cu_count(s, &cus);
         if (rc) return rc;
     }
     const int64_t gmax = std::max<int64_t>(NXCD, cus / NXCD * NXCD);
-    auto launch = [&](const GemmArgs &ab, int64_t total) {
+    auto launch = [&](const GemmArgs &ab_in, int64_t total) {
         const dim3 block(GEMM_THREADS);
-        const dim3 grid((unsigned)(total <= PERSIST_MAX * gmax ? std::min<int64_t>(total, gmax) : total));
+        // the dynamic order needs more tiles than work-groups (and then a grid of gmax,
+        // a multiple of 8); otherwise the static one
+        const bool dyn = ab_in.tile_ctr != nullptr && total > gmax;
+        GemmArgs ab = ab_in;
+        if (!dyn) ab.tile_ctr = nullptr;
+        const dim3 grid((unsigned)(dyn ? gmax : total <= PERSIST_MAX * gmax ? std::min<int64_t>(total, gmax) : total));
         const bool c = ab.C != nullptr, d = ab.D != nullptr, dt = ab.DT != nullptr;
         const int gm = ab.gm;
         // every tile in range with 16-byte output rows: unconditional stores
@@ -1535,7 +1566,8 @@ struct NSPrepare {
 // The prologue over `batch` matrices: X0 and the tile sums (see ns_prologue_kernel),
 // the first products' factors, and the rescale of out-of-range matrices.
 static int ns_prologue(const uint16_t *in, const NSPrepare *pp, int64_t batch, int64_t rows, int64_t cols,
-                       uint16_t *X0, float *tpart, float *alphas, int *rexp, const NSLayout &L, hipStream_t s) {
+                       uint16_t *X0, float *tpart, float *alphas, int *rexp, int *tile_ctr, const NSLayout &L,
+                       hipStream_t s) {
     const int64_t numel = rows * cols, xs = L.mp * L.np;
     const int64_t Rp = L.transposed ? L.np : L.mp;
     const int64_t Cp = L.transposed ? L.mp : L.np;
@@ -1579,7 +1611,8 @@ static int ns_prologue(const uint16_t *in, const NSPrepare *pp, int64_t batch, i
         int rc = check_launch("ns_prologue_kernel");
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(ns_finalize_kernel, dim3((unsigned)batch), dim3(256), 0, s, tpart, L.ntiles, batch, alphas, rexp);
+    hipLaunchKernelGGL(ns_finalize_kernel, dim3((unsigned)batch), dim3(256), 0, s, tpart, L.ntiles, batch, alphas, rexp,
+                       tile_ctr);
     int rc = check_launch("ns_finalize_kernel");
     if (rc) return rc;
     const int64_t n8 = xs / 8, bpm = std::min<int64_t>((n8 + 255) / 256, 64);
@@ -1629,8 +1662,9 @@ static int ns_run(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows
         return normalize(dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch), out, cols,
                          numel, rows, cols);
     }
+    int *tile_ctr = (int *)(ws + L.off_ctr);
     if ((rc = ns_prologue(in, pp, batch, rows, cols, X[0], (float *)(ws + L.off_tpart), alphas,
-                          (int *)(ws + L.off_rexp), L, s)))
+                          (int *)(ws + L.off_rexp), tile_ctr, L, s)))
         return rc;
 
     const int mp = (int)L.mp, np = (int)L.np;
@@ -1648,6 +1682,7 @@ static int ns_run(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows
         g.alpha = 1.0f; g.beta = 0.0f; g.symmetric = 1; g.gm = GM_RR;
         g.alpha_b = it == 0 ? alphas : nullptr;   // s0^2 x0 x0^T
         g.resid = rho; g.sv = mp;
+        g.tile_ctr = tile_ctr;
         if ((rc = launch_gemm(g, batch, s))) return rc;
         // B' = c (A A) + b A + a I (diagonal corrected for rho), reading A's lower tiles as the
         // transposed upper ones; upper tiles stored
@@ -1659,6 +1694,7 @@ static int ns_run(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows
         g.M = mp; g.N = mp; g.K = mp; g.Mv = mp; g.Nv = mp;
         g.alpha = c_coef; g.beta = b_coef; g.diag = a_coef; g.symmetric = 1; g.gm = GM_TRI_PQ;
         g.rvec = rho; g.resid = rr; g.sv = mp;
+        g.tile_ctr = tile_ctr;
         if ((rc = launch_gemm(g, batch, s))) return rc;
         // X' = B' X + r X (= B X + a X), X read K-major, B' lower tiles as the transposed upper ones
         g = GemmArgs{};
@@ -1669,6 +1705,7 @@ static int ns_run(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows
         g.alpha = 1.0f; g.beta = 0.0f; g.symmetric = 0; g.gm = GM_TRI_P;
         g.alpha_b = it == 0 ? alphas + batch : nullptr;   // s0 (B' x0 + r x0)
         g.rvec = rr; g.sv = mp;
+        g.tile_ctr = tile_ctr;
         if (!last) {
             g.D = X[cur ^ 1]; g.ldd = np; g.sD = xs;
             g.DT = nullptr;

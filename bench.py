@@ -434,7 +434,57 @@ def bench_muon(shapes, steps_timed, warmup, label):
                executed_tflop=fx / 1e12, executed_tflops=fx / (ms * 1e9))
     del opt, params, grads
     torch.cuda.empty_cache()
+    out.update(bench_ns_alone(shapes))
     return out
+
+
+def bench_ns_alone(shapes, reps=3):
+    """Newton-Schulz alone (msr_newton_schulz, 5 iterations, bf16 in and out) over the same
+    matrices, one call per shape group and chunk as the optimizer makes them: the step's
+    Newton-Schulz without the momentum step and the parameter update.  Inputs resident in
+    HBM; one workspace serves the calls in turn (one stream)."""
+    import ctypes
+    import torch
+    from muon_sr_amd import _lib
+    from muon_sr_amd.muon import NS_BATCH_NUMEL, NS_COEFFS
+    L = _lib.lib()
+    dev = "cuda:0"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(6)
+    counts = {}
+    for s in shapes:
+        counts[s] = counts.get(s, 0) + 1
+    calls, ws_bytes = [], 0
+    for (r, c), k in counts.items():
+        chunk = max(1, NS_BATCH_NUMEL // (r * c))
+        for b0 in range(0, k, chunk):
+            b = min(chunk, k - b0)
+            x = (torch.randn(b, r, c, device=dev, generator=gen) * 1e-3).to(torch.bfloat16)
+            nb = ctypes.c_size_t(0)
+            _lib.check(L.msr_ns_workspace_bytes(b, r, c, ctypes.byref(nb)), "msr_ns_workspace_bytes")
+            ws_bytes = max(ws_bytes, nb.value)
+            calls.append((x, torch.empty_like(x), b, r, c))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    a, b_, c_ = NS_COEFFS
+
+    def one_pass():
+        for x, y, b, r, c in calls:
+            _lib.check(L.msr_newton_schulz(x.data_ptr(), y.data_ptr(), b, r, c, 5, a, b_, c_, ws.data_ptr(), ws_bytes,
+                                           stream), "msr_newton_schulz")
+    one_pass()
+    sync()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        one_pass()
+    e1.record()
+    sync()
+    ms = e0.elapsed_time(e1) / reps
+    fl, n_calls = ns_flops(shapes), len(calls)
+    del calls, ws
+    torch.cuda.empty_cache()
+    return dict(ns_alone_ms=ms, ns_alone_tflops=fl / (ms * 1e9), ns_alone_calls=n_calls)
 
 
 def bench_gemm_nt(reps=10):
@@ -518,8 +568,10 @@ def bench_full(steps_timed, warmup):
     fl, fx = ns_flops([tuple(p.shape) for p in muon]), ns_exec_flops([tuple(p.shape) for p in muon])
     out = dict(muon_matrices=len(muon), adamw_tensors=len(adam), ns_tflop=fl / 1e12, ms_per_step=ms,
                ns_tflops_effective=fl / (ms * 1e9), executed_tflop=fx / 1e12, executed_tflops_effective=fx / (ms * 1e9))
+    shapes = [tuple(p.shape) for p in muon]
     del opt, muon, adam
     torch.cuda.empty_cache()
+    out.update(bench_ns_alone(shapes))
     return out
 
 
@@ -785,6 +837,9 @@ def main():
         # what the matrix cores execute: the symmetric products skip their lower 256-tiles
         line["ns_executed_frac_of_bf16_peak"] = round(configs["muon_ns_16L_d2048"]["executed_tflops"] / BF16_PEAK_TFLOPS,
                                                    4)
+        # Newton-Schulz alone on the same matrices (no momentum step, no parameter update)
+        line["ns_alone_frac_of_bf16_peak"] = round(configs["muon_ns_16L_d2048"]["ns_alone_tflops"] / BF16_PEAK_TFLOPS,
+                                                4)
     if "hybrid_llama3_8b" in configs:
         line["full_step_ms"] = configs["hybrid_llama3_8b"]["ms_per_step"]
     print(json.dumps(line), flush=True)

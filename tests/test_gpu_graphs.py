@@ -82,12 +82,13 @@ def test_adamw8bit_step_in_hip_graph(L, mode):
     _replay_vs_eager(call, [p, s1, s2, a1, a2])
 
 
-@pytest.mark.parametrize("rows,cols", [(512, 768), (768, 512)])
-def test_muon_fused_step_in_hip_graph(L, rows, cols):
+@pytest.mark.parametrize("k,rows,cols", [(3, 512, 768), (3, 768, 512), (8, 2048, 5632)])
+def test_muon_fused_step_in_hip_graph(L, k, rows, cols):
     """Momentum step, Newton-Schulz and the parameter update (msr_muon_fused_step) of
-    a chunk of 3 matrices, wide and tall."""
+    a chunk of k matrices, wide and tall.  8 x 2048 x 5632 gives the products more
+    tiles than work-groups, so their work-groups draw tiles from the counters in the
+    workspace (whole matrices per XCD for A and B', tiles spread for X')."""
     from muon_sr_amd.muon import NS_COEFFS
-    k = 3
     gen = torch.Generator(device=DEV)
     gen.manual_seed(rows + cols)
     grads = [(torch.randn(rows, cols, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16) for _ in range(k)]
@@ -98,7 +99,7 @@ def test_muon_fused_step_in_hip_graph(L, rows, cols):
     ws = torch.empty(nbytes.value, dtype=torch.uint8, device=DEV)
     a, b, c = NS_COEFFS
     gtab = ptr_array([t.data_ptr() for t in grads])
-    seeds = ptr_array([11, 22, 33], ctypes.c_uint32)
+    seeds = ptr_array([11 * (i + 1) for i in range(k)], ctypes.c_uint32)
     scale = max(1.0, rows / cols) ** 0.5
 
     def call(t, stream):

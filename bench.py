@@ -419,7 +419,7 @@ def bench_muon(shapes, steps_timed, warmup, label):
     # prologue, the 5 iterations and the parameter update done by the last product's
     # store), bracketed on their stream, beside the whole step (which adds the host work
     # between the calls)
-    with LaunchTimer("msr_muon_fused_step", "msr_muon_ns_apply", "msr_newton_schulz") as lt:
+    with LaunchTimer("msr_muon_fused_step", "msr_muon_fused_steps", "msr_muon_ns_apply", "msr_newton_schulz") as lt:
         t0 = time.perf_counter()
         lt.on = True
         for _ in range(steps_timed):

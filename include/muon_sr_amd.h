@@ -261,6 +261,37 @@ int msr_muon_fused_step(const void *const *grads, int32_t grads_f32, uint16_t *b
                         void *workspace, size_t workspace_bytes, msr_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * (b) The whole Muon step of several shape groups in one call: one
+ * msr_muon_fused_step per group, with the groups' matrices sharing each
+ * Newton-Schulz product launch.  Replaces, for shape groups whose shapes are
+ * transposes of each other (a model's tall and wide projections), the
+ * per-group loop of muon_sr/triton_muon_sr.py:128-177 (group order does not
+ * matter: groups touch disjoint memory).  Equal, bit for bit, to
+ * msr_muon_fused_step called once per group with the same arguments (params,
+ * apply_seeds and a group's prepare_seed as there); a shared launch only fills
+ * the GPU's last round of tiles better than separate ones.
+ *   groups: HOST array of n_groups; every group's shape is rows x cols or
+ *           cols x rows of group 0's; pointers as in msr_muon_fused_step
+ *           (grads, params, apply_seeds: HOST arrays of `batch` entries).
+ * noise_mode: MSR_NOISE_TRITON or MSR_NOISE_PHILOX8.  steps >= 1; workspace as
+ * msr_ns_workspace_bytes(sum of the groups' batch, rows, cols) of group 0.
+ * ------------------------------------------------------------------------- */
+typedef struct msr_muon_group {
+    const void *const *grads;      /* bf16, or fp32 with grads_f32 */
+    uint16_t *buf;                 /* momentum of the group's first matrix, [batch][rows][cols] */
+    uint16_t *const *params;
+    const uint32_t *apply_seeds;
+    int64_t first;                 /* index of buf's first matrix in its stack (noise offsets) */
+    int64_t batch, rows, cols;
+    uint32_t prepare_seed;
+    int32_t grads_f32;
+    float scale;                   /* the group's sqrt(max(1, rows/cols)) */
+} msr_muon_group;
+int msr_muon_fused_steps(const msr_muon_group *groups, int32_t n_groups, float beta, int32_t nesterov,
+                         int32_t steps, float a, float b, float c, float lr, float weight_decay,
+                         int32_t noise_mode, void *workspace, size_t workspace_bytes, msr_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Diagnostics (no counterpart in the reference; used by the parity tests).
  * ------------------------------------------------------------------------- */
 

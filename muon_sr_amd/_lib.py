@@ -32,6 +32,14 @@ class AccumItem(ctypes.Structure):
 ACCUM_ZERO_INIT = 1
 ACCUM_GRAD_F32 = 2
 
+
+class MuonGroup(ctypes.Structure):
+    """msr_muon_group (include/muon_sr_amd.h)."""
+    _fields_ = [("grads", ctypes.c_void_p), ("buf", ctypes.c_void_p), ("params", ctypes.c_void_p),
+                ("apply_seeds", ctypes.c_void_p), ("first", ctypes.c_int64), ("batch", ctypes.c_int64),
+                ("rows", ctypes.c_int64), ("cols", ctypes.c_int64), ("prepare_seed", ctypes.c_uint32),
+                ("grads_f32", ctypes.c_int32), ("scale", ctypes.c_float)]
+
 # name -> (restype, argtypes); mirrors include/muon_sr_amd.h
 SIGNATURES = {
     "msr_version": (ctypes.c_int, []),
@@ -52,6 +60,8 @@ SIGNATURES = {
                                          _P, ctypes.c_size_t, _P]),
     "msr_muon_fused_step": (ctypes.c_int, [_P, _I32, _P, _I64, _I64, _I64, _I64, _F, _I32, _U32, _I32, _F, _F, _F,
                                            _P, _P, _P, _F, _F, _F, _I32, _P, _P, _P, ctypes.c_size_t, _P]),
+    "msr_muon_fused_steps": (ctypes.c_int, [ctypes.POINTER(MuonGroup), _I32, _F, _I32, _I32, _F, _F, _F, _F, _F, _I32,
+                                            _P, ctypes.c_size_t, _P]),
     "msr_noise_fill": (ctypes.c_int, [_P, _I64, _I64, _U32, _U32, _I32, _P]),
     "msr_quantize": (ctypes.c_int, [_P, _P, _I64, _P, _I32, _P, _P]),
     "msr_quant_table_bytes": (ctypes.c_size_t, []),

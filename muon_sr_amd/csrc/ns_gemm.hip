@@ -33,6 +33,7 @@
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
+#include <vector>
 
 #include "common.hpp"
 #include "vecio.hpp"
@@ -1563,33 +1564,47 @@ struct NSPrepare {
     int noise_mode;
 };
 
-// The prologue over `batch` matrices: X0 and the tile sums (see ns_prologue_kernel),
-// the first products' factors, and the rescale of out-of-range matrices.
-static int ns_prologue(const uint16_t *in, const NSPrepare *pp, int64_t batch, int64_t rows, int64_t cols,
-                       uint16_t *X0, float *tpart, float *alphas, int *rexp, int *tile_ctr, const NSLayout &L,
-                       hipStream_t s) {
-    const int64_t numel = rows * cols, xs = L.mp * L.np;
-    const int64_t Rp = L.transposed ? L.np : L.mp;
-    const int64_t Cp = L.transposed ? L.mp : L.np;
+// Matrices [b0, b0 + batch) of a Newton-Schulz call, all of one shape group.
+// Every part of a call has the same Newton-Schulz shape (m x n, m <= n); a
+// part of rows > cols (tall) is iterated transposed.  The input is `in` (a
+// [batch][rows][cols] stack), or the update made by the momentum step of `pp`;
+// the last product writes `out` ([batch][rows][cols]), or, with `ap`, updates
+// the parameters (then `out` only marks the layout and is never accessed).
+struct NSPart {
+    int64_t b0, batch, rows, cols;
+    const uint16_t *in;
+    uint16_t *out;
+    const NSApply *ap;
+    const NSPrepare *pp;
+};
+
+// The prologue of one part: its X0 (at X0 + b0 xs) and tile sums (see ns_prologue_kernel).
+static int ns_prologue_part(const NSPart &pt, uint16_t *X0, float *tpart, const NSLayout &L, hipStream_t s) {
+    const int64_t rows = pt.rows, cols = pt.cols, numel = rows * cols, xs = L.mp * L.np;
+    const bool transposed = rows > cols;
+    const int64_t Rp = transposed ? L.np : L.mp;
+    const int64_t Cp = transposed ? L.mp : L.np;
+    const NSPrepare *pp = pt.pp;
     bool vec = (cols % 8) == 0;
     if (pp) {
         vec = vec && aligned(pp->buf, 16);
-        for (int64_t i = 0; i < batch && vec; ++i) vec = aligned(pp->grads[i], 16);
+        for (int64_t i = 0; i < pt.batch && vec; ++i) vec = aligned(pp->grads[i], 16);
     } else {
-        vec = vec && aligned(in, 16);
+        vec = vec && aligned(pt.in, 16);
     }
-    for (int64_t b0 = 0; b0 < batch; b0 += PRO_MAX) {
-        const int64_t nb = std::min<int64_t>(PRO_MAX, batch - b0);
+    for (int64_t b0 = 0; b0 < pt.batch; b0 += PRO_MAX) {
+        const int64_t nb = std::min<int64_t>(PRO_MAX, pt.batch - b0);
+        uint16_t *x0 = X0 + (pt.b0 + b0) * xs;
         PrologueArgs a = {};
         a.rows = rows; a.cols = cols;
-        a.S = L.transposed ? nullptr : X0 + b0 * xs; a.ldS = Cp; a.sS = xs;
-        a.T = L.transposed ? X0 + b0 * xs : nullptr; a.ldT = Rp; a.sT = xs;
+        a.S = transposed ? nullptr : x0; a.ldS = Cp; a.sS = xs;
+        a.T = transposed ? x0 : nullptr; a.ldT = Rp; a.sT = xs;
         a.Rp = Rp; a.Cp = Cp;
-        a.tpart = tpart + b0 * L.ntiles;
+        a.tpart = tpart + (pt.b0 + b0) * L.ntiles;
         a.ntx = Cp / 64; a.ntiles = L.ntiles;
         const dim3 grid((unsigned)(Cp / 64), (unsigned)(Rp / 64), (unsigned)nb);
         if (!pp) {
-            a.in = in + b0 * numel;
+            a.in = pt.in + b0 * numel;
             if (vec) hipLaunchKernelGGL((ns_prologue_kernel<SRC_COPY, NOISE_TRITON, false, false, true>), grid, dim3(256), 0, s, a);
             else hipLaunchKernelGGL((ns_prologue_kernel<SRC_COPY, NOISE_TRITON, false, false, false>), grid, dim3(256), 0, s, a);
         } else {
@@ -1611,6 +1626,14 @@ static int ns_prologue(const uint16_t *in, const NSPrepare *pp, int64_t batch, i
         int rc = check_launch("ns_prologue_kernel");
         if (rc) return rc;
     }
+    return MSR_OK;
+}
+
+// After the parts' prologues, over all `batch` matrices of the call: the first
+// products' factors and the rescale of out-of-range matrices.
+static int ns_prologue_finish(int64_t batch, uint16_t *X0, float *tpart, float *alphas, int *rexp, int *tile_ctr,
+                              const NSLayout &L, hipStream_t s) {
+    const int64_t xs = L.mp * L.np;
     hipLaunchKernelGGL(ns_finalize_kernel, dim3((unsigned)batch), dim3(256), 0, s, tpart, L.ntiles, batch, alphas, rexp,
                        tile_ctr);
     int rc = check_launch("ns_finalize_kernel");
@@ -1620,52 +1643,25 @@ static int ns_prologue(const uint16_t *in, const NSPrepare *pp, int64_t batch, i
     return check_launch("ns_rescale_kernel");
 }
 
-// Newton-Schulz of `batch` matrices; with `ap`, the last product updates the
-// parameters instead of writing `out` (which is then unused); with `pp`, the
-// update is made by the Muon momentum step in the prologue (`in` is unused).
-// Arguments are validated by the callers.
-static int ns_run(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows, int64_t cols, int32_t steps,
-                  float a_coef, float b_coef, float c_coef, void *workspace, const NSLayout &L, hipStream_t s,
-                  const NSApply *ap, const NSPrepare *pp = nullptr) {
+// Newton-Schulz (steps >= 1) of the `batch` matrices of `parts` (which cover
+// [0, batch) in order): one prologue per part, the iterations over the whole
+// batch, and the last product per part.  Arguments are validated by the callers.
+static int ns_run_parts(const NSPart *parts, int n_parts, int64_t batch, int32_t steps, float a_coef, float b_coef,
+                        float c_coef, void *workspace, const NSLayout &L, hipStream_t s) {
     char *ws = static_cast<char *>(workspace);
     uint16_t *X[2] = {(uint16_t *)(ws + L.off_x[0]), (uint16_t *)(ws + L.off_x[1])};
     uint16_t *A = (uint16_t *)(ws + L.off_a);
     uint16_t *B = (uint16_t *)(ws + L.off_b);
-    float *part = (float *)(ws + L.off_part);
     float *alphas = (float *)(ws + L.off_alpha);   // [0, batch): s0^2, [batch, 2 batch): s0
+    float *tpart = (float *)(ws + L.off_tpart);
     float *rho = (float *)(ws + L.off_rho);
     float *rr = (float *)(ws + L.off_r);
-    const int64_t numel = rows * cols;
-    const int64_t xs = L.mp * L.np, as = L.mp * L.mp;
-
-    // 16-byte accesses when every row of the input starts 16-byte aligned
-    const bool vec = (cols % 8) == 0 && aligned(in, 16);
-    int rc = MSR_OK;
-    // steps == 0: the output is the reference's bf16 normalisation of the input
-    auto normalize = [&](dim3 grid, uint16_t *S, int64_t ldS, int64_t sS, int64_t Rp, int64_t Cp) {
-        const bool v = vec && aligned(S, 16) && ldS % 8 == 0 && sS % 8 == 0 && Rp % 8 == 0 && Cp % 8 == 0;
-        if (v)
-            hipLaunchKernelGGL(normalize_vec_kernel, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, nullptr,
-                               0, 0, Rp, Cp);
-        else
-            hipLaunchKernelGGL(normalize_kernel, grid, dim3(256), 0, s, in, rows, cols, part, S, ldS, sS, nullptr, 0,
-                               0, Rp, Cp);
-        return check_launch("normalize_kernel");
-    };
-
-    if (steps == 0) {
-        if (vec)
-            hipLaunchKernelGGL(sumsq_kernel<true>, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
-        else
-            hipLaunchKernelGGL(sumsq_kernel<false>, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
-        if ((rc = check_launch("sumsq_kernel"))) return rc;
-        return normalize(dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch), out, cols,
-                         numel, rows, cols);
-    }
     int *tile_ctr = (int *)(ws + L.off_ctr);
-    if ((rc = ns_prologue(in, pp, batch, rows, cols, X[0], (float *)(ws + L.off_tpart), alphas,
-                          (int *)(ws + L.off_rexp), tile_ctr, L, s)))
-        return rc;
+    const int64_t xs = L.mp * L.np, as = L.mp * L.mp;
+    int rc = MSR_OK;
+    for (int i = 0; i < n_parts; ++i)
+        if ((rc = ns_prologue_part(parts[i], X[0], tpart, L, s))) return rc;
+    if ((rc = ns_prologue_finish(batch, X[0], tpart, alphas, (int *)(ws + L.off_rexp), tile_ctr, L, s))) return rc;
 
     const int mp = (int)L.mp, np = (int)L.np;
     int cur = 0;
@@ -1710,42 +1706,89 @@ static int ns_run(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows
             g.D = X[cur ^ 1]; g.ldd = np; g.sD = xs;
             g.DT = nullptr;
             g.Mv = mp; g.Nv = np;
-        } else if (!L.transposed) {
-            g.D = out; g.ldd = cols; g.sD = numel;  // out[m][n], m = rows, n = cols
-            g.DT = nullptr;
-            g.Mv = (int)L.m; g.Nv = (int)L.n;
-        } else {
-            g.D = nullptr;
-            g.DT = out; g.lddt = cols; g.sDT = numel;  // out[n][m], n = rows, m = cols
-            g.Mv = (int)L.m; g.Nv = (int)L.n;
+            if ((rc = launch_gemm(g, batch, s))) return rc;
+            cur ^= 1;
+            continue;
         }
-        if (last && ap) {
+        for (int i = 0; i < n_parts; ++i) {   // the last product, per part: its output layout and update
+            const NSPart &pt = parts[i];
+            if (pt.batch == 0) continue;
+            const int64_t numel = pt.rows * pt.cols;
+            GemmArgs gp = g;
+            gp.P += pt.b0 * g.sP;
+            gp.Q += pt.b0 * g.sQ;
+            gp.alpha_b = g.alpha_b ? g.alpha_b + pt.b0 : nullptr;
+            gp.rvec += pt.b0 * g.sv;
+            gp.Mv = (int)L.m; gp.Nv = (int)L.n;
+            if (pt.rows <= pt.cols) {
+                gp.D = pt.out; gp.ldd = pt.cols; gp.sD = numel;     // out[m][n], m = rows, n = cols
+                gp.DT = nullptr;
+            } else {
+                gp.D = nullptr;
+                gp.DT = pt.out; gp.lddt = pt.cols; gp.sDT = numel;  // out[n][m], n = rows, m = cols
+            }
+            const NSApply *ap = pt.ap;
+            if (!ap) {
+                if ((rc = launch_gemm(gp, pt.batch, s))) return rc;
+                continue;
+            }
             // the store updates params[b] (the layout of out) in launches of up to APPLY_MAX matrices
-            g.apply1 = 1 + ap->noise_mode;
-            g.ap.numel = numel;
-            g.ap.lr = ap->lr;
-            g.ap.decay = 1.0f - ap->lr * ap->weight_decay;          // :72
-            g.ap.scale = ap->scale;
-            for (int64_t b0 = 0; b0 < batch; b0 += APPLY_MAX) {
-                const int64_t nb = std::min<int64_t>(APPLY_MAX, batch - b0);
-                GemmArgs ga = g;
-                ga.P += b0 * g.sP;
-                ga.Q += b0 * g.sQ;
-                ga.alpha_b = g.alpha_b ? g.alpha_b + b0 : nullptr;
-                ga.rvec += b0 * g.sv;
-                for (int64_t i = 0; i < nb; ++i) {
-                    ga.ap.p[i] = ap->params[b0 + i];
-                    ga.ap.seed[i] = ap->seeds[b0 + i];
+            gp.apply1 = 1 + ap->noise_mode;
+            gp.ap.numel = numel;
+            gp.ap.lr = ap->lr;
+            gp.ap.decay = 1.0f - ap->lr * ap->weight_decay;          // :72
+            gp.ap.scale = ap->scale;
+            for (int64_t b0 = 0; b0 < pt.batch; b0 += APPLY_MAX) {
+                const int64_t nb = std::min<int64_t>(APPLY_MAX, pt.batch - b0);
+                GemmArgs ga = gp;
+                ga.P += b0 * gp.sP;
+                ga.Q += b0 * gp.sQ;
+                ga.alpha_b = gp.alpha_b ? gp.alpha_b + b0 : nullptr;
+                ga.rvec += b0 * gp.sv;
+                for (int64_t j = 0; j < nb; ++j) {
+                    ga.ap.p[j] = ap->params[b0 + j];
+                    ga.ap.seed[j] = ap->seeds[b0 + j];
                 }
                 ga.ap.inject = ap->inject ? ap->inject + b0 * numel : nullptr;
                 if ((rc = launch_gemm(ga, nb, s))) return rc;
             }
-        } else if ((rc = launch_gemm(g, batch, s))) {
-            return rc;
         }
-        cur ^= 1;
     }
     return MSR_OK;
+}
+
+// Newton-Schulz of `batch` matrices of one shape; with `ap`, the last product
+// updates the parameters instead of writing `out` (which is then unused); with
+// `pp`, the update is made by the Muon momentum step in the prologue (`in` is
+// unused).  Arguments are validated by the callers.
+static int ns_run(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows, int64_t cols, int32_t steps,
+                  float a_coef, float b_coef, float c_coef, void *workspace, const NSLayout &L, hipStream_t s,
+                  const NSApply *ap, const NSPrepare *pp = nullptr) {
+    if (steps >= 1) {
+        const NSPart part{0, batch, rows, cols, in, out, ap, pp};
+        return ns_run_parts(&part, 1, batch, steps, a_coef, b_coef, c_coef, workspace, L, s);
+    }
+    // steps == 0: the output is the reference's bf16 normalisation of the input
+    char *ws = static_cast<char *>(workspace);
+    float *part = (float *)(ws + L.off_part);
+    const int64_t numel = rows * cols;
+    // 16-byte accesses when every row of the input starts 16-byte aligned
+    const bool vec = (cols % 8) == 0 && aligned(in, 16);
+    if (vec)
+        hipLaunchKernelGGL(sumsq_kernel<true>, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
+    else
+        hipLaunchKernelGGL(sumsq_kernel<false>, dim3(NPART, (unsigned)batch), dim3(NORM_THREADS), 0, s, in, numel, part);
+    int rc = check_launch("sumsq_kernel");
+    if (rc) return rc;
+    const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch);
+    const bool v = vec && aligned(out, 16) && cols % 8 == 0 && numel % 8 == 0 && rows % 8 == 0;
+    if (v)
+        hipLaunchKernelGGL(normalize_vec_kernel, grid, dim3(256), 0, s, in, rows, cols, part, out, cols, numel, nullptr,
+                           0, 0, rows, cols);
+    else
+        hipLaunchKernelGGL(normalize_kernel, grid, dim3(256), 0, s, in, rows, cols, part, out, cols, numel, nullptr, 0,
+                           0, rows, cols);
+    return check_launch("normalize_kernel");
 }
 
 extern "C" {
@@ -1888,6 +1931,114 @@ int msr_muon_fused_step(const void *const *grads, int32_t grads_f32, uint16_t *b
     // the last product's store writes params[b]: its `out` only marks the output layout (never accessed)
     return ns_run(nullptr, static_cast<uint16_t *>(workspace), batch, rows, cols, steps, a_coef, b_coef, c_coef,
                   workspace, L, (hipStream_t)stream, &ap, &pp);
+}
+
+int msr_muon_fused_steps(const msr_muon_group *groups, int32_t n_groups, float beta, int32_t nesterov, int32_t steps,
+                         float a_coef, float b_coef, float c_coef, float lr, float weight_decay, int32_t noise_mode,
+                         void *workspace, size_t workspace_bytes, msr_stream_t stream) {
+    if (!groups || n_groups < 1 || steps < 1) {
+        set_error("msr_muon_fused_steps: bad arguments (at least one group; steps must be >= 1)");
+        return MSR_ERR_ARG;
+    }
+    if (noise_mode != NOISE_TRITON && noise_mode != NOISE_PHILOX8) {
+        set_error("msr_muon_fused_steps: bad noise_mode %d (injected noise: msr_muon_fused_step)", (int)noise_mode);
+        return MSR_ERR_ARG;
+    }
+    const int64_t m = std::min(groups[0].rows, groups[0].cols), n = std::max(groups[0].rows, groups[0].cols);
+    int64_t total = 0;
+    for (int32_t i = 0; i < n_groups; ++i) {
+        const msr_muon_group &g = groups[i];
+        if (!g.grads || !g.buf || !g.params || !g.apply_seeds || g.first < 0 || g.batch < 0 || g.rows <= 0 ||
+            g.cols <= 0) {
+            set_error("msr_muon_fused_steps: bad arguments in group %d", (int)i);
+            return MSR_ERR_ARG;
+        }
+        if (std::min(g.rows, g.cols) != m || std::max(g.rows, g.cols) != n) {
+            set_error("msr_muon_fused_steps: group %d is %lld x %lld, group 0 %lld x %lld: the groups of a call must "
+                      "have the same shape up to transposition", (int)i, (long long)g.rows, (long long)g.cols,
+                      (long long)groups[0].rows, (long long)groups[0].cols);
+            return MSR_ERR_ARG;
+        }
+        total += g.batch;
+    }
+    if (total == 0) return MSR_OK;
+    const NSLayout L = ns_layout(total, m, n);
+    if (!workspace || workspace_bytes < L.total) {
+        set_error("msr_muon_fused_steps: workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
+                  L.total);
+        return MSR_ERR_WORKSPACE;
+    }
+    if (L.mp > (1 << 30) || L.np > (1 << 30)) { set_error("msr_muon_fused_steps: matrix too large"); return MSR_ERR_ARG; }
+    {
+        // as msr_muon_fused_step, across the groups: the momenta and the parameters are
+        // written while the gradients, the momenta and the workspace are read; none may
+        // share memory with another, except that gradients may repeat
+        const size_t pb = 2 * (size_t)m * (size_t)n;
+        auto touch = [](const void *x, size_t nx, const void *y, size_t ny) {
+            return (uintptr_t)x < (uintptr_t)y + ny && (uintptr_t)y < (uintptr_t)x + nx;
+        };
+        auto gbytes = [&](const msr_muon_group &g) { return (g.grads_f32 ? 4 : 2) * (size_t)m * (size_t)n; };
+        auto bbytes = [&](const msr_muon_group &g) { return pb * (size_t)g.batch; };
+        for (int32_t i = 0; i < n_groups; ++i) {
+            const msr_muon_group &gi = groups[i];
+            bool race = touch(gi.buf, bbytes(gi), workspace, L.total);
+            for (int32_t j = 0; j < i && !race; ++j) race = touch(gi.buf, bbytes(gi), groups[j].buf, bbytes(groups[j]));
+            if (race) {
+                set_error("msr_muon_fused_steps: the momentum of group %d overlaps the workspace or another momentum",
+                          (int)i);
+                return MSR_ERR_OVERLAP;
+            }
+            for (int64_t k = 0; k < gi.batch; ++k) {
+                if (!gi.grads[k] || !gi.params[k]) {
+                    set_error("msr_muon_fused_steps: null pointer in group %d, matrix %lld", (int)i, (long long)k);
+                    return MSR_ERR_ARG;
+                }
+                race = touch(gi.grads[k], gbytes(gi), workspace, L.total);
+                for (int32_t j = 0; j < n_groups && !race; ++j)
+                    race = touch(gi.grads[k], gbytes(gi), groups[j].buf, bbytes(groups[j]));
+                if (race) {
+                    set_error("msr_muon_fused_steps: gradient %lld of group %d overlaps a momentum or the workspace",
+                              (long long)k, (int)i);
+                    return MSR_ERR_OVERLAP;
+                }
+            }
+        }
+        for (int32_t i = 0; i < n_groups; ++i) {
+            for (int64_t k = 0; k < groups[i].batch; ++k) {
+                const void *p = groups[i].params[k];
+                bool race = touch(p, pb, workspace, L.total);
+                for (int32_t j = 0; j < n_groups && !race; ++j) {
+                    const msr_muon_group &gj = groups[j];
+                    race = touch(p, pb, gj.buf, bbytes(gj));
+                    for (int64_t l = 0; l < gj.batch && !race; ++l) race = touch(p, pb, gj.grads[l], gbytes(gj));
+                    for (int64_t l = 0; l < gj.batch && !race && (j < i || (j == i && l < k)); ++l)
+                        race = touch(p, pb, gj.params[l], pb);
+                }
+                if (race) {
+                    set_error("msr_muon_fused_steps: parameter %lld of group %d overlaps another operand", (long long)k,
+                              (int)i);
+                    return MSR_ERR_OVERLAP;
+                }
+            }
+        }
+    }
+    std::vector<NSPrepare> pps((size_t)n_groups);
+    std::vector<NSApply> aps((size_t)n_groups);
+    std::vector<NSPart> parts((size_t)n_groups);
+    int64_t b0 = 0;
+    for (int32_t i = 0; i < n_groups; ++i) {
+        const msr_muon_group &g = groups[i];
+        Noise pns;
+        pns.key = seed_key(g.prepare_seed, 0);
+        pns.inject = nullptr;
+        pps[i] = NSPrepare{g.grads, g.grads_f32 != 0, g.buf, g.first, beta, nesterov != 0, pns, (int)noise_mode};
+        aps[i] = NSApply{g.params, g.apply_seeds, lr, weight_decay, g.scale, (int)noise_mode, nullptr};
+        // the last product's store writes params[b]: `out` only marks the output layout (never accessed)
+        parts[i] = NSPart{b0, g.batch, g.rows, g.cols, nullptr, static_cast<uint16_t *>(workspace), &aps[i], &pps[i]};
+        b0 += g.batch;
+    }
+    return ns_run_parts(parts.data(), (int)n_groups, total, steps, a_coef, b_coef, c_coef, workspace, L,
+                        (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -178,6 +178,62 @@ def _fused_step(grads, buf, first, params, beta, nesterov, prepare_seed, ns_step
     _lib.check(rc, "msr_muon_fused_step")
 
 
+def _fused_steps(groups, beta, nesterov, ns_steps, lr, weight_decay):
+    """The whole Muon step of several shape groups in one library call
+    (msr_muon_fused_steps): each group as _fused_step, with the groups' matrices
+    sharing each Newton-Schulz product launch, so that the last round of tiles of
+    the symmetric products fills the GPU better.  Every group's shape is group 0's
+    or its transpose.  Equal, bit for bit, to one _fused_step per group.
+    groups: (grads, buf, first, params, prepare_seed, scale, apply_seeds) per group."""
+    L = _lib.lib()
+    rows, cols = groups[0][3][0].shape
+    total = sum(len(g[0]) for g in groups)
+    nbytes = _lib.ctypes.c_size_t(0)
+    _lib.check(L.msr_ns_workspace_bytes(total, rows, cols, _lib.ctypes.byref(nbytes)), "msr_ns_workspace_bytes")
+    buf0 = groups[0][1]
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=buf0.device)
+    a, b, c = NS_COEFFS
+    tables = []   # the host pointer tables, alive until the call returns
+    arr = (_lib.MuonGroup * len(groups))()
+    for i, (grads, buf, first, params, prepare_seed, scale, apply_seeds) in enumerate(groups):
+        gtab = _lib.ptr_array([g.data_ptr() for g in grads])
+        ptab = _lib.ptr_array([q.data_ptr() for q in params])
+        stab = _lib.ptr_array(apply_seeds, _lib.ctypes.c_uint32)
+        tables += [gtab, ptab, stab]
+        r, c_ = params[0].shape
+        arr[i] = _lib.MuonGroup(_lib.ctypes.addressof(gtab), buf.data_ptr(), _lib.ctypes.addressof(ptab),
+                                _lib.ctypes.addressof(stab), first, len(grads), r, c_, prepare_seed,
+                                int(grads[0].dtype == torch.float32), scale)
+    rc = L.msr_muon_fused_steps(arr, len(groups), beta, int(bool(nesterov)), ns_steps, a, b, c, lr, weight_decay,
+                                _lib.noise_mode(), ws.data_ptr(), nbytes.value, _lib.stream_of(buf0))
+    _lib.check(rc, "msr_muon_fused_steps")
+
+
+def _transposed_partners(items, ns_steps):
+    """Shape groups stepped together by _fused_steps: {i: j, j: i} for 2-D shapes
+    (r, c) and (c, r), r != c (a model's tall and wide projections), when every
+    parameter of both has a gradient and is a contiguous GPU tensor and both whole
+    groups fit one call (NS_BATCH_NUMEL).  Groups touch disjoint memory and their
+    seeds do not depend on the order of the groups, so stepping a group at its
+    partner's turn changes no result."""
+    if ns_steps < 1:
+        return {}
+    index = {tuple(shape): i for i, (shape, _) in enumerate(items)}
+    pairs = {}
+    for i, (shape, ps) in enumerate(items):
+        if len(shape) != 2 or shape[0] == shape[1] or i in pairs:
+            continue
+        j = index.get((shape[1], shape[0]))
+        if j is None or j in pairs:
+            continue
+        both = list(ps) + list(items[j][1])
+        if len(both) * shape[0] * shape[1] > NS_BATCH_NUMEL:
+            continue
+        if all(q.grad is not None and q.is_cuda and q.is_contiguous() for q in both):
+            pairs[i], pairs[j] = j, i
+    return pairs
+
+
 def _check_param(p, name):
     _lib.require_gpu(p, name, RuntimeError)
     if not p.is_contiguous():
@@ -204,9 +260,25 @@ def _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns
     prepare over the whole momentum stack (seed salt 0, index shape_idx), then
     NS + apply per chunk (seed salt 1, index shape_idx*10000 + i).  A group with
     missing gradients falls back to per-parameter steps with index
-    shape_idx*10000 + i.
+    shape_idx*10000 + i.  Two whole groups of transposed shapes take one call
+    (_fused_steps) with the same seeds and results.
     """
-    for shape_idx, (shape, grp_params) in enumerate(shape_groups.items()):
+    items = list(shape_groups.items())
+    partners = _transposed_partners(items, ns_steps)
+
+    def whole_group(idx):   # the one chunk of a whole group, as the loop below makes it
+        shape, grp = items[idx]
+        ordered = sorted(grp, key=lambda q: buf_indices[id(q)])
+        seeds = [_deterministic_seed(step, idx * 10000 + j, salt=1) for j in range(len(ordered))]
+        return ([_bf16_contig(q.grad) for q in ordered], stacked_bufs[shape][0], 0, [q.data for q in ordered],
+                _deterministic_seed(step, idx, salt=0), _ns_scale(shape), seeds)
+
+    for shape_idx, (shape, grp_params) in enumerate(items):
+        j = partners.get(shape_idx)
+        if j is not None:
+            if j > shape_idx:   # at the first group's turn, both groups (the second's turn is skipped)
+                _fused_steps([whole_group(shape_idx), whole_group(j)], beta, nesterov, ns_steps, lr, weight_decay)
+            continue
         active = [p for p in grp_params if p.grad is not None]
         if not active:
             continue

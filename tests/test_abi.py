@@ -106,3 +106,46 @@ def test_overlapping_operands_are_rejected(lib):
     assert lib.msr_ns_workspace_bytes(2, 256, 256, ctypes.byref(nb)) == 0
     assert lib.msr_newton_schulz(A, B, 2, 256, 256, 5, 3.4445, -4.775, 2.0315, A + 1024, nb.value, None) == OVERLAP
     assert b"overlap" in lib.msr_last_error()
+
+
+def test_fused_steps_validation_without_gpu(lib):
+    """msr_muon_fused_steps rejects, before any HIP call, groups of different
+    Newton-Schulz shapes, injected noise, a short workspace and operands shared
+    across groups (fake device addresses: nothing is dereferenced)."""
+    from muon_sr_amd import _lib
+    keep = []
+
+    def group(base, k, rows, cols, params=None):
+        n = rows * cols
+        grads = (ctypes.c_void_p * k)(*[base + 2 * n * i for i in range(k)])
+        prm = (ctypes.c_void_p * k)(*(params or [base + (1 << 32) + 2 * n * i for i in range(k)]))
+        seeds = (ctypes.c_uint32 * k)(*range(k))
+        keep.extend([grads, prm, seeds])
+        return _lib.MuonGroup(ctypes.addressof(grads), base + (2 << 32), ctypes.addressof(prm), ctypes.addressof(seeds),
+                              0, k, rows, cols, 7, 0, 1.0)
+
+    def call(groups, mode=1, ws_bytes=1 << 40, steps=5):
+        arr = (_lib.MuonGroup * len(groups))(*groups)
+        return lib.msr_muon_fused_steps(arr, len(groups), 0.95, 1, steps, 3.4, -4.7, 2.0, 0.02, 0.01, mode,
+                                        1 << 46, ws_bytes, None)
+
+    g0 = group(1 << 36, 2, 256, 512)
+    g1 = group(1 << 37, 1, 512, 256)
+    assert call([g0, group(1 << 38, 1, 512, 384)]) == 1001
+    assert b"same shape up to transposition" in lib.msr_last_error()
+    assert call([g0, g1], mode=2) == 1001          # injected noise: msr_muon_fused_step only
+    assert call([g0, g1], steps=0) == 1001
+    assert lib.msr_muon_fused_steps(None, 0, 0.95, 1, 5, 3.4, -4.7, 2.0, 0.02, 0.01, 1, 1 << 46, 1 << 40, None) == 1001
+    nb = ctypes.c_size_t(0)
+    assert lib.msr_ns_workspace_bytes(3, 256, 512, ctypes.byref(nb)) == 0
+    assert call([g0, g1], ws_bytes=nb.value - 1) == 1004
+    # a parameter of group 1 that is also one of group 0's
+    g2 = group(1 << 38, 1, 512, 256, params=[(1 << 36) + (1 << 32)])
+    assert call([g0, g2], ws_bytes=nb.value) == 1005
+    assert b"overlaps another operand" in lib.msr_last_error()
+    # a gradient of group 1 inside group 0's momentum
+    g3 = group((1 << 36) + (2 << 32), 1, 512, 256)
+    g3.buf = (1 << 39) + (2 << 32)
+    assert call([g0, g3], ws_bytes=nb.value) == 1005
+    assert b"overlaps a momentum" in lib.msr_last_error()
+

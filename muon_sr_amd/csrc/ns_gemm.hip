@@ -1098,29 +1098,51 @@ __global__ __launch_bounds__(256) void ns_prologue_kernel(PrologueArgs a) {
     const int j = threadIdx.x & 7, i0 = threadIdx.x >> 3;
     const float one_m_beta = 1.0f - a.beta;
     float s = 0.0f;
+    // Both rows' loads are issued before any store: the momentum is updated in place, so
+    // the compiler would not move row 1's loads above row 0's stores by itself.
+    uint32_t ld0[2][4] = {}, ld1[2][4] = {};   // SRC_COPY: u; SRC_PREPARE: bf16 gradient, momentum
+    float g32[2][8];                            // SRC_PREPARE with G32: the gradient
+    int64_t offs[2];
+    int valids[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int64_t r = r0 + i0 + 32 * h, c = c0 + 8 * j;
+        valids[h] = (r < a.rows && c < a.cols) ? (int)min<int64_t>(8, a.cols - c) : 0;
+        offs[h] = r * a.cols + c;
+        if (valids[h] > 0) {
+            if constexpr (SRC == SRC_COPY) {
+                load_bf16x8<VEC>(a.in + b * numel, offs[h], valids[h], ld0[h]);
+            } else {
+                if constexpr (G32)
+                    load_f32x8<VEC>(static_cast<const float *>(a.grad[b]) + offs[h], 0, valids[h], g32[h]);
+                else
+                    load_bf16x8<VEC>(static_cast<const uint16_t *>(a.grad[b]) + offs[h], 0, valids[h], ld0[h]);
+                load_bf16x8<VEC>(a.buf + b * numel + offs[h], 0, valids[h], ld1[h]);
+            }
+        }
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int i = i0 + 32 * h;
         const int64_t r = r0 + i, c = c0 + 8 * j;
         uint32_t w[4] = {0u, 0u, 0u, 0u};   // u as bf16 pairs
-        if (r < a.rows && c < a.cols) {
-            const int64_t off = r * a.cols + c;
-            const int valid = (int)min<int64_t>(8, a.cols - c);
+        if (valids[h] > 0) {
+            const int64_t off = offs[h];
+            const int valid = valids[h];
             if constexpr (SRC == SRC_COPY) {
-                load_bf16x8<VEC>(a.in + b * numel, off, valid, w);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) w[k] = ld0[h][k];
             } else {
                 float gf[8], bf[8];
                 uint32_t wb[4];
                 if constexpr (G32) {
-                    load_f32x8<VEC>(static_cast<const float *>(a.grad[b]) + off, 0, valid, gf);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) gf[k] = g32[h][k];
                 } else {
-                    uint32_t wg[4];
-                    load_bf16x8<VEC>(static_cast<const uint16_t *>(a.grad[b]) + off, 0, valid, wg);
-                    unpack8(wg, gf);
+                    unpack8(ld0[h], gf);
                 }
                 uint16_t *bp = a.buf + b * numel + off;
-                load_bf16x8<VEC>(bp, 0, valid, wb);
-                unpack8(wb, bf);
+                unpack8(ld1[h], bf);
                 const int64_t o0 = a.noise0 + b * numel + off;
                 uint32_t rn[8];
                 if (VEC || MODE != NOISE_PHILOX8) {

@@ -24,6 +24,15 @@ def L():
     return need_gpu()
 
 
+@pytest.fixture
+def noise():
+    """Select the SR noise stream for one test and restore it afterwards."""
+    import muon_sr_amd
+    old = muon_sr_amd.get_sr_noise()
+    yield muon_sr_amd.set_sr_noise
+    muon_sr_amd.set_sr_noise(old)
+
+
 def _bits(t):
     return t.detach().contiguous().view(torch.int16)
 
@@ -116,3 +125,41 @@ def test_fused_steps_equal_one_call_per_group(L, case, mode):
         assert torch.equal(_bits(gr.stack), _bits(st)), (case, i, "momentum")
         assert torch.equal(_bits(gr.params), _bits(pr)), (case, i, "params")
         assert not torch.equal(_bits(gr.params), _bits(gr.params0)), (case, i, "no update")
+
+
+@pytest.mark.parametrize("mode_name", ["triton", "philox8"])
+def test_batch_step_merged_equals_chunked(L, noise, mode_name, monkeypatch):
+    """TritonMuonSR(batch_ns=True) with a pair of transposed shape groups: the step that
+    takes both groups in one call (msr_muon_fused_steps) equals, bit for bit, the step
+    with a chunk limit so small that each group runs alone in chunks of two matrices."""
+    from muon_sr_amd import TritonMuonSR
+    from muon_sr_amd import muon as M
+    noise(mode_name)
+    shapes = [(256, 512), (512, 256), (256, 512), (384, 384), (512, 256), (256, 512)]
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(17)
+    p0 = [(torch.randn(s, device=DEV, generator=gen) * 0.02).to(torch.bfloat16) for s in shapes]
+    grads = [[(torch.randn(s, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16) for s in shapes]
+             for _ in range(2)]
+    calls = []
+    real = M._fused_steps
+    monkeypatch.setattr(M, "_fused_steps", lambda *a, **k: (calls.append(1), real(*a, **k)))
+
+    def run(chunk):
+        monkeypatch.setattr(M, "NS_BATCH_NUMEL", chunk)
+        ps = [torch.nn.Parameter(x.clone()) for x in p0]
+        opt = TritonMuonSR(ps, lr=0.02, weight_decay=0.01, batch_ns=True)
+        for step in range(2):
+            for p, g in zip(ps, grads[step]):
+                p.grad = g
+            opt.step()
+        torch.cuda.synchronize()
+        return [p.detach().clone() for p in ps], [opt.state[p]["momentum_buffer"].clone() for p in ps]
+
+    merged = run(1 << 30)
+    assert len(calls) == 2, "one merged call per step expected"
+    chunked = run(2 * 256 * 512)
+    assert len(calls) == 2, "the small chunk limit must not merge"
+    for i in range(len(shapes)):
+        assert torch.equal(_bits(merged[0][i]), _bits(chunked[0][i])), ("param", i)
+        assert torch.equal(_bits(merged[1][i]), _bits(chunked[1][i])), ("momentum", i)

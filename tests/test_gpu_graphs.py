@@ -109,3 +109,37 @@ def test_muon_fused_step_in_hip_graph(L, k, rows, cols):
                                        seeds, 0.02, 0.01, scale, O.NOISE_PHILOX8, None, None, ws.data_ptr(),
                                        nbytes.value, stream), "fused step")
     _replay_vs_eager(call, [buf, params])
+
+
+def test_muon_fused_steps_in_hip_graph(L):
+    """msr_muon_fused_steps of a wide and a tall shape group (3 x 2048 x 5632 and 5 x 5632 x
+    2048: more tiles than work-groups, so the products draw tiles from the workspace
+    counters) captured and replayed."""
+    from muon_sr_amd import _lib
+    from muon_sr_amd.muon import NS_COEFFS
+    shapes = [(3, 2048, 5632), (5, 5632, 2048)]
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(29)
+    grads = [[(torch.randn(r, c, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16) for _ in range(k)]
+             for k, r, c in shapes]
+    bufs = [(torch.randn(k, r, c, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16) for k, r, c in shapes]
+    params = [(torch.randn(k, r, c, device=DEV, generator=gen) * 0.02).to(torch.bfloat16) for k, r, c in shapes]
+    nbytes = ctypes.c_size_t(0)
+    check(L, L.msr_ns_workspace_bytes(8, 2048, 5632, ctypes.byref(nbytes)), "workspace")
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=DEV)
+    a, b, c = NS_COEFFS
+    gtabs = [ptr_array([g.data_ptr() for g in gs]) for gs in grads]
+    stabs = [ptr_array([7 * (i + 1) + 100 * j for i in range(k)], ctypes.c_uint32) for j, (k, _, _) in enumerate(shapes)]
+
+    def call(t, stream):
+        keep = []
+        arr = (_lib.MuonGroup * 2)()
+        for j, (k, r, cc) in enumerate(shapes):
+            bb, pp = t[j], t[2 + j]
+            ptab = ptr_array([pp[i].data_ptr() for i in range(k)])
+            keep.append(ptab)
+            arr[j] = _lib.MuonGroup(ctypes.addressof(gtabs[j]), bb.data_ptr(), ctypes.addressof(ptab),
+                                    ctypes.addressof(stabs[j]), 0, k, r, cc, 1234 + j, 0, max(1.0, r / cc) ** 0.5)
+        check(L, L.msr_muon_fused_steps(arr, 2, 0.95, 1, 5, a, b, c, 0.02, 0.01, O.NOISE_PHILOX8, ws.data_ptr(),
+                                        nbytes.value, stream), "fused steps")
+    _replay_vs_eager(call, bufs + params)

@@ -131,7 +131,7 @@ def bench_adamw8bit(steps, warmup, n=N8):
         lt.on = False
         sync()
         wall = (time.perf_counter() - t0) * 1e3 / steps
-    kms = lt.median_ms()      # the median launch (timed steps, median)
+    kms = lt.median_ms()      # the median launch of the timed steps
     nbytes = B8_PER_ELEM * n
     st = opt.state[p]
     assert st["optim_bits"] == 8 and st["state1"].dtype == torch.uint8

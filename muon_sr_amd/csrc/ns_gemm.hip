@@ -139,7 +139,7 @@ __device__ __forceinline__ void apply_chunk(const ApplyTab &ap, uint16_t *P, con
 // Work-group -> (matrix, tile).  Consecutive work-group ids are dispatched
 // round-robin over the 8 XCDs (each with its own L2), so tiles that share
 // operand row blocks should run on one XCD at the same time:
-//  * small matrices (at most PER_XCD_TILES tiles) in launches over a multiple
+//  * small matrices (at most PER_XCD_TILES tiles, 192 for X' = B' X) in launches over a multiple
 //    of 8 matrices (1-D grid): whole matrices per XCD.  Work-group L runs on
 //    XCD L % 8 and takes slot L / 8 of that XCD's list, the tiles of matrices
 //    xcd, xcd + 8, xcd + 16, ... in tile order;
@@ -1444,7 +1444,11 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
     const int64_t per_launch = (int64_t(1) << 30) / tiles;
     if (per_launch < 1) { set_error("gemm: a matrix of 2^30 tiles or more"); return MSR_ERR_ARG; }
     int64_t b0 = 0;
-    while (tiles <= PER_XCD_TILES && per_launch >= NXCD && batch - b0 >= NXCD) {
+    // X' = B' X (GM_TRI_P) keeps whole matrices per XCD up to 192 tiles: 1 % faster on
+    // 48 x 2048 x 5632 (176 tiles per matrix), equal elsewhere; the symmetric products
+    // measured slower that way at 136 tiles (4096 x 4096)
+    const int64_t per_xcd_max = a.gm == GM_TRI_P ? 192 : PER_XCD_TILES;
+    while (tiles <= per_xcd_max && per_launch >= NXCD && batch - b0 >= NXCD) {
         const int64_t nb = std::min((batch - b0) / NXCD * NXCD, per_launch / NXCD * NXCD);
         GemmArgs ab = offset(b0);
         ab.per_xcd = 1;

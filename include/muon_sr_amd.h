@@ -206,6 +206,8 @@ int msr_muon_apply(uint16_t *const *params, const uint16_t *upd, int64_t numel_e
  * steps == 0 returns the reference's bf16 normalisation bf16(G / bf16(bf16(
  * ||G||_F) + 1e-7)).
  * Results do not depend on `batch` (each matrix is computed independently).
+ * The workspace holds the iterates and the products' tile counters: calls that
+ * may run at the same time (other streams) need workspaces of their own.
  * ------------------------------------------------------------------------- */
 int msr_ns_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, size_t *bytes);
 int msr_newton_schulz(const uint16_t *in, uint16_t *out, int64_t batch, int64_t rows, int64_t cols,

@@ -212,8 +212,8 @@ def _fused_steps(groups, beta, nesterov, ns_steps, lr, weight_decay):
 def _transposed_partners(items, ns_steps):
     """Shape groups stepped together by _fused_steps: {i: j, j: i} for 2-D shapes
     (r, c) and (c, r), r != c (a model's tall and wide projections), when every
-    parameter of both has a gradient and is a contiguous GPU tensor and both whole
-    groups fit one call (NS_BATCH_NUMEL).  Groups touch disjoint memory and their
+    parameter of both has a gradient and is a contiguous tensor on one GPU and both
+    whole groups fit one call (NS_BATCH_NUMEL).  Groups touch disjoint memory and their
     seeds do not depend on the order of the groups, so stepping a group at its
     partner's turn changes no result."""
     if ns_steps < 1:
@@ -229,7 +229,8 @@ def _transposed_partners(items, ns_steps):
         both = list(ps) + list(items[j][1])
         if len(both) * shape[0] * shape[1] > NS_BATCH_NUMEL:
             continue
-        if all(q.grad is not None and q.is_cuda and q.is_contiguous() for q in both):
+        dev = both[0].device
+        if all(q.grad is not None and q.is_cuda and q.is_contiguous() and q.device == dev for q in both):
             pairs[i], pairs[j] = j, i
     return pairs
 

@@ -39,30 +39,37 @@ EXTRA_FLAGS = {}
 _NOISE = "is not a recognized feature for this target"  # hipcc host pass; harmless
 
 
-def _run(cmd, verbose):
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
+def _finish(cmd, res, verbose):
     err = "\n".join(line for line in res.stderr.splitlines() if _NOISE not in line)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+        raise RuntimeError(f"hipcc failed ({res.returncode}): {' '.join(cmd)}\n{err}")
     if verbose and err.strip():
         print(err)
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source (each with its own flags) and link one shared library.
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    _finish(cmd, subprocess.run(cmd, capture_output=True, text=True), verbose)
 
-    Always recompiles; objects go to muon_sr_amd/_build/.
-    """
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP source (each with its own flags, all at once) and link one
+    shared library.  Always recompiles; objects go to muon_sr_amd/_build/."""
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
-    objs = []
+    objs, jobs = [], []
     for src in sources():
         obj = os.path.join(objdir, os.path.basename(src) + ".o")
         flags = [f for f in HIPCC_FLAGS if f != "-shared"]
-        _run([hipcc(), *flags, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", "-o", obj, src], verbose)
+        cmd = [hipcc(), *flags, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", "-o", obj, src]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        jobs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
         objs.append(obj)
+    for cmd, proc in jobs:
+        out, err = proc.communicate()
+        _finish(cmd, subprocess.CompletedProcess(cmd, proc.returncode, out, err), verbose)
     tmp = LIB + ".tmp"
     _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB)

@@ -153,6 +153,7 @@ uint32_t orc_noise16(const orc_noise_t *ns, int64_t offset)
 void orc_sr_accum(uint16_t *acc, const void *grad, int32_t grad_is_f32, int64_t n,
                   const orc_noise_t *ns)
 {
+#pragma omp parallel for schedule(static)
     for (int64_t o = 0; o < n; ++o) {
         float a = bf16_to_f32(acc[o]);
         float g = grad_is_f32 ? ((const float *)grad)[o] : bf16_to_f32(((const uint16_t *)grad)[o]);
@@ -312,6 +313,7 @@ void orc_muon_prepare(const void *g, int32_t g_is_f32, uint16_t *buf, float *out
                       int64_t n, float beta, int32_t nesterov, const orc_noise_t *ns)
 {
     const float one_m_beta = 1.0f - beta;
+#pragma omp parallel for schedule(static)
     for (int64_t o = 0; o < n; ++o) {
         /* the gradient in its own dtype (:34): bf16, or fp32 on the per-parameter path */
         float gf = g_is_f32 ? ((const float *)g)[o] : bf16_to_f32(((const uint16_t *)g)[o]);
@@ -329,6 +331,7 @@ void orc_muon_apply(uint16_t *p, const uint16_t *upd, int64_t n, float lr, float
                     float scale, const orc_noise_t *ns)
 {
     const float decay = 1.0f - lr * weight_decay;              /* :72 */
+#pragma omp parallel for schedule(static)
     for (int64_t o = 0; o < n; ++o) {
         float pf = bf16_to_f32(p[o]);
         float u = bf16_to_f32(upd[o]) * scale;                  /* :70 */
@@ -341,6 +344,7 @@ void orc_muon_apply(uint16_t *p, const uint16_t *upd, int64_t n, float lr, float
 /* Vectorised helpers for the Python side of the oracle. */
 void orc_noise16_batch(const orc_noise_t *ns, const int64_t *offsets, int64_t n, uint16_t *out)
 {
+#pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) out[i] = (uint16_t)orc_noise16(ns, offsets[i]);
 }
 

@@ -231,7 +231,9 @@ LABELS = {
 }
 
 
-def train(name, base, xs, ys, steps, log_every):
+def train(name, base, xs, ys, steps, log_every, keep=False):
+    """Trains a copy of `base` with variant `name`; with `keep`, the result also holds the
+    trained model and its optimizer (key "trained")."""
     model = copy.deepcopy(base)
     if name == "fp32":
         model = model.float()
@@ -266,11 +268,15 @@ def train(name, base, xs, ys, steps, log_every):
     peak = torch.cuda.max_memory_allocated() / 2 ** 20
     for h in hooks:
         h.remove()
-    del model, opt
-    torch.cuda.empty_cache()
-    return {"variant": name, "label": LABELS[name], "final_loss": losses[-1],
-            "mean_last_50": sum(losses[-50:]) / min(50, len(losses)), "time_s": elapsed, "peak_mb": peak,
-            "losses": losses}
+    out = {"variant": name, "label": LABELS[name], "final_loss": losses[-1],
+           "mean_last_50": sum(losses[-50:]) / min(50, len(losses)), "time_s": elapsed, "peak_mb": peak,
+           "losses": losses}
+    if keep:
+        out["trained"] = (model, opt)
+    else:
+        del model, opt
+        torch.cuda.empty_cache()
+    return out
 
 
 def main():

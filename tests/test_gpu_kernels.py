@@ -944,9 +944,11 @@ def test_muon_fused_step_equals_separate_calls(L, batch, rows, cols, first, f32,
                                        (5632, 2048), (2048, 5632)])
 def test_muon_fused_step_at_config_shapes(L, rows, cols):
     """At the Llama-3-8B (config 5) and config-4 shapes, two matrices of a chunk that starts at
-    row 1 of its momentum stack: msr_muon_fused_step equals msr_muon_prepare + msr_newton_schulz
-    + msr_muon_apply bit for bit (momentum and parameters; tall shapes through the NS output and
-    one apply launch, as the classes run them), in the reference's noise stream."""
+    row 1 of its momentum stack: msr_muon_fused_step with the apply in the last product's store,
+    as the classes run it for wide and tall matrices alike (tall ones store that product
+    transposed), equals msr_muon_prepare + msr_newton_schulz + msr_muon_apply bit for bit
+    (momentum and parameters), in the reference's noise stream.  Tall shapes also take the NS
+    output (`out`) followed by one msr_muon_apply launch, which must give the same bits."""
     import ctypes
     from muon_sr_amd.muon import newton_schulz, NS_COEFFS
     a, b, c = NS_COEFFS
@@ -972,25 +974,34 @@ def test_muon_fused_step_at_config_shapes(L, rows, cols):
     p_ref = params0.clone()
     check(L, L.msr_muon_apply(ptr_array([p_ref[i].data_ptr() for i in range(batch)]), X.data_ptr(), numel, batch, lr,
                               wd, scale, seeds_c, mode, None, stream()), "msr_muon_apply")
-    del work, X
-    # the fused call, as the classes make it
-    wide = rows <= cols
-    stack, prm = stack0.clone(), params0.clone()
+    del work
     nb = ctypes.c_size_t(0)
     check(L, L.msr_ns_workspace_bytes(batch, rows, cols, ctypes.byref(nb)), "ws")
     ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
-    out = None if wide else torch.empty(batch, rows, cols, dtype=torch.bfloat16, device=DEV)
+    gtab = ptr_array([g.data_ptr() for g in grads])
+    # the fused call as the classes make it: the update applied in the last product's store
+    stack, prm = stack0.clone(), params0.clone()
     ptab = ptr_array([prm[i].data_ptr() for i in range(batch)])
-    check(L, L.msr_muon_fused_step(ptr_array([g.data_ptr() for g in grads]), 0, stack[first].data_ptr(), first, batch,
-                                   rows, cols, beta, 1, pseed, 5, a, b, c, None if wide else out.data_ptr(),
-                                   ptab if wide else None, seeds_c if wide else None, lr, wd, scale, mode, None, None,
+    check(L, L.msr_muon_fused_step(gtab, 0, stack[first].data_ptr(), first, batch, rows, cols, beta, 1, pseed, 5,
+                                   a, b, c, None, ptab, seeds_c, lr, wd, scale, mode, None, None,
                                    ws.data_ptr(), nb.value, stream()), "msr_muon_fused_step")
-    if not wide:
-        check(L, L.msr_muon_apply(ptab, out.data_ptr(), numel, batch, lr, wd, scale, seeds_c, mode, None, stream()),
-              "msr_muon_apply")
     torch.cuda.synchronize()
     assert torch.equal(stack.view(torch.int16), stack_ref.view(torch.int16))
     assert torch.equal(prm.view(torch.int16), p_ref.view(torch.int16))
+    if rows > cols:
+        # the same step with the NS output written, then one apply launch
+        stack, prm = stack0.clone(), params0.clone()
+        out = torch.empty(batch, rows, cols, dtype=torch.bfloat16, device=DEV)
+        ptab = ptr_array([prm[i].data_ptr() for i in range(batch)])
+        check(L, L.msr_muon_fused_step(gtab, 0, stack[first].data_ptr(), first, batch, rows, cols, beta, 1, pseed,
+                                       5, a, b, c, out.data_ptr(), None, None, lr, wd, scale, mode, None, None,
+                                       ws.data_ptr(), nb.value, stream()), "msr_muon_fused_step")
+        check(L, L.msr_muon_apply(ptab, out.data_ptr(), numel, batch, lr, wd, scale, seeds_c, mode, None, stream()),
+              "msr_muon_apply")
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), X.view(torch.int16))
+        assert torch.equal(stack.view(torch.int16), stack_ref.view(torch.int16))
+        assert torch.equal(prm.view(torch.int16), p_ref.view(torch.int16))
 
 
 @pytest.mark.parametrize("shape", [(2, 128, 256), (2, 256, 96)])

@@ -142,6 +142,52 @@ def bench_adamw8bit(steps, warmup, n=N8):
     return out
 
 
+def bench_stream8_probe(n=N8, reps=10):
+    """The 8-bit step's memory accesses with the arithmetic taken out (msr_stream_probe8: the
+    same pair walk, loads and stores, one integer operation per word), swept over occupancy
+    (k work-groups of 4 waves per CU, set by each work-group's LDS) and grid (1 or 2 rounds of
+    the resident work-groups).  The best rate is the memory system's ceiling for this access
+    pattern on this GPU, measured in the same run as the step."""
+    import torch
+    from muon_sr_amd import _lib
+    L = _lib.lib()
+    dev = "cuda:0"
+    p = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    g = torch.ones(n, dtype=torch.bfloat16, device=dev)
+    m = torch.zeros(n, dtype=torch.uint8, device=dev)
+    v = torch.zeros(n, dtype=torch.uint8, device=dev)
+    a1 = torch.zeros(n // 256, dtype=torch.float32, device=dev)
+    a2 = torch.zeros(n // 256, dtype=torch.float32, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    lds_per_cu = 160 << 10
+    nbytes = B8_PER_ELEM * n
+    rows = []
+    for k in (2, 3, 4, 6, 8):                       # work-groups (of 4 waves) per CU
+        lds = min(64 << 10, lds_per_cu // k - (1 << 10))
+        for rounds in (1, 2):
+            grid = 256 * k * rounds
+
+            def run():
+                _lib.check(L.msr_stream_probe8(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), a1.data_ptr(),
+                                               a2.data_ptr(), n, grid, lds, s), "msr_stream_probe8")
+            for _ in range(3):
+                run()
+            evs = []
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                run()
+                e1.record()
+                evs.append((e0, e1))
+            sync()
+            ms = statistics.median(x.elapsed_time(y) for x, y in evs)
+            rows.append(dict(waves_per_cu=4 * k, grid=grid, ms=round(ms, 4), gbps=round(nbytes / (ms * 1e6), 1)))
+    best = max(rows, key=lambda r: r["gbps"])
+    del p, g, m, v, a1, a2
+    torch.cuda.empty_cache()
+    return dict(bytes_per_launch=nbytes, best_gbps=best["gbps"], best=best, sweep=rows)
+
+
 def host_cpu():
     try:
         for line in open("/proc/cpuinfo"):
@@ -415,23 +461,29 @@ def bench_muon(shapes, steps_timed, warmup, label):
     for _ in range(warmup):
         opt.step()
     sync()
-    # the fused step calls alone (per chunk: the momentum step made in the Newton-Schulz
-    # prologue, the 5 iterations and the parameter update done by the last product's
-    # store), bracketed on their stream, beside the whole step (which adds the host work
-    # between the calls)
-    with LaunchTimer("msr_muon_fused_step", "msr_muon_fused_steps", "msr_muon_ns_apply", "msr_newton_schulz") as lt:
-        t0 = time.perf_counter()
-        lt.on = True
-        for _ in range(steps_timed):
-            opt.step()
-        lt.on = False
-        sync()
-        ms = (time.perf_counter() - t0) * 1e3 / steps_timed
-    ns_ms = lt.total_ms() / steps_timed
+    # The step's device time beside its wall time: events on the caller's stream right
+    # before and after each step (the calls on the side stream join that stream before
+    # the step returns; with the steps enqueued back to back, the device runs step k + 1
+    # right after step k and the events bracket its own work).  Per chunk the library
+    # call makes the momentum step in the Newton-Schulz prologue, the 5 iterations and
+    # the parameter update in the last product's store.
+    evs = []
+    t0 = time.perf_counter()
+    for _ in range(steps_timed):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        opt.step()
+        e1.record()
+        evs.append((e0, e1))
+    sync()
+    ms = (time.perf_counter() - t0) * 1e3 / steps_timed
+    ns_ms = sum(x.elapsed_time(y) for x, y in evs) / steps_timed
     fl, fx = ns_flops(shapes), ns_exec_flops(shapes)
+    # executed: the flops the MFMAs run over the step's device time; step_executed: the
+    # same flops over the whole step's wall time (host work included)
     out = dict(matrices=len(shapes), ns_tflop=fl / 1e12, ms_per_step=ms, tflops=fl / (ms * 1e9),
-               ns_calls_per_step=len(lt.pairs) // steps_timed, fused_calls_ms=ns_ms, fused_calls_tflops=fl / (ns_ms * 1e9),
-               executed_tflop=fx / 1e12, executed_tflops=fx / (ms * 1e9))
+               fused_calls_ms=ns_ms, fused_calls_tflops=fl / (ns_ms * 1e9), executed_tflop=fx / 1e12,
+               executed_tflops=fx / (ns_ms * 1e9), step_executed_tflops=fx / (ms * 1e9))
     del opt, params, grads
     torch.cuda.empty_cache()
     out.update(bench_ns_alone(shapes))
@@ -566,8 +618,9 @@ def bench_full(steps_timed, warmup):
     sync()
     ms = (time.perf_counter() - t0) * 1e3 / steps_timed
     fl, fx = ns_flops([tuple(p.shape) for p in muon]), ns_exec_flops([tuple(p.shape) for p in muon])
+    # over the whole hybrid step's wall time (the 8-bit AdamW group and host work included)
     out = dict(muon_matrices=len(muon), adamw_tensors=len(adam), ns_tflop=fl / 1e12, ms_per_step=ms,
-               ns_tflops_effective=fl / (ms * 1e9), executed_tflop=fx / 1e12, executed_tflops_effective=fx / (ms * 1e9))
+               ns_tflops_effective=fl / (ms * 1e9), executed_tflop=fx / 1e12, step_executed_tflops=fx / (ms * 1e9))
     shapes = [tuple(p.shape) for p in muon]
     del opt, muon, adam
     torch.cuda.empty_cache()
@@ -726,7 +779,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="adamw8bit,sr_accum,ns,centralize,wgrad,full")
+    ap.add_argument("--configs", default="adamw8bit,probe8,sr_accum,ns,centralize,wgrad,full")
     ap.add_argument("--noise", default="philox8", choices=["philox8", "triton"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -752,6 +805,11 @@ def main():
     copy_gbps = device_copy_gbps()
     log(f"device copy 2 GiB -> 2 GiB: {copy_gbps:.0f} GB/s")
     configs = {"adamw8bit_2^28": {k: round(v, 4) for k, v in r8.items()}}
+    probe = None
+    if "probe8" in todo:
+        probe = bench_stream8_probe()
+        log(f"8-bit access pattern without the arithmetic: best {probe['best']}")
+        configs["stream8_probe_2^28"] = probe
     other = "triton" if args.noise == "philox8" else "philox8"
     if "adamw8bit" in todo:   # the same step with the other noise stream (triton: the reference's bits)
         muon_sr_amd.set_sr_noise(other)
@@ -770,7 +828,7 @@ def main():
         configs[f"sr_accum_24L_d2048_{other}_noise"] = {k: round(v, 4) if isinstance(v, float) else v
                                                         for k, v in r.items()}
     if "ns" in todo:
-        r = bench_muon(config4_shapes(), steps_timed=3, warmup=1, label="config4")
+        r = bench_muon(config4_shapes(), steps_timed=5, warmup=2, label="config4")
         log(f"muon config4: {r}")
         configs["muon_ns_16L_d2048"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
     if "gemm" in todo:
@@ -786,7 +844,7 @@ def main():
         log(f"wgrad: {r}")
         configs["wgrad_sr_accum_llama3_8b_layer"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
     if "full" in todo:
-        r = bench_full(steps_timed=2, warmup=1)
+        r = bench_full(steps_timed=5, warmup=2)
         log(f"full hybrid: {r}")
         configs["hybrid_llama3_8b"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in r.items()}
 
@@ -829,12 +887,17 @@ def main():
         "cpu_baseline": cpu,
         "configs": configs,
     }
+    if probe is not None:
+        # the same accesses without the arithmetic, best over occupancy and grid, this run
+        line["roofline"]["pattern_ceiling_gbps"] = probe["best_gbps"]
+        line["roofline"]["frac_of_pattern_ceiling"] = round(kernel_gbps / probe["best_gbps"], 4)
     if "muon_ns_16L_d2048" in configs:
         line["ns_tflops"] = configs["muon_ns_16L_d2048"]["tflops"]
         line["ns_frac_of_bf16_peak"] = round(configs["muon_ns_16L_d2048"]["tflops"] / BF16_PEAK_TFLOPS, 4)
         line["fused_calls_frac_of_bf16_peak"] = round(configs["muon_ns_16L_d2048"]["fused_calls_tflops"] / BF16_PEAK_TFLOPS,
                                                    4)
-        # what the matrix cores execute: the symmetric products skip their lower 256-tiles
+        # what the matrix cores execute (the symmetric products skip their lower 256-tiles),
+        # over the fused calls' launch time
         line["ns_executed_frac_of_bf16_peak"] = round(configs["muon_ns_16L_d2048"]["executed_tflops"] / BF16_PEAK_TFLOPS,
                                                    4)
         # Newton-Schulz alone on the same matrices (no momentum step, no parameter update)

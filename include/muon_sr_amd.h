@@ -301,6 +301,15 @@ int msr_muon_fused_steps(const msr_muon_group *groups, int32_t n_groups, float b
 int msr_noise_fill(uint16_t *out, int64_t n, int64_t offset0, uint32_t seed, uint32_t k,
                    int32_t noise_mode, msr_stream_t stream);
 
+/* Streaming probe of the fused 8-bit step's memory accesses: the pair walk, loads and
+ * stores of the fast kernel over n elements (n a multiple of 512; p, g 16-byte and the
+ * codes 8-byte aligned; absmax1/2 hold n/256 floats), with the arithmetic replaced by one
+ * integer operation per word (every buffer is overwritten).  `grid` work-groups of 256
+ * threads, each holding `lds_bytes` (<= 64 KiB) of LDS that sets the work-groups per CU.
+ * Measurement aid: no counterpart in the reference. */
+int msr_stream_probe8(uint16_t *p, const uint16_t *g, uint8_t *state1, uint8_t *state2, float *absmax1,
+                      float *absmax2, int64_t n, int32_t grid, int32_t lds_bytes, msr_stream_t stream);
+
 /* out[i] = quantizer code of x[i] against qmap (reference search rule), or
  * through qtable when it is not NULL. */
 int msr_quantize(const float *x, uint8_t *out, int64_t n, const float *qmap, int32_t is_signed,

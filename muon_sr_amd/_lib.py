@@ -63,6 +63,7 @@ SIGNATURES = {
     "msr_muon_fused_steps": (ctypes.c_int, [ctypes.POINTER(MuonGroup), _I32, _F, _I32, _I32, _F, _F, _F, _F, _F, _I32,
                                             _P, ctypes.c_size_t, _P]),
     "msr_noise_fill": (ctypes.c_int, [_P, _I64, _I64, _U32, _U32, _I32, _P]),
+    "msr_stream_probe8": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P]),
     "msr_quantize": (ctypes.c_int, [_P, _P, _I64, _P, _I32, _P, _P]),
     "msr_quant_table_bytes": (ctypes.c_size_t, []),
     "msr_quant_table_build": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t]),

@@ -222,8 +222,12 @@ __global__ __launch_bounds__((BLOCK / 8 > THREADS) ? BLOCK / 8 : THREADS) void a
 #ifndef MSR_F8_WAVES
 #define MSR_F8_WAVES 4
 #endif
-constexpr int F8_THREADS = 64 * MSR_F8_WAVES;   // each wave owns 2 quant blocks (512 elements) per iteration
-constexpr int F8_PAIR = 512;                 // elements per wave-iteration (2 blocks of 256)
+#ifndef MSR_F8_NP
+#define MSR_F8_NP 1
+#endif
+constexpr int F8_THREADS = 64 * MSR_F8_WAVES;
+constexpr int F8_NP = MSR_F8_NP;             // adjacent pairs a wave takes per iteration
+constexpr int F8_PAIR = 512;                 // elements of a pair (2 blocks of 256: 64 lanes x 8)
 constexpr int F8_DEFER = 64;                 // pairs a wave defers to its exact pass before flushing
 
 struct Raw8 {
@@ -335,96 +339,125 @@ __device__ __forceinline__ F8Consts f8_consts(const Adam8Args &a) {
     return k;
 }
 
-// One pair of quantization blocks (the wave's 64 lanes x 8 elements, pair index pr) on the
-// fast branch.  Returns false, having written nothing, when some lane of the pair needs the
-// exact arithmetic (the caller then defers the pair to adam8_pair_exact).
-template <int MODE>
-__device__ __forceinline__ bool adam8_pair_fast(const Adam8Args &a, const F8Consts &k, const Raw8 &raw, int64_t pr,
-                                                uint32_t lane, const float *q1s, const float *q2s,
-                                                const uint32_t *s_flat) {
-    float p[8], g[8], m[8], v[8];
+// NP adjacent pairs of quantization blocks (pair pr0 + q: the wave's 64 lanes x 8 elements)
+// on the fast branch.  Returns the mask of the pairs done; a pair whose bit is clear needs
+// the exact arithmetic in some lane and has written nothing (the caller defers it to
+// adam8_pair_exact).  The pairs' instruction chains are independent, so with NP > 1 the
+// scheduler interleaves them: one wave keeps NP pairs of latency in flight.
+template <int MODE, int NP>
+__device__ __forceinline__ uint32_t adam8_pairs_fast(const Adam8Args &a, const F8Consts &k, const Raw8 (&raw)[NP],
+                                                     int64_t pr0, uint32_t lane, const float *q1s, const float *q2s,
+                                                     const uint32_t *s_flat) {
+    float p[NP][8], m[NP][8], v[NP][8], mx[NP], vx[NP];
+    int32_t neg[NP];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        p[j] = bf16_at(raw.p, j);
-        g[j] = bf16_at(raw.g, j);
-    }
-    // a sum of the 8 gradients is finite iff all of them are (or it overflows: exact)
-    const float gsum = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
-    float mx = 0.0f, vx = 0.0f;
-    uint32_t mnz = 0xffffffffu;   // min of 2 bits(|m|) - 2: (bits of the smallest nonzero |m|) - 1, times 2
+    for (int q = 0; q < NP; ++q) {
+        float g[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float mq = q1s[byte_of(raw.mc, j)] * raw.ms;                    // :65
-        const float vq = q2s[byte_of(raw.vc, j)] * raw.vs;                    // :66
-        m[j] = k.b1 * mq + k.omb1 * g[j];                                     // :71
-        v[j] = k.b2 * vq + (k.omb2 * g[j]) * g[j];                            // :72
-        mx = fmaxf(mx, fabsf(m[j]));
-        vx = fmaxf(vx, v[j]);
-        mnz = min(mnz, (__float_as_uint(m[j]) << 1) - 2u);                    // +-0 gives 0xfffffffe
-    }
-    const float ms = raw.ms, vs = raw.vs;
-    halfwave_max2(mx, vx);                                                    // :80-81
-    const float md = mx > 0.0f ? mx : 1.0f;                                   // :82
-    const float vd = vx > 0.0f ? vx : 1.0f;                                   // :83
-    // Fast-branch conditions as sign bits of differences of non-negative bit patterns:
-    // finite gradients and block scales, vs >= +0 (then m' is finite or +-inf and v' >= 0
-    // finite or +inf, never NaN, so the maxima above are exact), max v' < 2^62, both
-    // divisors in [2^-60, 2) and the update's numerators |step_c * m'| zero or in
-    // [2^-90, 2^60) (the block maximum of |m'| bounds them from above).
-    const int32_t FMAX = 0x7f7fffff, DLO = 0x21800000, DHI = 0x3fffffff, VXHI = 0x5e7fffff;
-    const int32_t NHI = 0x5d7fffff;   // bits(2^60) - 1
-    const int32_t gsb = (int32_t)(__float_as_uint(gsum) & 0x7fffffffu);
-    const int32_t msb = (int32_t)(__float_as_uint(ms) & 0x7fffffffu);
-    const int32_t vsb = (int32_t)__float_as_uint(vs), vxb = (int32_t)__float_as_uint(vx);
-    const int32_t mdb = (int32_t)__float_as_uint(md), vdb = (int32_t)__float_as_uint(vd);
-    const int32_t nxb = (int32_t)__float_as_uint(k.step_abs * mx), mnb = (int32_t)(mnz >> 1);
-    const int32_t neg = (FMAX - gsb) | (FMAX - msb) | vsb | (FMAX - vsb) | (VXHI - vxb) | (mdb - DLO) |
-                        (DHI - mdb) | (vdb - DLO) | (DHI - vdb) | (NHI - nxb) | (mnb - k.tm1);
-    if (__builtin_amdgcn_ballot_w64(neg < 0) != 0) return false;
-    const int64_t o0 = pr * F8_PAIR + lane * 8;
-    const int64_t qb = pr * 2 + (lane >> 5);
-    uint32_t rp[8], w[8];
-    noise8<MODE>(a.ns_p, o0, 8, rp);
+        for (int j = 0; j < 8; ++j) {
+            p[q][j] = bf16_at(raw[q].p, j);
+            g[j] = bf16_at(raw[q].g, j);
+        }
+        // a sum of the 8 gradients is finite iff all of them are (or it overflows: exact)
+        const float gsum = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
+        float mxq = 0.0f, vxq = 0.0f;
+        uint32_t mnz = 0xffffffffu;   // min of 2 bits(|m|) - 2: (bits of the smallest nonzero |m|) - 1, times 2
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float den = __builtin_fmaf(sqrt_rn_x2p32(v[j]), 0x1p-32f, k.eps_c);   // :74 sqrt(v) + eps
-        const float upd = (p[j] - div_upd(k.step_c * m[j], den)) * k.decay;
-        w[j] = __float_as_uint(upd) + rp[j];                                  // :75-78 (SR)
+        for (int j = 0; j < 8; ++j) {
+            const float mq = q1s[byte_of(raw[q].mc, j)] * raw[q].ms;               // :65
+            const float vq = q2s[byte_of(raw[q].vc, j)] * raw[q].vs;               // :66
+            m[q][j] = k.b1 * mq + k.omb1 * g[j];                                   // :71
+            v[q][j] = k.b2 * vq + (k.omb2 * g[j]) * g[j];                          // :72
+            mxq = fmaxf(mxq, fabsf(m[q][j]));
+            vxq = fmaxf(vxq, v[q][j]);
+            mnz = min(mnz, (__float_as_uint(m[q][j]) << 1) - 2u);                  // +-0 gives 0xfffffffe
+        }
+        halfwave_max2(mxq, vxq);                                                   // :80-81
+        mx[q] = mxq;
+        vx[q] = vxq;
+        const float md = mxq > 0.0f ? mxq : 1.0f;                                  // :82
+        const float vd = vxq > 0.0f ? vxq : 1.0f;                                  // :83
+        // Fast-branch conditions as sign bits of differences of non-negative bit patterns:
+        // finite gradients and block scales, vs >= +0 (then m' is finite or +-inf and v' >= 0
+        // finite or +inf, never NaN, so the maxima above are exact), max v' < 2^62, both
+        // divisors in [2^-60, 2) and the update's numerators |step_c * m'| zero or in
+        // [2^-90, 2^60) (the block maximum of |m'| bounds them from above).
+        const int32_t FMAX = 0x7f7fffff, DLO = 0x21800000, DHI = 0x3fffffff, VXHI = 0x5e7fffff;
+        const int32_t NHI = 0x5d7fffff;   // bits(2^60) - 1
+        const int32_t gsb = (int32_t)(__float_as_uint(gsum) & 0x7fffffffu);
+        const int32_t msb = (int32_t)(__float_as_uint(raw[q].ms) & 0x7fffffffu);
+        const int32_t vsb = (int32_t)__float_as_uint(raw[q].vs), vxb = (int32_t)__float_as_uint(vxq);
+        const int32_t mdb = (int32_t)__float_as_uint(md), vdb = (int32_t)__float_as_uint(vd);
+        const int32_t nxb = (int32_t)__float_as_uint(k.step_abs * mxq), mnb = (int32_t)(mnz >> 1);
+        neg[q] = (FMAX - gsb) | (FMAX - msb) | vsb | (FMAX - vsb) | (VXHI - vxb) | (mdb - DLO) |
+                 (DHI - mdb) | (vdb - DLO) | (DHI - vdb) | (NHI - nxb) | (mnb - k.tm1);
     }
-    st_nt4(a.p + o0, u32x4_t{__builtin_amdgcn_perm(w[1], w[0], 0x07060302u), __builtin_amdgcn_perm(w[3], w[2], 0x07060302u),
-                             __builtin_amdgcn_perm(w[5], w[4], 0x07060302u), __builtin_amdgcn_perm(w[7], w[6], 0x07060302u)});
-    const float ym = rcp_rn(md), yv = rcp_rn(vd);
-    uint32_t rm[8], rv[8];
+    uint32_t ok = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        rm[j] = qf_signed(div_rn(m[j], md, ym), s_flat, k.lo1, k.scap);            // :82,84
-        rv[j] = qf_unsigned(div_rn(v[j], vd, yv), s_flat + QF_SIGNED, k.lo1);     // :83,85
+    for (int q = 0; q < NP; ++q)
+        if (__builtin_amdgcn_ballot_w64(neg[q] < 0) == 0) ok |= 1u << q;
+    // the update, its SR store and the requantization of pair q
+    auto finish = [&](int q) {
+        const int64_t o0 = (pr0 + q) * F8_PAIR + lane * 8;
+        uint32_t rp[8], w[8];
+        noise8<MODE>(a.ns_p, o0, 8, rp);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float den = __builtin_fmaf(sqrt_rn_x2p32(v[q][j]), 0x1p-32f, k.eps_c);   // :74 sqrt(v) + eps
+            const float upd = (p[q][j] - div_upd(k.step_c * m[q][j], den)) * k.decay;
+            w[j] = __float_as_uint(upd) + rp[j];                                           // :75-78 (SR)
+        }
+        stu_nt4(a.p + (pr0 + q) * F8_PAIR, lane * 16u,
+                u32x4_t{__builtin_amdgcn_perm(w[1], w[0], 0x07060302u), __builtin_amdgcn_perm(w[3], w[2], 0x07060302u),
+                        __builtin_amdgcn_perm(w[5], w[4], 0x07060302u), __builtin_amdgcn_perm(w[7], w[6], 0x07060302u)});
+        const float md = mx[q] > 0.0f ? mx[q] : 1.0f, vd = vx[q] > 0.0f ? vx[q] : 1.0f;
+        const float ym = rcp_rn(md), yv = rcp_rn(vd);
+        uint32_t rm[8], rv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            rm[j] = qf_signed(div_rn(m[q][j], md, ym), s_flat, k.lo1, k.scap);            // :82,84
+            rv[j] = qf_unsigned(div_rn(v[q][j], vd, yv), s_flat + QF_SIGNED, k.lo1);     // :83,85
+        }
+        stu_nt2(static_cast<uint8_t *>(a.s1) + (pr0 + q) * F8_PAIR, lane * 8u,
+                u32x2_t{pack_codes(rm[0], rm[1], rm[2], rm[3]), pack_codes(rm[4], rm[5], rm[6], rm[7])});
+        stu_nt2(static_cast<uint8_t *>(a.s2) + (pr0 + q) * F8_PAIR, lane * 8u,
+                u32x2_t{pack_codes(rv[0], rv[1], rv[2], rv[3]), pack_codes(rv[4], rv[5], rv[6], rv[7])});
+        if ((lane & 31) == 0) {
+            stu_f32(a.absmax1 + (pr0 + q) * 2, (lane >> 5) * 4u, mx[q]);         // :86
+            stu_f32(a.absmax2 + (pr0 + q) * 2, (lane >> 5) * 4u, vx[q]);         // :87
+        }
+    };
+    constexpr uint32_t ALL = (1u << NP) - 1u;
+    if (ok == ALL) {
+#pragma unroll
+        for (int q = 0; q < NP; ++q) finish(q);
+    } else {
+#pragma unroll
+        for (int q = 0; q < NP; ++q)
+            if ((ok >> q) & 1u) finish(q);
     }
-    st_nt2(static_cast<uint8_t *>(a.s1) + o0, u32x2_t{pack_codes(rm[0], rm[1], rm[2], rm[3]), pack_codes(rm[4], rm[5], rm[6], rm[7])});
-    st_nt2(static_cast<uint8_t *>(a.s2) + o0, u32x2_t{pack_codes(rv[0], rv[1], rv[2], rv[3]), pack_codes(rv[4], rv[5], rv[6], rv[7])});
-    if ((lane & 31) == 0) {
-        a.absmax1[qb] = mx;                                                   // :86
-        a.absmax2[qb] = vx;                                                   // :87
-    }
-    return true;
+    return ok;
 }
 
-// Raw inputs of pair pr, loaded into VGPRs (the deferred exact pairs).
+// Raw inputs of pair pr (wave-uniform), loaded into VGPRs: buffer loads from the pair's
+// base address, so the address arithmetic runs on the scalar unit.
 __device__ __forceinline__ Raw8 fetch_pair(const Adam8Args &a, int64_t pr, uint32_t lane) {
-    const char *pb = reinterpret_cast<const char *>(a.p), *gb = reinterpret_cast<const char *>(a.g);
-    const char *mb = static_cast<const char *>(a.s1), *vb = static_cast<const char *>(a.s2);
     Raw8 r;
-    r.p = ld_nt4(pb + pr * (2 * F8_PAIR) + lane * 16u);
-    r.g = ld_nt4(gb + pr * (2 * F8_PAIR) + lane * 16u);
-    r.mc = ld_nt2(mb + pr * F8_PAIR + lane * 8u);
-    r.vc = ld_nt2(vb + pr * F8_PAIR + lane * 8u);
-    r.ms = a.absmax1[pr * 2 + (lane >> 5)];
-    r.vs = a.absmax2[pr * 2 + (lane >> 5)];
+    r.p = ldu_nt4(a.p + pr * F8_PAIR, lane * 16u);
+    r.g = ldu_nt4(a.g + pr * F8_PAIR, lane * 16u);
+    r.mc = ldu_nt2(static_cast<const uint8_t *>(a.s1) + pr * F8_PAIR, lane * 8u);
+    r.vc = ldu_nt2(static_cast<const uint8_t *>(a.s2) + pr * F8_PAIR, lane * 8u);
+    r.ms = ldu_f32(a.absmax1 + pr * 2, (lane >> 5) * 4u);
+    r.vs = ldu_f32(a.absmax2 + pr * 2, (lane >> 5) * 4u);
     return r;
 }
 
+// Four waves per SIMD (16 per CU) hide the branch's latency chains: at most 128 VGPRs.
+#ifndef MSR_F8_MIN_WAVES
+#define MSR_F8_MIN_WAVES 4
+#endif
 template <int MODE>
-__global__ __launch_bounds__(F8_THREADS) void adamw8bit_fast_kernel(Adam8Args a, int64_t npairs) {
+__global__ __launch_bounds__(F8_THREADS, MSR_F8_MIN_WAVES) void adamw8bit_fast_kernel(Adam8Args a, int64_t npairs) {
     __shared__ float q1s[256], q2s[256];
     __shared__ uint32_t s_flat[QF_TOTAL];
     __shared__ uint32_t s_deferred[F8_THREADS / 64][F8_DEFER];
@@ -436,21 +469,36 @@ __global__ __launch_bounds__(F8_THREADS) void adamw8bit_fast_kernel(Adam8Args a,
     __syncthreads();
     const F8Consts k = f8_consts(a);
     const uint32_t lane = threadIdx.x & 63u;
-    // the pair index is wave-uniform: addresses are a scalar base plus a fixed lane offset
+    // the pair index is wave-uniform: addresses are a scalar base plus a fixed lane offset.
+    // Each wave takes F8_NP adjacent pairs per iteration (npairs is a multiple of F8_NP).
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int64_t wstride = (int64_t)gridDim.x * (F8_THREADS / 64);
-    int64_t pr = (int64_t)blockIdx.x * (F8_THREADS / 64) + wave;
+    const int64_t wstride = (int64_t)gridDim.x * (F8_THREADS / 64) * F8_NP;
+    int64_t pr = ((int64_t)blockIdx.x * (F8_THREADS / 64) + wave) * F8_NP;
     uint32_t *deferred = s_deferred[wave];
     for (;;) {
         int ndef = 0;
-        Raw8 nxt;
-        if (pr < npairs) nxt = fetch_pair(a, pr, lane);
+        Raw8 nxt[F8_NP];
+        if (pr < npairs) {
+#pragma unroll
+            for (int q = 0; q < F8_NP; ++q) nxt[q] = fetch_pair(a, pr + q, lane);
+        }
         for (; pr < npairs; pr += wstride) {
-            const Raw8 raw = nxt;
-            if (pr + wstride < npairs) nxt = fetch_pair(a, pr + wstride, lane);
-            if (adam8_pair_fast<MODE>(a, k, raw, pr, lane, q1s, q2s, s_flat)) continue;
-            if (lane == 0) deferred[ndef] = (uint32_t)pr;
-            if (++ndef == F8_DEFER) {
+            Raw8 raw[F8_NP];
+#pragma unroll
+            for (int q = 0; q < F8_NP; ++q) raw[q] = nxt[q];
+            if (pr + wstride < npairs) {
+#pragma unroll
+                for (int q = 0; q < F8_NP; ++q) nxt[q] = fetch_pair(a, pr + wstride + q, lane);
+            }
+            const uint32_t ok = adam8_pairs_fast<MODE, F8_NP>(a, k, raw, pr, lane, q1s, q2s, s_flat);
+            if (ok == (1u << F8_NP) - 1u) continue;
+#pragma unroll
+            for (int q = 0; q < F8_NP; ++q) {
+                if ((ok >> q) & 1u) continue;
+                if (lane == 0) deferred[ndef] = (uint32_t)(pr + q);
+                ++ndef;
+            }
+            if (ndef > F8_DEFER - F8_NP) {
                 pr += wstride;
                 break;
             }
@@ -461,6 +509,36 @@ __global__ __launch_bounds__(F8_THREADS) void adamw8bit_fast_kernel(Adam8Args a,
             adam8_pair_exact<MODE>(a, fetch_pair(a, pe, lane), pe * F8_PAIR + lane * 8, pe * 2 + (lane >> 5), q1s, q2s);
         }
         if (pr >= npairs) break;
+    }
+}
+
+// Streaming probe of the fast kernel's memory accesses (a measurement aid, no counterpart
+// in the reference): the same pair walk, loads and stores as adamw8bit_fast_kernel (read p,
+// g 16 B and the m, v codes 8 B per lane, and the two block scales; write p, m, v and the
+// scales), with one integer operation per word in place of the arithmetic.  Its rate is what
+// the memory system delivers for this pattern at a given grid and occupancy (set by the
+// dynamic LDS of each work-group); the step cannot stream faster.
+__global__ __launch_bounds__(F8_THREADS) void stream8_probe_kernel(Adam8Args a, int64_t npairs) {
+    extern __shared__ uint32_t occupancy_pad[];
+    const uint32_t lane = threadIdx.x & 63u;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t wstride = (int64_t)gridDim.x * (F8_THREADS / 64);
+    int64_t pr = (int64_t)blockIdx.x * (F8_THREADS / 64) + wave;
+    if (pr >= npairs) return;
+    Raw8 nxt = fetch_pair(a, pr, lane);
+    for (; pr < npairs; pr += wstride) {
+        const Raw8 raw = nxt;
+        if (pr + wstride < npairs) nxt = fetch_pair(a, pr + wstride, lane);
+        const int64_t o0 = pr * F8_PAIR + lane * 8;
+        const u32x4_t pw = raw.p ^ raw.g;
+        st_nt4(a.p + o0, pw);
+        st_nt2(static_cast<uint8_t *>(a.s1) + o0, u32x2_t{raw.mc.x ^ 0x01010101u, raw.mc.y ^ 0x01010101u});
+        st_nt2(static_cast<uint8_t *>(a.s2) + o0, u32x2_t{raw.vc.x + 0x01010101u, raw.vc.y + 0x01010101u});
+        if ((lane & 31) == 0) {
+            const int64_t qb = pr * 2 + (lane >> 5);
+            a.absmax1[qb] = raw.ms + 1.0f;
+            a.absmax2[qb] = raw.vs * 0.5f;
+        }
     }
 }
 
@@ -674,13 +752,13 @@ static void launch_quant(int mode, bool vec, const Adam8Args &a, hipStream_t s, 
 
 // Fast kernel over the first 2 * npairs blocks (block 256); returns blocks done.
 static int64_t launch_fast8(int mode, const Adam8Args &a, hipStream_t s, int64_t nfull) {
-    const int64_t npairs = nfull / 2;
+    const int64_t npairs = nfull / (2 * F8_NP) * F8_NP;   // whole groups of F8_NP pairs; the rest goes to the general kernel
     if (npairs == 0 || npairs >= ((int64_t)1 << 31)) return 0;   // deferred pairs are recorded as int32
     // the update's divisor sqrt(v') + eps_c must lie in [2^-60, 2^32) (sqrt(v') < 2^31 is
     // checked per pair), and step_c must be finite: the same fp32 arithmetic as adam8_consts
     const float sqrt_bc2 = sqrtf(a.bc2), eps_c = sqrt_bc2 * a.eps, step_c = (a.lr * sqrt_bc2) / a.bc1;
     if (!(eps_c >= 0x1p-60f && eps_c <= 0x1p30f) || !std::isfinite(step_c)) return 0;
-    const unsigned grid = grid_for(npairs, F8_THREADS / 64, MSR_F8_GRID_CAP);
+    const unsigned grid = grid_for(npairs / F8_NP, F8_THREADS / 64, MSR_F8_GRID_CAP);
     if (mode == NOISE_TRITON) hipLaunchKernelGGL((adamw8bit_fast_kernel<NOISE_TRITON>), dim3(grid), dim3(F8_THREADS), 0, s, a, npairs);
     else if (mode == NOISE_PHILOX8) hipLaunchKernelGGL((adamw8bit_fast_kernel<NOISE_PHILOX8>), dim3(grid), dim3(F8_THREADS), 0, s, a, npairs);
     else hipLaunchKernelGGL((adamw8bit_fast_kernel<NOISE_INJECT>), dim3(grid), dim3(F8_THREADS), 0, s, a, npairs);
@@ -746,6 +824,27 @@ int msr_adamw8bit_step(uint16_t *p, const uint16_t *g, void *state1, void *state
         else { MSR_DISPATCH_NOISE(noise_mode, M, hipLaunchKernelGGL((adamw8bit_bf16_kernel<M, false>), dim3(grid), dim3(THREADS), 0, s, a)); }
     }
     return check_launch("msr_adamw8bit_step");
+}
+
+int msr_stream_probe8(uint16_t *p, const uint16_t *g, uint8_t *state1, uint8_t *state2, float *absmax1,
+                      float *absmax2, int64_t n, int32_t grid, int32_t lds_bytes, msr_stream_t stream) {
+    if (n <= 0 || n % F8_PAIR || !p || !g || !state1 || !state2 || !absmax1 || !absmax2) {
+        set_error("msr_stream_probe8: n must be a positive multiple of %d and every pointer set", F8_PAIR);
+        return MSR_ERR_ARG;
+    }
+    if (!aligned(p, 16) || !aligned(g, 16) || !aligned(state1, 8) || !aligned(state2, 8)) {
+        set_error("msr_stream_probe8: p, g need 16-byte and the codes 8-byte alignment");
+        return MSR_ERR_ALIGN;
+    }
+    if (grid < 1 || grid > (1 << 20) || lds_bytes < 0 || lds_bytes > (64 << 10)) {
+        set_error("msr_stream_probe8: grid %d not in [1, 2^20] or lds_bytes %d not in [0, 64 KiB]", (int)grid, (int)lds_bytes);
+        return MSR_ERR_ARG;
+    }
+    Adam8Args a = {};
+    a.p = p; a.g = g; a.s1 = state1; a.s2 = state2; a.absmax1 = absmax1; a.absmax2 = absmax2; a.n = n;
+    hipLaunchKernelGGL(stream8_probe_kernel, dim3((unsigned)grid), dim3(F8_THREADS), (unsigned)lds_bytes,
+                       (hipStream_t)stream, a, n / F8_PAIR);
+    return check_launch("msr_stream_probe8");
 }
 
 int msr_quantize(const float *x, uint8_t *out, int64_t n, const float *qmap, int32_t is_signed, const void *qtable,

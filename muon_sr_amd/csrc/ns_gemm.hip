@@ -870,9 +870,10 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_nt_kernel(GemmArgs a) {
         };
         // The next tile's first slab was loaded before this tile's stores.  With
         // FL the epilogue issues 16 unconditional store instructions per lane
-        // after those loads, and vector memory operations complete in order, so
-        // waiting for all but the last 16 leaves the stores in flight; otherwise
-        // wait for everything.
+        // after those loads (with APPLY also 16 parameter loads, each block's before
+        // its stores), and vector memory operations complete in order, so waiting
+        // for all but the last 16 leaves stores in flight and the slab landed;
+        // otherwise wait for everything.
         epilogue(std::integral_constant<bool, FULL>{});
         if constexpr (FULL) wait_vm<16>();
         else __builtin_amdgcn_s_waitcnt(0);
@@ -1394,7 +1395,9 @@ static int launch_gemm(const GemmArgs &a0, int64_t batch, hipStream_t s) {
             if (!ab.rvec) { set_error("gemm: X' = B' X needs the diagonal residuals"); return (int)MSR_ERR_ARG; }
             if (ab.apply1 > 0) {   // the last product of msr_muon_ns_apply: D / DT are the parameters
                 if (c || d == dt) { set_error("gemm: unsupported apply epilogue"); return (int)MSR_ERR_ARG; }
-                if (d) { MSR_DISPATCH_NOISE(ab.apply1 - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P, -1, EPI_X, M>), grid, block, 0, s, ab)); }
+                if (d && full) { MSR_DISPATCH_NOISE(ab.apply1 - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P, -1, EPI_X, M, true>), grid, block, 0, s, ab)); }
+                else if (d) { MSR_DISPATCH_NOISE(ab.apply1 - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P, -1, EPI_X, M>), grid, block, 0, s, ab)); }
+                else if (full) { MSR_DISPATCH_NOISE(ab.apply1 - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, false, true, GM_TRI_P, -1, EPI_X, M, true>), grid, block, 0, s, ab)); }
                 else { MSR_DISPATCH_NOISE(ab.apply1 - 1, M, hipLaunchKernelGGL((gemm_nt_kernel<false, false, false, true, GM_TRI_P, -1, EPI_X, M>), grid, block, 0, s, ab)); }
             } else if (!c && d && !dt) {
                 if (full) hipLaunchKernelGGL((gemm_nt_kernel<false, false, true, false, GM_TRI_P, -1, EPI_X, -1, true>), grid, block, 0, s, ab);

@@ -26,6 +26,34 @@ __device__ __forceinline__ f32x4_t ld_nt4f(const void *p) { return __builtin_non
 __device__ __forceinline__ void st_nt4(void *p, u32x4_t v) { __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t *>(p)); }
 __device__ __forceinline__ void st_nt2(void *p, u32x2_t v) { __builtin_nontemporal_store(v, reinterpret_cast<u32x2_t *>(p)); }
 
+// Non-temporal accesses at a wave-uniform base plus a per-lane byte offset, through a
+// buffer resource made from the base (scalar instructions): the 64-bit address
+// arithmetic of the global forms stays off the VALU.  `ubase` must be the same in
+// every lane; the offset is below 2^31.  aux 2 = nt.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *ubase) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(ubase), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ u32x4_t ldu_nt4(const void *ubase, uint32_t off) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(uniform_rsrc(ubase), (int)off, 0, 2));
+}
+__device__ __forceinline__ u32x2_t ldu_nt2(const void *ubase, uint32_t off) {
+    return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(uniform_rsrc(ubase), (int)off, 0, 2));
+}
+__device__ __forceinline__ float ldu_f32(const void *ubase, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(uniform_rsrc(ubase), (int)off, 0, 0));
+}
+__device__ __forceinline__ void stu_nt4(void *ubase, uint32_t off, u32x4_t v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v),
+                                           uniform_rsrc(ubase), (int)off, 0, 2);
+}
+__device__ __forceinline__ void stu_nt2(void *ubase, uint32_t off, u32x2_t v) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, v),
+                                          uniform_rsrc(ubase), (int)off, 0, 2);
+}
+__device__ __forceinline__ void stu_f32(void *ubase, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), uniform_rsrc(ubase), (int)off, 0, 0);
+}
+
 template <bool VEC>
 __device__ __forceinline__ void load_bf16x8(const uint16_t *base, int64_t o0, int valid, uint32_t w[4]) {
     if (VEC && valid == 8) {

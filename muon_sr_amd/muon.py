@@ -235,6 +235,51 @@ def _transposed_partners(items, ns_steps):
     return pairs
 
 
+# Independent library calls of one batch_ns step (one shape group or chunk each) alternate
+# between the caller's stream and a side stream per device, so that the last, partly
+# filled round of tiles of one call's Newton-Schulz products overlaps the next call's
+# work (config 4: 0.5 % faster).  Results do not depend on it: the calls touch disjoint
+# memory and their seeds do not depend on the order.  Streams keep the default priority.
+TWO_STREAMS = True
+_side_streams = {}
+
+
+def _side_stream(device):
+    s = _side_streams.get(device)
+    if s is None:
+        s = torch.cuda.Stream(device=device)
+        _side_streams[device] = s
+    return s
+
+
+def _run_calls(calls, device):
+    """Runs `calls` [(fn, tensors)]: every other one on the side stream, which first waits
+    for the caller's stream (the gradients are written there) and which the caller's
+    stream waits for at the end.  Tensors a side-stream call reads or writes are marked
+    as in use by that stream (record_stream), so memory freed after the step is not
+    reused before it is done; its workspace is allocated on the side stream itself."""
+    if len(calls) < 2 or not TWO_STREAMS:
+        for fn, _ in calls:
+            fn()
+        return
+    main = torch.cuda.current_stream(device)
+    side = _side_stream(device)
+    start = torch.cuda.Event()
+    start.record(main)
+    side.wait_event(start)
+    for i, (fn, tensors) in enumerate(calls):
+        if i % 2 == 0:
+            fn()
+            continue
+        with torch.cuda.stream(side):
+            fn()
+        for t in tensors:
+            t.record_stream(side)
+    done = torch.cuda.Event()
+    done.record(side)
+    main.wait_event(done)
+
+
 def _check_param(p, name):
     _lib.require_gpu(p, name, RuntimeError)
     if not p.is_contiguous():
@@ -262,10 +307,12 @@ def _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns
     NS + apply per chunk (seed salt 1, index shape_idx*10000 + i).  A group with
     missing gradients falls back to per-parameter steps with index
     shape_idx*10000 + i.  Two whole groups of transposed shapes take one call
-    (_fused_steps) with the same seeds and results.
+    (_fused_steps) with the same seeds and results.  The fused calls of whole
+    groups run last, on two streams (_run_calls).
     """
     items = list(shape_groups.items())
     partners = _transposed_partners(items, ns_steps)
+    calls = []   # the fused library calls of whole groups, run at the end by _run_calls
 
     def whole_group(idx):   # the one chunk of a whole group, as the loop below makes it
         shape, grp = items[idx]
@@ -274,11 +321,16 @@ def _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns
         return ([_bf16_contig(q.grad) for q in ordered], stacked_bufs[shape][0], 0, [q.data for q in ordered],
                 _deterministic_seed(step, idx, salt=0), _ns_scale(shape), seeds)
 
+    def used(groups):   # the tensors a call reads or writes
+        return [t for g in groups for t in (*g[0], g[1], *g[3])]
+
     for shape_idx, (shape, grp_params) in enumerate(items):
         j = partners.get(shape_idx)
         if j is not None:
             if j > shape_idx:   # at the first group's turn, both groups (the second's turn is skipped)
-                _fused_steps([whole_group(shape_idx), whole_group(j)], beta, nesterov, ns_steps, lr, weight_decay)
+                pair = [whole_group(shape_idx), whole_group(j)]
+                calls.append((lambda pair=pair: _fused_steps(pair, beta, nesterov, ns_steps, lr, weight_decay),
+                              used(pair)))
             continue
         active = [p for p in grp_params if p.grad is not None]
         if not active:
@@ -296,9 +348,9 @@ def _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns
                 for start in range(0, Na, k):
                     chunk = ordered[start:start + k]
                     seeds = [_deterministic_seed(step, shape_idx * 10000 + start + j, salt=1) for j in range(len(chunk))]
-                    _fused_step(grads[start:start + k], stacked_buf[start], start, [p.data for p in chunk], beta,
-                                nesterov, _deterministic_seed(step, shape_idx, salt=0), ns_steps, lr, weight_decay,
-                                scale, seeds)
+                    args = (grads[start:start + k], stacked_buf[start], start, [p.data for p in chunk], beta, nesterov,
+                            _deterministic_seed(step, shape_idx, salt=0), ns_steps, lr, weight_decay, scale, seeds)
+                    calls.append((lambda args=args: _fused_step(*args), [*args[0], args[1], *args[3]]))
                 continue
             work = torch.empty(Na, *shape, dtype=torch.bfloat16, device=active[0].device)
             _run_prepare(grads, stacked_buf, work, beta, nesterov, _deterministic_seed(step, shape_idx, salt=0))
@@ -314,6 +366,11 @@ def _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns
                 idx = buf_indices[id(p)]
                 _muon_step(p, p.grad, stacked_buf[idx], beta, nesterov, ns_steps, lr, weight_decay, step,
                            shape_idx * 10000 + idx)
+    by_device = {}
+    for c in calls:
+        by_device.setdefault(c[1][0].device, []).append(c)
+    for device, cs in by_device.items():
+        _run_calls(cs, device)
 
 
 def _init_stacked_bufs(params, device, state):

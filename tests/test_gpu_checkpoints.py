@@ -109,9 +109,17 @@ def _gpu_ns(U):
     return dev_to_u16(newton_schulz(u16_to_dev(U.ravel()).view(U.shape))).reshape(U.shape)
 
 
+# Relative Frobenius distance allowed between this library's and the reference's Muon step
+# deltas: the reference's bf16 Newton-Schulz differs from this library's by 2-3 % on such
+# inputs, and a small difference before stochastic rounding flips whole-ulp rounding
+# decisions although the noise bits are the same (the trajectory tests measure 3.8-4.5e-2).
+MUON_DELTA_TOL = 6e-2
+
+
 def _check_muon_batch(opt, ps, rec, idx, lr, wd):
     """Muon parameters idx: momentum against the reference, parameters against the oracle's
-    composition of the same step with this library's NS (seeds at the restored global step)."""
+    composition of the same step with this library's NS (seeds at the restored global step),
+    and the step itself against the reference's next parameters within MUON_DELTA_TOL."""
     sd = rec["state_dict"]
     params = [_u16(rec["p_ckpt"][j]).reshape(tuple(rec["p_ckpt"][j].shape)) for j in idx]
     grads = [_u16(rec["grads_next"][j]).reshape(params[i].shape) for i, j in enumerate(idx)]
@@ -127,6 +135,13 @@ def _check_muon_batch(opt, ps, rec, idx, lr, wd):
         assert st["step"] == rec["state_next"][j]["step"] == step, ("step", j)
         assert _same_tensor(st["momentum_buffer"], rec["state_next"][j]["momentum_buffer"]), ("momentum", j)
         assert np.array_equal(dev_to_u16(ps[j].data).ravel(), new_p[i].ravel()), ("param", j)
+        before = torch.from_numpy(np.ascontiguousarray(params[i]).view(np.int16).copy()).view(torch.bfloat16).double()
+        ref_next = rec["p_next"][j].detach().cpu().double().reshape(before.shape)
+        d_ours = ps[j].data.detach().cpu().double().reshape(before.shape) - before
+        d_ref = ref_next - before
+        e = (torch.linalg.norm(d_ours - d_ref) / torch.linalg.norm(d_ref)).item()
+        print(f"param {j}: step delta vs the reference's, relative Frobenius {e:.3e}")
+        assert e < MUON_DELTA_TOL, ("step delta", j, e)
 
 
 def test_reference_checkpoint_triton_adamw(L, ckpt, triton_noise):

@@ -163,3 +163,46 @@ def test_batch_step_merged_equals_chunked(L, noise, mode_name, monkeypatch):
     for i in range(len(shapes)):
         assert torch.equal(_bits(merged[0][i]), _bits(chunked[0][i])), ("param", i)
         assert torch.equal(_bits(merged[1][i]), _bits(chunked[1][i])), ("momentum", i)
+
+
+@pytest.mark.parametrize("mode_name", ["triton", "philox8"])
+def test_batch_step_two_streams_equals_one(L, noise, mode_name, monkeypatch):
+    """The fused calls of a batch_ns step alternate between the caller's stream and a side
+    stream; three steps with several calls each (a transposed pair, a square group and a
+    group cut into chunks) equal, bit for bit, the same steps on one stream, and the
+    caller's stream sees the results without a device-wide synchronisation."""
+    from muon_sr_amd import TritonMuonSR
+    from muon_sr_amd import muon as M
+    noise(mode_name)
+    shapes = [(256, 512), (512, 256), (384, 384), (256, 512), (128, 640), (128, 640), (128, 640)]
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(23)
+    p0 = [(torch.randn(s, device=DEV, generator=gen) * 0.02).to(torch.bfloat16) for s in shapes]
+    grads = [[(torch.randn(s, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16) for s in shapes]
+             for _ in range(3)]
+    monkeypatch.setattr(M, "NS_BATCH_NUMEL", 2 * 128 * 640 + 1000)   # the 128 x 640 group runs in 2 chunks
+    n_calls = []
+    real = M._run_calls
+    monkeypatch.setattr(M, "_run_calls", lambda calls, dev: (n_calls.append(len(calls)), real(calls, dev)))
+
+    def run(two):
+        monkeypatch.setattr(M, "TWO_STREAMS", two)
+        ps = [torch.nn.Parameter(x.clone()) for x in p0]
+        opt = TritonMuonSR(ps, lr=0.02, weight_decay=0.01, batch_ns=True)
+        for step in range(3):
+            for p, g in zip(ps, grads[step]):
+                p.grad = g.clone()
+            opt.step()
+            for p in ps:
+                p.grad = None   # gradients freed while the side stream may still run
+        # read on the caller's stream: ordered after the side stream by the step's join
+        out = [p.detach().clone() for p in ps], [opt.state[p]["momentum_buffer"].clone() for p in ps]
+        torch.cuda.synchronize()
+        return out
+
+    one = run(False)
+    two = run(True)
+    assert n_calls and min(n_calls) >= 3, n_calls
+    for i in range(len(shapes)):
+        assert torch.equal(_bits(one[0][i]), _bits(two[0][i])), ("param", i)
+        assert torch.equal(_bits(one[1][i]), _bits(two[1][i])), ("momentum", i)

@@ -365,6 +365,7 @@ def bench_sr_accum(micro=16):
 
     model = Holder()
     TritonSRAccumulator.max_deferred_bytes = 1 << 40   # one launch per micro-batch
+    host_s = []   # host time of the hook loop, one launch per hook
 
     def micro_batch(gs, evs=None, deferred=True):
         s = torch.cuda.Event(enable_timing=True)
@@ -378,9 +379,11 @@ def bench_sr_accum(micro=16):
             e.record()
         else:
             s.record()
+            h0 = time.perf_counter()
             for p, g in zip(params, gs):
                 p.grad = g
                 TritonSRAccumulator._accum_hook(p)
+            host_s.append(time.perf_counter() - h0)
             e.record()
         if evs is not None:
             evs.append((s, e))
@@ -409,10 +412,13 @@ def bench_sr_accum(micro=16):
     TritonSRAccumulator.reassign_grad_buffer(model)
     sync()
     per_tensor = sum(s.elapsed_time(e) for s, e in evs1[1:]) / 3
+    # host time per hook (the Python hook, the ctypes call and the launch), micro-batches 2-4
+    host_us = sum(host_s[1:]) / len(host_s[1:]) / len(params) * 1e6
     out = dict(tensors=len(params), elements=numel, micro_batches=micro, total_ms=wall,
                first_microbatch_ms=ms[0], accumulate_ms=steady,
                accumulate_gbps=6.0 * numel / (steady * 1e6), first_gbps=4.0 * numel / (ms[0] * 1e6),
-               per_tensor_launch_ms=per_tensor, per_tensor_launch_gbps=6.0 * numel / (per_tensor * 1e6))
+               per_tensor_launch_ms=per_tensor, per_tensor_launch_gbps=6.0 * numel / (per_tensor * 1e6),
+               host_us_per_hook=host_us)
     del gsets, params, model
     torch.cuda.empty_cache()
     return out
@@ -891,6 +897,21 @@ def main():
         # the same accesses without the arithmetic, best over occupancy and grid, this run
         line["roofline"]["pattern_ceiling_gbps"] = probe["best_gbps"]
         line["roofline"]["frac_of_pattern_ceiling"] = round(kernel_gbps / probe["best_gbps"], 4)
+    k_other = f"adamw8bit_2^28_{other}_noise"
+    if k_other in configs:   # the same kernel with the other noise stream
+        line["roofline"][f"frac_{other}_noise"] = round(configs[k_other]["kernel_gbps"] / HBM_PEAK_GBPS, 4)
+    # config 3, SR accumulation (HBM-bound, 6 B per element and micro-batch): queued hooks
+    # (one launch per up to 80 tensors) and one launch per hook, in both noise streams
+    sr = {}
+    for key, tag in (("sr_accum_24L_d2048", args.noise), (f"sr_accum_24L_d2048_{other}_noise", other)):
+        if key in configs:
+            c = configs[key]
+            sr[tag] = {"queued_gbps": c["accumulate_gbps"], "queued_frac": round(c["accumulate_gbps"] / HBM_PEAK_GBPS, 4),
+                       "per_hook_gbps": c["per_tensor_launch_gbps"],
+                       "per_hook_frac": round(c["per_tensor_launch_gbps"] / HBM_PEAK_GBPS, 4),
+                       "host_us_per_hook": c["host_us_per_hook"]}
+    if sr:
+        line["roofline_sr_accum"] = {"bound": "hbm", "peak": HBM_PEAK_GBPS, "unit": "GB/s", "noise": sr}
     if "muon_ns_16L_d2048" in configs:
         line["ns_tflops"] = configs["muon_ns_16L_d2048"]["tflops"]
         line["ns_frac_of_bf16_peak"] = round(configs["muon_ns_16L_d2048"]["tflops"] / BF16_PEAK_TFLOPS, 4)

@@ -238,9 +238,14 @@ def _transposed_partners(items, ns_steps):
 # Independent library calls of one batch_ns step (one shape group or chunk each) alternate
 # between the caller's stream and a side stream per device, so that the last, partly
 # filled round of tiles of one call's Newton-Schulz products overlaps the next call's
-# work (config 4: 0.5 % faster).  Results do not depend on it: the calls touch disjoint
-# memory and their seeds do not depend on the order.  Streams keep the default priority.
+# work.  That pays where the launches are short: steps whose matrices total at most
+# TWO_STREAMS_MAX_NUMEL elements (config 4, 8.2e8 elements: 1.0 % faster); on config 5
+# (7.0e9 elements, launches of 30+ rounds of tiles) the overlapping calls measured 0.7 %
+# slower, and such steps stay on one stream.  Results do not depend on it: the calls
+# touch disjoint memory and their seeds do not depend on the order.  Streams keep the
+# default priority.
 TWO_STREAMS = True
+TWO_STREAMS_MAX_NUMEL = 1 << 30
 _side_streams = {}
 
 
@@ -253,13 +258,14 @@ def _side_stream(device):
 
 
 def _run_calls(calls, device):
-    """Runs `calls` [(fn, tensors)]: every other one on the side stream, which first waits
-    for the caller's stream (the gradients are written there) and which the caller's
-    stream waits for at the end.  Tensors a side-stream call reads or writes are marked
-    as in use by that stream (record_stream), so memory freed after the step is not
-    reused before it is done; its workspace is allocated on the side stream itself."""
-    if len(calls) < 2 or not TWO_STREAMS:
-        for fn, _ in calls:
+    """Runs `calls` [(fn, tensors, numel)]: with two streams, every other one on the side
+    stream, which first waits for the caller's stream (the gradients are written there)
+    and which the caller's stream waits for at the end.  Tensors a side-stream call reads
+    or writes are marked as in use by that stream (record_stream), so memory freed after
+    the step is not reused before it is done; its workspace is allocated on the side
+    stream itself."""
+    if len(calls) < 2 or not TWO_STREAMS or sum(c[2] for c in calls) > TWO_STREAMS_MAX_NUMEL:
+        for fn, _, _ in calls:
             fn()
         return
     main = torch.cuda.current_stream(device)
@@ -267,7 +273,7 @@ def _run_calls(calls, device):
     start = torch.cuda.Event()
     start.record(main)
     side.wait_event(start)
-    for i, (fn, tensors) in enumerate(calls):
+    for i, (fn, tensors, _) in enumerate(calls):
         if i % 2 == 0:
             fn()
             continue
@@ -330,7 +336,7 @@ def _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns
             if j > shape_idx:   # at the first group's turn, both groups (the second's turn is skipped)
                 pair = [whole_group(shape_idx), whole_group(j)]
                 calls.append((lambda pair=pair: _fused_steps(pair, beta, nesterov, ns_steps, lr, weight_decay),
-                              used(pair)))
+                              used(pair), sum(len(g[0]) * g[3][0].numel() for g in pair)))
             continue
         active = [p for p in grp_params if p.grad is not None]
         if not active:
@@ -350,7 +356,8 @@ def _muon_batch_step(shape_groups, stacked_bufs, buf_indices, beta, nesterov, ns
                     seeds = [_deterministic_seed(step, shape_idx * 10000 + start + j, salt=1) for j in range(len(chunk))]
                     args = (grads[start:start + k], stacked_buf[start], start, [p.data for p in chunk], beta, nesterov,
                             _deterministic_seed(step, shape_idx, salt=0), ns_steps, lr, weight_decay, scale, seeds)
-                    calls.append((lambda args=args: _fused_step(*args), [*args[0], args[1], *args[3]]))
+                    calls.append((lambda args=args: _fused_step(*args), [*args[0], args[1], *args[3]],
+                                  len(chunk) * chunk[0].numel()))
                 continue
             work = torch.empty(Na, *shape, dtype=torch.bfloat16, device=active[0].device)
             _run_prepare(grads, stacked_buf, work, beta, nesterov, _deterministic_seed(step, shape_idx, salt=0))

@@ -184,6 +184,7 @@ def test_batch_step_two_streams_equals_one(L, noise, mode_name, monkeypatch):
     n_calls = []
     real = M._run_calls
     monkeypatch.setattr(M, "_run_calls", lambda calls, dev: (n_calls.append(len(calls)), real(calls, dev)))
+    assert sum(p.numel() for p in p0) <= M.TWO_STREAMS_MAX_NUMEL
 
     def run(two):
         monkeypatch.setattr(M, "TWO_STREAMS", two)

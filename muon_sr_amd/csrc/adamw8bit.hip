@@ -452,6 +452,30 @@ __device__ __forceinline__ Raw8 fetch_pair(const Adam8Args &a, int64_t pr, uint3
     return r;
 }
 
+// The pairs a wave walks: pr, pr + stride, ... below end (groups of np adjacent pairs).
+// The work-groups of one XCD take runs of MSR_F8_XCD_RUN consecutive places of the
+// grid-stride order (-1: a run of g / 8, the XCD's whole share of each sweep).  A run of 4
+// work-groups is 16 pairs, one 128-byte line of each block-scale array, which is then
+// written from one XCD's L2 rather than from four.  Measured on 2^28 elements (A/B in one
+// process, bit-exact): the step 2.4 % faster than places in dispatch order (runs of 32
+// and g / 8: 1.4 % and 0 %), the access-pattern probe at 16 waves per CU 8.5 % faster.
+#ifndef MSR_F8_XCD_RUN
+#define MSR_F8_XCD_RUN 4
+#endif
+struct F8Walk {
+    int64_t pr, end, stride;
+};
+__device__ __forceinline__ F8Walk f8_walk(int64_t npairs, int wave, int np) {
+    const int64_t b = blockIdx.x, g = gridDim.x;
+    constexpr int W = F8_THREADS / 64;
+    const int64_t run = MSR_F8_XCD_RUN >= 0 ? MSR_F8_XCD_RUN : ((g & 7) == 0 ? g / 8 : 0);
+    F8Walk w;
+    w.pr = (xcd_place(b, g, run) * W + wave) * np;
+    w.end = npairs;
+    w.stride = g * W * np;
+    return w;
+}
+
 // Four waves per SIMD (16 per CU) hide the branch's latency chains: at most 128 VGPRs.
 #ifndef MSR_F8_MIN_WAVES
 #define MSR_F8_MIN_WAVES 4
@@ -472,21 +496,22 @@ __global__ __launch_bounds__(F8_THREADS, MSR_F8_MIN_WAVES) void adamw8bit_fast_k
     // the pair index is wave-uniform: addresses are a scalar base plus a fixed lane offset.
     // Each wave takes F8_NP adjacent pairs per iteration (npairs is a multiple of F8_NP).
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int64_t wstride = (int64_t)gridDim.x * (F8_THREADS / 64) * F8_NP;
-    int64_t pr = ((int64_t)blockIdx.x * (F8_THREADS / 64) + wave) * F8_NP;
+    const F8Walk walk = f8_walk(npairs, wave, F8_NP);
+    const int64_t wstride = walk.stride, pend = walk.end;
+    int64_t pr = walk.pr;
     uint32_t *deferred = s_deferred[wave];
     for (;;) {
         int ndef = 0;
         Raw8 nxt[F8_NP];
-        if (pr < npairs) {
+        if (pr < pend) {
 #pragma unroll
             for (int q = 0; q < F8_NP; ++q) nxt[q] = fetch_pair(a, pr + q, lane);
         }
-        for (; pr < npairs; pr += wstride) {
+        for (; pr < pend; pr += wstride) {
             Raw8 raw[F8_NP];
 #pragma unroll
             for (int q = 0; q < F8_NP; ++q) raw[q] = nxt[q];
-            if (pr + wstride < npairs) {
+            if (pr + wstride < pend) {
 #pragma unroll
                 for (int q = 0; q < F8_NP; ++q) nxt[q] = fetch_pair(a, pr + wstride + q, lane);
             }
@@ -508,7 +533,7 @@ __global__ __launch_bounds__(F8_THREADS, MSR_F8_MIN_WAVES) void adamw8bit_fast_k
             const int64_t pe = (int64_t)__builtin_amdgcn_readfirstlane(deferred[i]);
             adam8_pair_exact<MODE>(a, fetch_pair(a, pe, lane), pe * F8_PAIR + lane * 8, pe * 2 + (lane >> 5), q1s, q2s);
         }
-        if (pr >= npairs) break;
+        if (pr >= pend) break;
     }
 }
 
@@ -522,13 +547,14 @@ __global__ __launch_bounds__(F8_THREADS) void stream8_probe_kernel(Adam8Args a, 
     extern __shared__ uint32_t occupancy_pad[];
     const uint32_t lane = threadIdx.x & 63u;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int64_t wstride = (int64_t)gridDim.x * (F8_THREADS / 64);
-    int64_t pr = (int64_t)blockIdx.x * (F8_THREADS / 64) + wave;
-    if (pr >= npairs) return;
+    const F8Walk walk = f8_walk(npairs, wave, 1);
+    const int64_t wstride = walk.stride, pend = walk.end;
+    int64_t pr = walk.pr;
+    if (pr >= pend) return;
     Raw8 nxt = fetch_pair(a, pr, lane);
-    for (; pr < npairs; pr += wstride) {
+    for (; pr < pend; pr += wstride) {
         const Raw8 raw = nxt;
-        if (pr + wstride < npairs) nxt = fetch_pair(a, pr + wstride, lane);
+        if (pr + wstride < pend) nxt = fetch_pair(a, pr + wstride, lane);
         const int64_t o0 = pr * F8_PAIR + lane * 8;
         const u32x4_t pw = raw.p ^ raw.g;
         st_nt4(a.p + o0, pw);

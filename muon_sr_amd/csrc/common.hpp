@@ -322,6 +322,16 @@ __device__ __forceinline__ float quotient_unsigned(float v, double rd) { return 
 // (msr_fastmath_check).
 // ---------------------------------------------------------------------------
 
+// Work-group b of a grid of g -> its place in the work order.  Consecutive work-groups
+// are dispatched over the 8 XCDs in turn; each run of 8 K work-groups takes 8 runs of K
+// consecutive places, one run per XCD, so neighbouring work is done from one XCD's L2
+// (K = 0: places in dispatch order; work-groups past the last whole run keep theirs).
+__device__ __forceinline__ int64_t xcd_place(int64_t b, int64_t g, int64_t K) {
+    if (K <= 0 || b >= g / (8 * K) * (8 * K)) return b;
+    const int64_t r = b % (8 * K);
+    return b - r + (r & 7) * K + (r >> 3);
+}
+
 // Opaque VGPR copy of a wave-uniform value, so arithmetic with it keeps the
 // fast issue rate (the compiler would otherwise read kernel arguments as SGPRs).
 __device__ __forceinline__ float vgpr(float x) {

@@ -1089,12 +1089,22 @@ struct PrologueArgs {
     int64_t ntx, ntiles;
 };
 
+// Tiles in runs of MSR_PRO_XCD consecutive tiles per XCD (a row of 32 tiles of a
+// 2048-column matrix): config 4's prologue 14 % faster than tiles in dispatch order
+// (1.27 -> 1.09 ms per step; runs of 8: 12 %), bit-exact.
+#ifndef MSR_PRO_XCD
+#define MSR_PRO_XCD 32
+#endif
 template <int SRC, int MODE, bool NEST, bool G32, bool VEC>
 __global__ __launch_bounds__(256) void ns_prologue_kernel(PrologueArgs a) {
     __shared__ __align__(16) uint16_t tile[64][72];
     __shared__ float red[256];
-    const int64_t b = blockIdx.z;
-    const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+    // tile (tx, ty) of matrix b: work-groups in runs of MSR_PRO_XCD consecutive tiles per XCD
+    const int64_t gx = gridDim.x, gy = gridDim.y;
+    const int64_t lin = xcd_place((int64_t)blockIdx.x + gx * ((int64_t)blockIdx.y + gy * (int64_t)blockIdx.z),
+                                  gx * gy * (int64_t)gridDim.z, MSR_PRO_XCD);
+    const int64_t tx = lin % gx, ty = (lin / gx) % gy, b = lin / (gx * gy);
+    const int64_t r0 = ty * 64, c0 = tx * 64;
     const int64_t numel = a.rows * a.cols;
     const int j = threadIdx.x & 7, i0 = threadIdx.x >> 3;
     const float one_m_beta = 1.0f - a.beta;
@@ -1192,7 +1202,7 @@ __global__ __launch_bounds__(256) void ns_prologue_kernel(PrologueArgs a) {
         if (threadIdx.x < wdt) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + wdt];
         __syncthreads();
     }
-    if (threadIdx.x == 0) a.tpart[b * a.ntiles + (int64_t)blockIdx.y * a.ntx + blockIdx.x] = red[0];
+    if (threadIdx.x == 0) a.tpart[b * a.ntiles + ty * a.ntx + tx] = red[0];
     if (!a.T) return;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {

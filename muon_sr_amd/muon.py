@@ -263,8 +263,9 @@ def _run_calls(calls, device):
     and which the caller's stream waits for at the end.  Tensors a side-stream call reads
     or writes are marked as in use by that stream (record_stream), so memory freed after
     the step is not reused before it is done; its workspace is allocated on the side
-    stream itself."""
-    if len(calls) < 2 or not TWO_STREAMS or sum(c[2] for c in calls) > TWO_STREAMS_MAX_NUMEL:
+    stream itself.  Under HIP graph capture every call stays on the caller's stream."""
+    if (len(calls) < 2 or not TWO_STREAMS or sum(c[2] for c in calls) > TWO_STREAMS_MAX_NUMEL
+            or torch.cuda.is_current_stream_capturing()):
         for fn, _, _ in calls:
             fn()
         return

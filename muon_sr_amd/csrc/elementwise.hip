@@ -51,10 +51,17 @@ int check_launch(const char *what) {
 // before computing them.  A tensor's offsets, and so its noise counters,
 // start at 0: the result equals one sr_accum_kernel launch per tensor.
 constexpr int ACC_MAXT = 80;
+// Tiles of 128 threads x 2 groups (2048 elements).  Measured on config 3's 217 tensors
+// against 256 x 4: the per-hook launches (one per tensor) 7 % faster (256 x 1 and 256 x 2
+// within 1 %, 256 x 8 12 % slower), the multi-tensor launch 2.2 % faster (256 x 2 and
+// 512 x 2 0.4-1.0 %, 64 x 4 0.3 %).
 #ifndef MSR_ACC_U
-#define MSR_ACC_U 4
+#define MSR_ACC_U 2
 #endif
-constexpr int ACC_THREADS = 256, ACC_U = MSR_ACC_U, ACC_TILE = ACC_THREADS * ACC_U;
+#ifndef MSR_ACC_THREADS
+#define MSR_ACC_THREADS 128
+#endif
+constexpr int ACC_THREADS = MSR_ACC_THREADS, ACC_U = MSR_ACC_U, ACC_TILE = ACC_THREADS * ACC_U;
 constexpr uint32_t ACC_ZERO = 1, ACC_F32 = 2, ACC_VEC = 4;
 struct AccumMultiArgs {
     int count;
@@ -119,11 +126,12 @@ __global__ __launch_bounds__(ACC_THREADS) void sr_accum_kernel(uint16_t *__restr
 }
 
 // The multi-tensor launch takes its tiles in runs of MSR_ACC_XCD consecutive tiles per XCD
-// (512 KiB of bf16 accumulator): config 3's accumulation 1.4-1.5 % faster than tiles in
-// dispatch order (runs of 4: 7 % slower, 256: equal), bit-exact.  The one-tensor launches
-// of the per-hook path measured 5 % slower that way and keep the dispatch order.
+// (128 tiles: 512 KiB of bf16 accumulator), 0.7 % faster than tiles in dispatch order (runs
+// of 16 tiles 5 % slower, 32 and 64 equal; with 16 KiB tiles of 256 x 4 groups, runs of 32
+// measured 1.4 %); bit-exact.  The one-tensor launches of the per-hook path keep the
+// dispatch order (runs of 32 tiles of 256 x 4 groups measured 5 % slower there).
 #ifndef MSR_ACC_XCD
-#define MSR_ACC_XCD 32
+#define MSR_ACC_XCD 128
 #endif
 
 template <int MODE>
@@ -352,7 +360,7 @@ static inline Noise make_noise(uint32_t seed, uint32_t k, const uint16_t *inject
     } while (0)
 
 #ifndef MSR_ACC_GRID_CAP
-#define MSR_ACC_GRID_CAP (1 << 20)   // one work-group per tile: measured best (6.15 TB/s on 7.8 GB)
+#define MSR_ACC_GRID_CAP (1 << 20)   // one work-group per tile: measured best
 #endif
 
 extern "C" {

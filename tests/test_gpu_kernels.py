@@ -940,6 +940,50 @@ def test_muon_fused_step_equals_separate_calls(L, batch, rows, cols, first, f32,
         assert torch.equal(prm.view(torch.int16), params0.view(torch.int16))
 
 
+@pytest.mark.parametrize("steps", [1, 2, 3])
+@pytest.mark.parametrize("rows,cols", [(256, 512), (512, 256)])
+@pytest.mark.parametrize("mode", [O.NOISE_TRITON, O.NOISE_PHILOX8])
+def test_muon_fused_step_few_iterations(L, steps, rows, cols, mode):
+    """ns_steps below the default: with one iteration the first X' product both takes the
+    normalisation factor s (the prologue leaves X0 unscaled) and applies the update in its
+    store.  msr_muon_fused_step equals msr_muon_prepare + msr_newton_schulz(steps) +
+    msr_muon_apply bit for bit, wide and tall (muon_sr/triton_muon_sr.py:18-80; ns_steps is a
+    param-group key, muon_sr/triton_muon_sr.py:198-200)."""
+    import ctypes
+    from muon_sr_amd.muon import newton_schulz, NS_COEFFS
+    a, b, c = NS_COEFFS
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(31 * steps + rows + mode)
+    batch, numel = 3, rows * cols
+    grads = [(torch.randn(rows, cols, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16) for _ in range(batch)]
+    stack0 = (torch.randn(batch, rows, cols, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16)
+    params0 = (torch.randn(batch, rows, cols, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+    beta, pseed = 0.95, 0x1B873593
+    seeds = [(0x85EBCA6B * (i + 5)) & 0xFFFFFFFF for i in range(batch)]
+    lr, wd, scale = 0.02, 0.01, max(1.0, rows / cols) ** 0.5
+    gtab = ptr_array([g.data_ptr() for g in grads])
+    seeds_c = ptr_array(seeds, ctypes.c_uint32)
+    stack_ref = stack0.clone()
+    work = torch.empty(batch, rows, cols, dtype=torch.bfloat16, device=DEV)
+    check(L, L.msr_muon_prepare(gtab, 0, stack_ref.data_ptr(), work.data_ptr(), numel, batch, beta, 1, pseed, mode,
+                                None, stream()), "msr_muon_prepare")
+    X = newton_schulz(work, steps=steps)
+    p_ref = params0.clone()
+    check(L, L.msr_muon_apply(ptr_array([p_ref[i].data_ptr() for i in range(batch)]), X.data_ptr(), numel, batch, lr, wd,
+                              scale, seeds_c, mode, None, stream()), "msr_muon_apply")
+    stack, prm = stack0.clone(), params0.clone()
+    nb = ctypes.c_size_t(0)
+    check(L, L.msr_ns_workspace_bytes(batch, rows, cols, ctypes.byref(nb)), "ws")
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=DEV)
+    check(L, L.msr_muon_fused_step(gtab, 0, stack.data_ptr(), 0, batch, rows, cols, beta, 1, pseed, steps, a, b, c, None,
+                                   ptr_array([prm[i].data_ptr() for i in range(batch)]), seeds_c, lr, wd, scale, mode,
+                                   None, None, ws.data_ptr(), nb.value, stream()), "msr_muon_fused_step")
+    torch.cuda.synchronize()
+    assert torch.equal(stack.view(torch.int16), stack_ref.view(torch.int16))
+    assert torch.equal(prm.view(torch.int16), p_ref.view(torch.int16))
+    assert not torch.equal(prm.view(torch.int16), params0.view(torch.int16))
+
+
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (2048, 2048),
                                        (5632, 2048), (2048, 5632)])
 def test_muon_fused_step_at_config_shapes(L, rows, cols):

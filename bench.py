@@ -780,6 +780,22 @@ def measured_traffic():
     return None
 
 
+COUNTERS_FILE = os.path.join(ROOT, "profiles", "adamw8bit_2e28_counters.md")
+
+
+def measured_valu_issue():
+    """Fraction of the 8-bit kernel's time that its VALU instructions take to issue, from the
+    committed counter summary (SQ_INSTS_VALU per pair x 4 cycles / SIMDs / clock, against
+    the dispatch's duration in the same counter run), or None."""
+    try:
+        for line in open(COUNTERS_FILE):
+            if line.startswith("valu_issue_fraction:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -889,7 +905,12 @@ def main():
                      "bytes_per_launch": r8["bytes_per_step"],
                      # context, not the peak: the runtime's own device copy (half reads, half writes),
                      # measured in this run
-                     "device_copy_gbps_this_run": round(copy_gbps, 1)},
+                     "device_copy_gbps_this_run": round(copy_gbps, 1),
+                     # what binds the kernel below the HBM peak: the issue time of its VALU instructions
+                     "valu_issue_frac_of_kernel_time": measured_valu_issue(),
+                     "valu_issue_source": "profiles/adamw8bit_2e28_counters.md: rocprofv3 --pmc SQ_INSTS_VALU, "
+                                          "GRBM_GUI_ACTIVE runs of this kernel (committed counter run, not "
+                                          "measured in this run)"},
         "cpu_baseline": cpu,
         "configs": configs,
     }

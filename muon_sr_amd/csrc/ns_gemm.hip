@@ -1089,11 +1089,11 @@ struct PrologueArgs {
     int64_t ntx, ntiles;
 };
 
-// Tiles in runs of MSR_PRO_XCD consecutive tiles per XCD (a row of 32 tiles of a
-// 2048-column matrix): config 4's prologue 14 % faster than tiles in dispatch order
-// (1.27 -> 1.09 ms per step; runs of 8: 12 %), bit-exact.
+// Tiles in runs of MSR_PRO_XCD consecutive tiles per XCD (4 rows of 32 tiles of a
+// 2048-column matrix, 512 KiB of u): config 4's prologue 17 % faster than tiles in dispatch
+// order (1.27 -> 1.06 ms per step; runs of 8, 16, 32 and 64: 12-16 %), bit-exact.
 #ifndef MSR_PRO_XCD
-#define MSR_PRO_XCD 32
+#define MSR_PRO_XCD 128
 #endif
 template <int SRC, int MODE, bool NEST, bool G32, bool VEC>
 __global__ __launch_bounds__(256) void ns_prologue_kernel(PrologueArgs a) {

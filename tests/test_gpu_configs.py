@@ -122,6 +122,87 @@ def test_config1_hybrid_vs_oracle(L, noise, batch_ns, mode_name):
         assert opt._global_step == 10
 
 
+@pytest.mark.parametrize("mode_name", ["triton", "philox8"])
+def test_two_muon_groups_global_step_vs_oracle(L, noise, mode_name):
+    """Two batch_ns Muon groups with their own hyperparameters around an AdamW group.  The
+    reference advances the global step once per Muon group (muon_sr/triton_muon_sr.py:319-329),
+    so at step k the first group draws its seeds with global step 2k - 1 and the second with
+    2k; AdamW seeds use the group offset (:351-371).  After 3 steps the state goes through
+    state_dict() into a new optimizer, whose global step is restored as the largest per-param
+    step (:13-15), and 2 more steps continue the same sequence."""
+    from muon_sr_amd import TritonMuonSRWithAuxAdam
+    noise(mode_name)
+    mode = O.NOISE_TRITON if mode_name == "triton" else O.NOISE_PHILOX8
+    gen = torch.Generator().manual_seed(7)
+
+    def bf(shape, std):
+        return (torch.randn(shape, generator=gen) * std).to(torch.bfloat16)
+
+    def bits(t):
+        return t.view(torch.int16).numpy().view(np.uint16).copy()
+
+    sa = [(256, 256), (256, 512), (256, 256)]       # Muon group A
+    sb = [(256,), (128, 64)]                        # AdamW group
+    sc = [(256, 256), (512, 256)]                   # Muon group C
+    shapes = sa + sb + sc
+    p0 = [bf(x, 0.02) for x in shapes]
+    ps = [torch.nn.Parameter(x.to(DEV)) for x in p0]
+    hA = dict(lr=0.02, momentum=0.95, nesterov=True, weight_decay=0.01)
+    hC = dict(lr=0.01, momentum=0.9, nesterov=False, weight_decay=0.0)
+    alr, betas, eps, awd = 3e-4, (0.9, 0.95), 1e-10, 0.01
+
+    def make():
+        return TritonMuonSRWithAuxAdam([
+            dict(params=ps[0:3], use_muon=True, ns_steps=5, **hA),
+            dict(params=ps[3:5], use_muon=False, lr=alr, betas=betas, eps=eps, weight_decay=awd),
+            dict(params=ps[5:7], use_muon=True, ns_steps=5, **hC)], batch_ns=True)
+
+    opt = make()
+    P = [bits(x) for x in p0]
+    bufA = {sh: np.zeros((sa.count(sh), *sh), np.uint16) for sh in dict.fromkeys(sa)}
+    bufC = {sh: np.zeros((sc.count(sh), *sh), np.uint16) for sh in dict.fromkeys(sc)}
+    adam = {i: dict(e=np.zeros(int(np.prod(shapes[i])), np.uint16), s=np.zeros(int(np.prod(shapes[i])), np.uint16))
+            for i in (3, 4)}
+    b1, b2 = betas
+    for k in range(1, 6):
+        if k == 4:   # resume from a checkpoint of step 3
+            sd = opt.state_dict()
+            opt = make()
+            opt.load_state_dict(sd)
+        G = [bf(x, 1e-3) for x in shapes]
+        for p, g in zip(ps, G):
+            p.grad = g.to(DEV)
+        opt.step()
+        G = [bits(g) for g in G]
+        P[0:3], bufA = O.muon_batch_step(P[0:3], G[0:3], bufA, 2 * k - 1, hA["lr"], hA["weight_decay"],
+                                         hA["momentum"], hA["nesterov"], _gpu_ns, mode)
+        P[5:7], bufC = O.muon_batch_step(P[5:7], G[5:7], bufC, 2 * k, hC["lr"], hC["weight_decay"],
+                                         hC["momentum"], hC["nesterov"], _gpu_ns, mode)
+        bc, bcs = O.adamw_bias_corrections(b1, b2, k)
+        for i in (3, 4):
+            seed = O.deterministic_seed(k, i)
+            st = adam[i]
+            newp, st["e"], st["s"] = O.adamw_bf16(P[i].ravel(), G[i].ravel(), st["e"], st["s"], alr, b1, b2, eps, awd,
+                                                  bc, bcs, O.NoiseSpec(mode, seed, 0), O.NoiseSpec(mode, seed, 1),
+                                                  O.NoiseSpec(mode, seed, 2))
+            P[i] = newp.reshape(shapes[i])
+        for i, p in enumerate(ps):
+            assert np.array_equal(dev_to_u16(p.data).ravel(), P[i].ravel()), (k, i)
+        for j, (bufs, idx) in enumerate(((bufA, range(0, 3)), (bufC, range(5, 7)))):
+            seen = {}
+            for i in idx:
+                sh = shapes[i]
+                r = seen.get(sh, 0)
+                seen[sh] = r + 1
+                assert opt.state[ps[i]]["step"] == 2 * k - 1 + j, (k, i)
+                assert np.array_equal(dev_to_u16(opt.state[ps[i]]["momentum_buffer"]).ravel(),
+                                      np.asarray(bufs[sh][r]).ravel()), (k, i)
+        for i in (3, 4):
+            assert opt.state[ps[i]]["step"] == k
+            assert np.array_equal(dev_to_u16(opt.state[ps[i]]["ema"]).ravel(), adam[i]["e"]), (k, i)
+        assert opt._global_step == 2 * k
+
+
 # ---------------------------------------------------------------------------
 # Config 3
 # ---------------------------------------------------------------------------

@@ -203,6 +203,60 @@ def test_two_muon_groups_global_step_vs_oracle(L, noise, mode_name):
         assert opt._global_step == 2 * k
 
 
+@pytest.mark.parametrize("batch_ns", [True, False])
+@pytest.mark.parametrize("mode_name", ["triton", "philox8"])
+def test_muon_params_of_more_than_two_dims_vs_oracle(L, noise, batch_ns, mode_name):
+    """Muon parameters of 3 and 4 dimensions (stacks of matrices, conv-like weights) beside
+    2-D ones: the reference's Newton-Schulz treats the last two dimensions as the matrix and
+    the leading ones as a batch, normalizes each matrix on its own, transposes by the last two
+    dimensions (muon_sr/muon_sr.py:82-98) and scales by shape[-2] / shape[-1]
+    (muon_sr/triton_muon_sr.py:101-102).  TritonMuonSR, 3 steps, per parameter and batch_ns,
+    bit-exact against the oracle with this library's Newton-Schulz substituted."""
+    from muon_sr_amd import TritonMuonSR
+    noise(mode_name)
+    mode = O.NOISE_TRITON if mode_name == "triton" else O.NOISE_PHILOX8
+    gen = torch.Generator().manual_seed(11)
+
+    def bf(shape, std):
+        return (torch.randn(shape, generator=gen) * std).to(torch.bfloat16)
+
+    def bits(t):
+        return t.view(torch.int16).numpy().view(np.uint16).copy()
+
+    shapes = [(3, 64, 96), (2, 4, 48, 32), (3, 64, 96), (64, 96)]
+    p0 = [bf(x, 0.02) for x in shapes]
+    ps = [torch.nn.Parameter(x.to(DEV)) for x in p0]
+    lr, wd, beta = 0.02, 0.01, 0.95
+    opt = TritonMuonSR(ps, lr=lr, weight_decay=wd, momentum=beta, nesterov=True, batch_ns=batch_ns)
+    P = [bits(x) for x in p0]
+    if batch_ns:
+        bufs = {sh: np.zeros((shapes.count(sh), *sh), np.uint16) for sh in dict.fromkeys(shapes)}
+    else:
+        bufs = [np.zeros(sh, np.uint16) for sh in shapes]
+    for step in range(1, 4):
+        G = [bf(x, 1e-3) for x in shapes]
+        for p, g in zip(ps, G):
+            p.grad = g.to(DEV)
+        opt.step()
+        G = [bits(g) for g in G]
+        if batch_ns:
+            P, bufs = O.muon_batch_step(P, G, bufs, step, lr, wd, beta, True, _gpu_ns, mode)
+        else:
+            for j in range(len(shapes)):
+                P[j], bufs[j] = O.muon_param_step(P[j], G[j], bufs[j], step, j, lr, wd, beta, True, _gpu_ns, mode)
+        for i, p in enumerate(ps):
+            assert np.array_equal(dev_to_u16(p.data).ravel(), np.asarray(P[i]).ravel()), (step, i)
+        seen = {}
+        for i, p in enumerate(ps):
+            if batch_ns:
+                r = seen.get(shapes[i], 0)
+                seen[shapes[i]] = r + 1
+                exp = bufs[shapes[i]][r]
+            else:
+                exp = bufs[i]
+            assert np.array_equal(dev_to_u16(opt.state[p]["momentum_buffer"]).ravel(), np.asarray(exp).ravel()), (step, i)
+
+
 # ---------------------------------------------------------------------------
 # Config 3
 # ---------------------------------------------------------------------------

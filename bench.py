@@ -1,6 +1,7 @@
 """Benchmark of the muon_sr optimizer-step hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--configs adamw8bit,sr_accum,ns,centralize,full] [--noise philox8|triton]
+    python bench.py [--steps K] [--warmup W] [--configs adamw8bit,probe8,sr_accum,ns,centralize,wgrad,full]
+                    [--noise philox8|triton] [--no-cpu-baseline] [--copy-calibration]
 
 Prints ONE JSON line.  ``value`` is the headline workload (BASELINE.json
 configs[1]): one fused 8-bit blockwise AdamW step on a flat bf16 parameter of
